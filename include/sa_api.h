@@ -1,0 +1,88 @@
+/*
+ * sa_api.h -- C ABI of libsa_hip.so, the MI355X (gfx950) sparse-attention hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers, sizes and strides, and returns
+ * an int status (SA_OK or a negative SA_ERR_* code; sa_last_error() gives the message of
+ * the calling thread's last failure). Nothing here throws across the ABI.
+ *
+ * Conventions
+ *  - Tensors of shape [B, H, L, D] are passed as a device pointer plus three element
+ *    strides {stride_b, stride_h, stride_l}; the D axis must be contiguous (stride 1).
+ *    Element type is bf16 (uint16_t bit patterns) unless stated otherwise.
+ *  - Device buffers are owned by the caller (PyTorch's caching allocator in the Python
+ *    package). The library allocates no device memory.
+ *  - `stream` is a hipStream_t passed as void*; NULL means the default stream. All GPU
+ *    work is enqueued asynchronously on it; no entry point synchronises the device.
+ *  - Entry points documented as "host" run on the CPU only and touch no GPU state.
+ *  - Block-index lists ("kv lists") are int32 arrays kv_idx[rows][max_cnt] with per-row
+ *    counts kv_cnt[rows], rows = B*H*ceil(Lq/64), each list holding the key-block indices
+ *    to visit for one 64-row query block, ascending.
+ *
+ * Each declaration names the reference interface (file:line in
+ * xiaolong-li1/SparseAttnFunctions, package `special_attentions`) whose work it replaces.
+ */
+#ifndef SA_API_H
+#define SA_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_OK 0
+#define SA_ERR_INVALID (-1)     /* bad argument: null pointer, shape, stride, range */
+#define SA_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim != 64) */
+#define SA_ERR_HIP (-3)         /* a HIP runtime call failed (launch, device query) */
+
+#define SA_ABI_VERSION 1
+
+/* Version of this ABI (SA_ABI_VERSION). */
+int sa_abi_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). Never NULL. */
+const char* sa_last_error(void);
+
+/*
+ * Dense block mask -> kv lists.
+ * Replaces the per-program scan of the boolean block mask inside the Triton kernel
+ * (utils/block_sparse_attn_kernel.py:69-70, 163-199): the list is built once per call
+ * instead of each of the 278 x 60 programs loading every mask entry.
+ *   mask      uint8/bool, logical shape [B, H, nqb, nkb], element strides mask_strides[4]
+ *             (any strides, 0 for broadcast, as the reference accepts,
+ *             block_sparse_attn_kernel.py:125,141,155).
+ *   kv_idx    int32 [B*H*nqb][max_cnt], max_cnt >= nkb.  kv_cnt int32 [B*H*nqb].
+ */
+int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B, int H,
+                       int nqb, int nkb, int32_t* kv_idx, int max_cnt, int32_t* kv_cnt,
+                       void* stream);
+
+/*
+ * Block-sparse attention forward: out = softmax(q k^T * sm_scale [+ key_bias]) v restricted,
+ * for each 64-row query block, to the 64-key blocks in its kv list.
+ * Replaces `block_sparse_triton_fn` / `_forward` / `_fwd_kernel`
+ * (utils/block_sparse_attn_kernel.py:52-265, 293): same masking of the partial last key
+ * block (:87-89), fp32 online softmax, P rounded to bf16 before P.V (:107), no causal
+ * mask, query-block m uses mask row m (:155). A query block with an empty list writes 0
+ * (the reference divides by l=0 and writes NaN, :201-203).
+ *   q [B,H,Lq,64], k/v [B,H,Lk,64], out [B,H,Lq,64]: bf16, strides as above.
+ *   kv_idx/kv_cnt: lists for B*H*ceil(Lq/64) rows (row = (b*H + h)*nqb + m); entries
+ *             outside [0, ceil(Lk/64)) are skipped, counts are clamped to [0, max_cnt].
+ *   key_bias  nullable fp32, element [b*bias_strides[0] + h*bias_strides[1] + key]:
+ *             added to the scaled scores (proportional attention, MergeAttention.py:33-48).
+ *   sm_scale  > 0 and finite.
+ */
+int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                        const int64_t k_strides[3], const uint16_t* v,
+                        const int64_t v_strides[3], uint16_t* out,
+                        const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                        const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                        const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SA_API_H */

@@ -1,0 +1,12 @@
+"""CPU oracle of the sparse-attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the reference algorithms the HIP kernels implement, so
+that tests can check the GPU results. It is a checker, never a product path: only the
+tests under tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import it,
+and nothing in sparseattnfunctions_amd/ does.
+
+  attention.py  dense attention with the kron-expanded block mask, fp64 / fp32 (torch CPU)
+  sa_oracle.c   bit-exact integer/fp32 parts (block pooling, block scores, top-k lists,
+                local window, token-merge matching), built into liboracle.so by the
+                Makefile here and loaded through oracle/native.py
+"""

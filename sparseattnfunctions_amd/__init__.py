@@ -1,0 +1,28 @@
+"""MI355X-native (gfx950) sparse-attention hot path of special_attentions.
+
+Module layout mirrors the reference package `special_attentions`
+(xiaolong-li1/SparseAttnFunctions): the processor classes and utils keep their module and
+class names, and their forward passes run the HIP kernels of libsa_hip.so through the C ABI
+in include/sa_api.h. `install_alias()` registers this package under the name
+`special_attentions` so that code written against the reference imports it unchanged.
+"""
+from __future__ import annotations
+
+import importlib
+import sys
+
+__all__ = ["install_alias"]
+
+_SUBMODULES = (
+    "utils",
+    "utils.block_sparse_attn_kernel",
+)
+
+
+def install_alias(name: str = "special_attentions") -> None:
+    """Make `import special_attentions.<module>` resolve to this package's modules."""
+    pkg = sys.modules[__name__]
+    sys.modules.setdefault(name, pkg)
+    for sub in _SUBMODULES:
+        mod = importlib.import_module(f"{__name__}.{sub}")
+        sys.modules.setdefault(f"{name}.{sub}", mod)

@@ -1,0 +1,99 @@
+"""ctypes binding of libsa_hip.so (the C ABI declared in include/sa_api.h).
+
+PyTorch only provides device memory and the current HIP stream; every computation on the
+hot path is a HIP kernel of libsa_hip.so. There is no CPU or PyTorch fallback: if the
+library is missing, or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsa_hip.so")
+
+SA_OK = 0
+SA_ERR_INVALID = -1
+SA_ERR_UNSUPPORTED = -2
+SA_ERR_HIP = -3
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/sa_api.h.
+_PROTOTYPES = {
+    "sa_abi_version": (_I, []),
+    "sa_last_error": (ctypes.c_char_p, []),
+    "sa_mask_to_kv_list": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _P]),
+    "sa_block_sparse_fwd": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P],
+    ),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+class SAError(RuntimeError):
+    """A HIP runtime failure reported by libsa_hip.so."""
+
+
+def load() -> ctypes.CDLL:
+    """Loads libsa_hip.so once and declares the prototypes of every exported entry point."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `make -C sparseattnfunctions_amd/csrc` "
+                "(or __graft_entry__.build())"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _PROTOTYPES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def exported_names() -> Sequence[str]:
+    return tuple(_PROTOTYPES)
+
+
+def check(rc: int, what: str) -> None:
+    """Maps a C status to the exception the reference raises for the same condition."""
+    if rc == SA_OK:
+        return
+    msg = load().sa_last_error().decode(errors="replace") or what
+    if rc == SA_ERR_INVALID:
+        raise ValueError(msg)
+    if rc == SA_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise SAError(msg)
+
+
+def i64(*vals: int):
+    return (ctypes.c_int64 * len(vals))(*[int(x) for x in vals])
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of the tensor's device (hipStream_t as an integer)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError(
+                "special_attentions (MI355X build) runs on the GPU only; got a tensor on "
+                f"{t.device}. There is no CPU path."
+            )

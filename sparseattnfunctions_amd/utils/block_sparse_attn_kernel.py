@@ -1,0 +1,117 @@
+"""Block-sparse attention forward on MI355X (drop-in for the reference module of this name).
+
+Mirrors special_attentions/utils/block_sparse_attn_kernel.py of xiaolong-li1/SparseAttnFunctions:
+  * `block_sparse_triton_fn(q, k, v, block_sparse_mask, sm_scale)` (:293) -- same arguments,
+    same asserts (:226-231), output allocated like `torch.empty_like(q)` (:228), forward only
+    (backward raises NotImplementedError, :278-281);
+  * `sparse_attention_factory` (:283-291), `get_sparse_attn_mask_from_topk` (:31-39) and
+    `get_sparse_attn_mask_from_threshold` (:42-47).
+The name keeps "triton" for source compatibility; the work runs in the HIP kernels of
+libsa_hip.so (`sa_mask_to_kv_list` + `sa_block_sparse_fwd`), not Triton.
+
+Differences from the reference, by design:
+  * head_dim 64 only (the reference also accepts 128, :231) -> NotImplementedError;
+  * a query block whose mask row is empty yields 0 instead of NaN (:201-203);
+  * sm_scale must be > 0.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+from .._kv import KVList, kv_list_from_mask
+
+BLOCK = 64
+
+
+def _prep_qkv(t: torch.Tensor) -> torch.Tensor:
+    """bf16, last dim contiguous, 16-byte aligned rows (the kernel's vector loads)."""
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"expected bfloat16 tensors, got {t.dtype}")
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
+        t = t.contiguous()
+    return t
+
+
+def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None):
+    """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
+
+    q [B,H,Lq,64], k/v [B,H,Lk,64] bf16 on the GPU; key_bias optional fp32 [B,H,Lk] (any
+    strides with a contiguous key axis, stride 0 to broadcast).
+    """
+    _lib.require_gpu(q, k, v)
+    q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
+        raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if kv.rows != B * H * math.ceil(Lq / BLOCK):
+        raise ValueError(f"kv list has {kv.rows} rows, expected {B * H * math.ceil(Lq / BLOCK)}")
+    if out is None:
+        out = torch.empty_like(q)
+    bias_ptr, bias_strides = None, None
+    if key_bias is not None:
+        if key_bias.dtype != torch.float32 or key_bias.shape[-1] != Lk or key_bias.stride(-1) != 1:
+            raise ValueError("key_bias must be fp32 [B,H,Lk] with a contiguous key axis")
+        key_bias = key_bias.expand(B, H, Lk)
+        bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.sa_block_sparse_fwd(
+            q.data_ptr(), _lib.i64(*q.stride()[:3]),
+            k.data_ptr(), _lib.i64(*k.stride()[:3]),
+            v.data_ptr(), _lib.i64(*v.stride()[:3]),
+            out.data_ptr(), _lib.i64(*out.stride()[:3]),
+            B, H, Lq, Lk, D,
+            kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt,
+            bias_ptr, bias_strides, float(sm_scale),
+            _lib.stream_of(q),
+        )
+    _lib.check(rc, "sa_block_sparse_fwd")
+    return out
+
+
+def _forward(ctx, q, k, v, block_sparse_mask, sm_scale, BLOCK_M=64, BLOCK_N=64, num_warps=None,
+             num_stages=1, out=None):
+    """Reference host wrapper semantics (block_sparse_attn_kernel.py:211-265)."""
+    assert q.shape[-1] == k.shape[-1] == v.shape[-1]
+    assert k.shape[2] == v.shape[2]
+    assert q.shape[-1] in [64, 128]
+    if BLOCK_M != BLOCK or BLOCK_N != BLOCK:
+        raise NotImplementedError("the MI355X kernel uses 64x64 blocks")
+    B, H, Lq, _ = q.shape
+    kv = kv_list_from_mask(block_sparse_mask, B, H, math.ceil(Lq / BLOCK), math.ceil(k.shape[2] / BLOCK))
+    return block_sparse_attention(q, k, v, kv, sm_scale, out=out)
+
+
+class _sparse_attention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, block_sparse_dense, sm_scale):
+        return _forward(ctx, q, k, v, block_sparse_dense, sm_scale)
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError("It does not support gradient propagation yet")
+
+
+def sparse_attention_factory(BLOCK_M=64, BLOCK_N=64, **kwargs):
+    class _sparse_attention_config(_sparse_attention):
+        @staticmethod
+        def forward(ctx, q, k, v, block_sparse_dense, sm_scale):
+            return _forward(ctx, q, k, v, block_sparse_dense, sm_scale, BLOCK_M, BLOCK_N, **kwargs)
+
+    return _sparse_attention_config.apply
+
+
+block_sparse_triton_fn = _sparse_attention.apply
+
+
+def get_sparse_attn_mask_from_threshold(x, threshold, use_dense_for_last_block=False):
+    """Threshold block mask with lower-triangular restriction (reference :42-47)."""
+    dense_mask = x > threshold
+    if use_dense_for_last_block:
+        dense_mask[:, :, -2:, :] = True
+    dense_mask.tril_()
+    return dense_mask

@@ -1,0 +1,177 @@
+"""GPU parity of the block-sparse attention kernel against the CPU oracle (fp64).
+
+Tolerances: max-abs <= 2e-2 and mean-abs <= 2e-3 against the oracle
+computed from the same bf16 inputs; the reference's own check, allclose(atol=1e-2,
+rtol=1e-2) (block_sparse_attn_kernel.py:337), is asserted as well.
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import case
+from oracle.attention import masked_attention
+from sparseattnfunctions_amd._kv import KVList, kv_list_from_mask
+from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import (
+    block_sparse_attention, block_sparse_triton_fn, sparse_attention_factory)
+from sparseattnfunctions_amd.workloads import config1_inputs
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def _rand(shape, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype)
+
+
+def _check(got, want, atol_ref=True):
+    got = got.float().cpu().double()
+    err = (got - want).abs()
+    assert torch.isfinite(got).all()
+    assert err.max().item() <= MAX_ABS, err.max().item()
+    assert err.mean().item() <= MEAN_ABS, err.mean().item()
+    if atol_ref:
+        assert torch.allclose(got, want, atol=1e-2, rtol=1e-2)
+
+
+def test_config1_parity(dev):
+    case("config1 B=1 H=2 L=2048 random block mask (seed 1)")
+    q, k, v, mask, scale = config1_inputs()
+    qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    out = block_sparse_triton_fn(qb.to(dev), kb.to(dev), vb.to(dev), mask.to(dev), scale)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    _check(out, masked_attention(qb, kb, vb, mask, scale))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_reference_test_topk_partial_block(dev, seed):
+    # block_sparse_attn_kernel.py:296-339: B=1, H=3, L=257 (partial last block), all-ones mask.
+    case(f"L=257 all-ones seed={seed}")
+    q, k, v = (_rand((1, 3, 257, 64), seed * 3 + i) for i in range(3))
+    mask = torch.ones(1, 3, 5, 5, dtype=torch.bool)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 1 / 8)
+    _check(out, masked_attention(q, k, v, mask, 1 / 8))
+
+
+def test_reference_test_q_shorter_than_k(dev):
+    # block_sparse_attn_kernel.py:343-390: Lq=128 < Lk=256, top-1 mask with column 0 forced.
+    case("Lq=128 Lk=256 top-1")
+    q, k, v = _rand((2, 4, 128, 64), 10), _rand((2, 4, 256, 64), 11), _rand((2, 4, 256, 64), 12)
+    scores = _rand((2, 4, 4, 4), 13, torch.float32)
+    scores[..., 0] = 100
+    mask = torch.zeros(2, 4, 4, 4, dtype=torch.bool)
+    mask.scatter_(-1, scores.topk(1, dim=-1).indices, True)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 1 / 8)
+    _check(out, masked_attention(q, k, v, mask, 1 / 8))
+
+
+@pytest.mark.parametrize("L,density,seed", [(64, 1.0, 0), (130, 0.5, 1), (1000, 0.3, 2), (2048, 0.1, 3)])
+def test_random_masks(dev, L, density, seed):
+    case(f"random mask L={L} density={density}")
+    q, k, v = (_rand((2, 3, L, 64), 100 * seed + i) for i in range(3))
+    nb = math.ceil(L / 64)
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.rand(2, 3, nb, nb, generator=g) < density
+    mask[..., 0] = True
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125)
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_empty_rows_write_zero(dev):
+    case("empty rows")
+    q, k, v = (_rand((1, 2, 256, 64), 40 + i) for i in range(3))
+    mask = torch.ones(1, 2, 4, 4, dtype=torch.bool)
+    mask[0, 1, 2] = False
+    mask[0, 0] = False
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125).cpu()
+    assert torch.all(out[0, 0] == 0) and torch.all(out[0, 1, 128:192] == 0)
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_strided_and_broadcast(dev):
+    # q/k/v as views of a [B, L, H, D] buffer (non-contiguous heads) and a [1,1,n,n] mask.
+    case("strided BLHD views + broadcast mask")
+    B, L, H = 2, 300, 4
+    base = [_rand((B, L, H, 64), 50 + i) for i in range(3)]
+    q, k, v = (t.to(dev).permute(0, 2, 1, 3) for t in base)
+    nb = math.ceil(L / 64)
+    g = torch.Generator().manual_seed(5)
+    mask = torch.rand(1, 1, nb, nb, generator=g) < 0.5
+    mask[..., 0] = True
+    out = block_sparse_triton_fn(q, k, v, mask.to(dev), 0.125)
+    want = masked_attention(*(t.permute(0, 2, 1, 3) for t in base), mask, 0.125)
+    _check(out, want)
+
+
+def test_key_bias(dev):
+    case("key bias")
+    B, H, L = 2, 3, 700
+    q, k, v = (_rand((B, H, L, 64), 60 + i) for i in range(3))
+    g = torch.Generator().manual_seed(7)
+    bias = torch.log(torch.randint(1, 6, (B, 1, L), generator=g).float())
+    mask = torch.ones(1, 1, 11, 11, dtype=torch.bool)
+    kv = kv_list_from_mask(mask.to(dev), B, H, 11, 11)
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bias.to(dev))
+    _check(out, masked_attention(q, k, v, mask, 0.125, key_bias=bias.double()))
+
+
+def test_mask_to_kv_list_matches_nonzero(dev):
+    case("mask_to_kv_list")
+    g = torch.Generator().manual_seed(8)
+    mask = torch.rand(2, 3, 7, 150, generator=g) < 0.3
+    kv = kv_list_from_mask(mask.to(dev), 2, 3, 7, 150)
+    idx, cnt = kv.idx.cpu(), kv.cnt.cpu()
+    flat = mask.reshape(-1, 150)
+    for r in range(flat.shape[0]):
+        want = torch.nonzero(flat[r]).flatten().int()
+        assert cnt[r].item() == want.numel()
+        assert torch.equal(idx[r, : cnt[r]], want)
+    assert torch.equal(kv.to_mask().cpu(), mask)
+
+
+def test_invalid_list_entries_are_skipped(dev):
+    case("invalid kv entries")
+    q, k, v = (_rand((1, 1, 128, 64), 70 + i) for i in range(3))
+    idx = torch.tensor([[0, 99, -3], [1, 2, 0]], dtype=torch.int32)
+    cnt = torch.tensor([3, 1], dtype=torch.int32)
+    kv = KVList(idx.to(dev), cnt.to(dev), 1, 1, 2, 2)
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125)
+    mask = torch.tensor([[[[True, False], [False, True]]]])
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_factory_and_backward(dev):
+    case("factory + backward")
+    fn = sparse_attention_factory(64, 64)
+    q, k, v = (_rand((1, 1, 64, 64), 80 + i).to(dev) for i in range(3))
+    m = torch.ones(1, 1, 1, 1, dtype=torch.bool, device=dev)
+    out = fn(q, k, v, m, 0.125)
+    assert out.shape == q.shape
+    with pytest.raises(NotImplementedError):
+        sparse_attention_factory(128, 64)(q, k, v, m, 0.125)
+    qg = q.clone().requires_grad_(True)
+    o = block_sparse_triton_fn(qg, k, v, m, 0.125)
+    with pytest.raises(NotImplementedError):
+        o.float().sum().backward()
+
+
+def test_cogvideox_shape_subset_of_heads(dev):
+    # Full CogVideoX-2B shape (B=2, H=30, L=17776) with a random ~20% mask; the oracle checks
+    # 3 of the 60 heads (the kernel computes all of them).
+    case("CogVideoX shape random 20% mask")
+    B, H, L = 2, 30, 17776
+    nb = math.ceil(L / 64)
+    q, k, v = (_rand((B, H, L, 64), 90 + i) for i in range(3))
+    g = torch.Generator().manual_seed(9)
+    mask = torch.rand(B, H, nb, nb, generator=g) < 0.2
+    mask[:, :, :4, :] = True
+    mask[:, :, :, :4] = True
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125).cpu()
+    heads = [(0, 0), (1, 17), (1, 29)]
+    want = masked_attention(q, k, v, mask, 0.125, heads=heads)
+    for b, h in heads:
+        _check(out[b, h], want[b, h])
