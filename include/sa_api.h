@@ -81,6 +81,40 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         const float* key_bias, const int64_t bias_strides[2], float sm_scale,
                         void* stream);
 
+/*
+ * Block means of q and k: pooled[(b*H + h)*nb + blk][d] = mean over the block's tokens,
+ * nb = ceil(L/block), the last block averaging its L - (nb-1)*block tokens.
+ * Replaces the pooling half of the block-score estimator calc_attn_block_sum_efficient
+ * (utils/mask_related.py:40-81: replicate-pad, 8 random tokens per block, conv2d sum-pool)
+ * with the deterministic mean-pool of the top-k mask rule. Bit-exact contract: fp32 sum of
+ * the block's tokens in ascending order, then one IEEE division by the token count.
+ *   q, k      bf16 [B,H,L,64] (k may be NULL to pool q only); pooled outputs fp32
+ *             contiguous [B*H][nb][64].
+ */
+int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                  const int64_t k_strides[3], int B, int H, int L, int D, int block,
+                  float* q_pooled, float* k_pooled, void* stream);
+
+/*
+ * Per-row top-k block selection -> kv lists.
+ * Replaces get_sparse_attn_mask_from_topk (utils/block_sparse_attn_kernel.py:31-39:
+ * torch.topk + scatter) and the top-k/scatter of transfer_attn_to_mask with text rows and
+ * columns forced dense (SparseGen_Plus.py:28-50, 81-82); `local_bitmap` adds the static
+ * local-window part of the combined mask (union, as LocalGlobalAttention.py:227-237).
+ * For row r of head bh, the scores are score[c] = sum_d q_pooled[bh][r][d] *
+ * k_pooled[bh][c][d] (fmaf chain, d ascending) or scores_in[bh][r][c]; the kept set is the
+ * first `topk` columns in (score descending, column ascending) order, united with columns
+ * < n_text_blocks, all columns when r < n_text_blocks, and local_bitmap[r][c] != 0.
+ *   q_pooled [BH][nqb][D], k_pooled [BH][nkb][D] fp32 (D = 64), or scores_in fp32
+ *             [BH][nqb][nkb] (then the pooled inputs may be NULL). nkb <= 1024.
+ *   kv_idx    int32 [BH*nqb][max_cnt] (max_cnt >= nkb), kv_cnt int32 [BH*nqb].
+ *   mask_out  nullable uint8 [BH][nqb][nkb] (1 = kept); scores_out nullable fp32, same shape.
+ */
+int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const float* scores_in,
+                          int BH, int nqb, int nkb, int D, int topk, int n_text_blocks,
+                          const uint8_t* local_bitmap, int32_t* kv_idx, int max_cnt,
+                          int32_t* kv_cnt, uint8_t* mask_out, float* scores_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

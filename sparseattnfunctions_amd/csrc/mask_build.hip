@@ -1,0 +1,312 @@
+// Block-mask construction for gfx950: mean-pooled Q/K block scores, per-row top-k, union
+// with text rows/columns and an optional static local window, compaction to kv lists.
+//
+// Replaces the reference's mask builders that feed the block-sparse kernel:
+//   get_sparse_attn_mask_from_topk (utils/block_sparse_attn_kernel.py:31-39): torch.topk
+//     over block scores + scatter into a dense bool mask;
+//   transfer_attn_to_mask (SparseGen_Plus.py:12-84): sort/scatter per row, then text rows and
+//     columns forced dense (:81-82);
+//   calc_attn_block_sum_efficient (utils/mask_related.py:40-81): block scores, here from
+//     deterministic block means instead of 8 random samples per block.
+//
+// Bit-exactness contract (this translation unit is built with -ffp-contract=off):
+//   pooled[d] = (sum_{t in block, ascending} x[t][d]) / n_t      fp32 adds, IEEE division
+//   score     = fmaf chain over d = 0..D-1 ascending, starting from 0
+//   order     = score descending, then key-block index ascending (total order on fp32 bit
+//               patterns: -0 < +0, NaNs at the ends by sign)
+// The CPU oracle (oracle/sa_oracle.c) computes the same sequence of IEEE operations.
+#include "sa_common.h"
+
+namespace {
+
+constexpr int kPoolD = 64;        // head dim handled by the pooling kernel
+constexpr int kRowsPerWG = 16;    // score rows per top-k workgroup (4 per wave)
+constexpr int kColChunk = 64;     // key blocks staged in LDS per step
+constexpr int kKpStride = 65;     // LDS stride (floats) of a staged pooled-K row
+
+// ---------------------------------------------------------------------------------------
+// Pooling: wave = 8 blocks; lane = (block lane>>3, dims 8*(lane&7)..+7); each lane sums its
+// block's tokens sequentially with 16-byte loads. blockIdx.y selects the tensor (q or k).
+struct PoolArgs {
+  const uint16_t* x[2];
+  int64_t sb[2], sh[2], sl[2];
+  float* out[2];
+  int H, L, block, nb;
+  int64_t total_blocks;  // B*H*nb
+};
+
+__device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
+  const int t = blockIdx.y;
+  const int64_t gblk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+  if (gblk >= a.total_blocks) return;
+  const int dg = threadIdx.x & 7;
+  const int64_t bh = gblk / a.nb;
+  const int blk = (int)(gblk - bh * a.nb);
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int t0 = blk * a.block;
+  const int n = min(a.block, a.L - t0);
+  const uint16_t* p = a.x[t] + b * a.sb[t] + h * a.sh[t] + (int64_t)t0 * a.sl[t] + 8 * dg;
+  const int64_t sl = a.sl[t];
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int i = 0;
+  for (; i + 16 <= n; i += 16) {
+    uint4 w[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) w[u] = *reinterpret_cast<const uint4*>(p + (int64_t)(i + u) * sl);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      s[0] += bf16lo(w[u].x); s[1] += bf16hi(w[u].x);
+      s[2] += bf16lo(w[u].y); s[3] += bf16hi(w[u].y);
+      s[4] += bf16lo(w[u].z); s[5] += bf16hi(w[u].z);
+      s[6] += bf16lo(w[u].w); s[7] += bf16hi(w[u].w);
+    }
+  }
+  for (; i < n; ++i) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p + (int64_t)i * sl);
+    s[0] += bf16lo(w.x); s[1] += bf16hi(w.x);
+    s[2] += bf16lo(w.y); s[3] += bf16hi(w.y);
+    s[4] += bf16lo(w.z); s[5] += bf16hi(w.z);
+    s[6] += bf16lo(w.w); s[7] += bf16hi(w.w);
+  }
+  const float fn = (float)n;
+  float4* o = reinterpret_cast<float4*>(a.out[t] + gblk * kPoolD + 8 * dg);
+  o[0] = make_float4(s[0] / fn, s[1] / fn, s[2] / fn, s[3] / fn);
+  o[1] = make_float4(s[4] / fn, s[5] / fn, s[6] / fn, s[7] / fn);
+}
+
+// ---------------------------------------------------------------------------------------
+// Top-k: workgroup = 16 score rows of one (b, h); wave w sorts rows 4w..4w+3.
+struct TopkArgs {
+  const float* qp;         // [BH][nqb][D] (null when scores_in is given)
+  const float* kp;         // [BH][nkb][D]
+  const float* scores_in;  // [BH][nqb][nkb] or null
+  int nqb, nkb, D, topk, n_text;
+  const uint8_t* local;  // [nqb][nkb] or null
+  int32_t* kv_idx;
+  int max_cnt;
+  int32_t* kv_cnt;
+  uint8_t* mask_out;   // [BH][nqb][nkb] or null
+  float* scores_out;   // [BH][nqb][nkb] or null
+  int row_groups;      // ceil(nqb / kRowsPerWG)
+};
+
+__device__ inline uint32_t order_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Ascending 64-bit key: (score descending, index ascending).
+__device__ inline uint64_t sort_key(float score, int idx) {
+  return ((uint64_t)(~order_bits(score)) << 32) | (uint32_t)idx;
+}
+
+__device__ inline uint64_t shfl_xor_u64(uint64_t x, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)x, m);
+  const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort (ascending) of 64*NPL keys held as element i = lane*NPL + e.
+template <int NPL>
+__device__ inline void wave_bitonic_sort(uint64_t (&x)[NPL], int lane) {
+  constexpr int N = 64 * NPL;
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= NPL) {
+        const int m = j / NPL;
+        const bool lower = (lane & m) == 0;
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+          const int i = lane * NPL + e;
+          const bool asc = (i & k) == 0;
+          const uint64_t o = shfl_xor_u64(x[e], m);
+          const bool take_min = (lower == asc);
+          x[e] = take_min ? (o < x[e] ? o : x[e]) : (o > x[e] ? o : x[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < NPL; ++e) {
+          const int p = e ^ j;
+          if (p > e) {
+            const int i = lane * NPL + e;
+            const bool asc = (i & k) == 0;
+            const uint64_t lo = x[e] < x[p] ? x[e] : x[p];
+            const uint64_t hi = x[e] < x[p] ? x[p] : x[e];
+            x[e] = asc ? lo : hi;
+            x[p] = asc ? hi : lo;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int NPL>
+__global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
+  constexpr int NPAD = 64 * NPL;
+  __shared__ float s_lds[kRowsPerWG][NPAD];
+  __shared__ float q_lds[kRowsPerWG][kPoolD];
+  __shared__ float k_lds[kColChunk * kKpStride];
+  __shared__ uint32_t bits[kRowsPerWG][NPAD / 32];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int bh = blockIdx.x / a.row_groups;
+  const int r0 = (blockIdx.x - bh * a.row_groups) * kRowsPerWG;
+  const int64_t row_base = (int64_t)bh * a.nqb;
+
+  if (a.scores_in) {
+    for (int e = tid; e < kRowsPerWG * a.nkb; e += 256) {
+      const int rr = e / a.nkb, c = e - rr * a.nkb;
+      if (r0 + rr < a.nqb) s_lds[rr][c] = a.scores_in[(row_base + r0 + rr) * a.nkb + c];
+    }
+  } else {
+    const int D = a.D;
+    for (int e = tid; e < kRowsPerWG * D; e += 256) {
+      const int rr = e / D, d = e - rr * D;
+      q_lds[rr][d] = (r0 + rr < a.nqb) ? a.qp[(row_base + r0 + rr) * D + d] : 0.f;
+    }
+    const float* kpb = a.kp + (int64_t)bh * a.nkb * D;
+    for (int c0 = 0; c0 < a.nkb; c0 += kColChunk) {
+      __syncthreads();
+      const int nc = min(kColChunk, a.nkb - c0);
+      for (int e = tid; e < nc * D; e += 256) {
+        const int c = e / D, d = e - c * D;
+        k_lds[c * kKpStride + d] = kpb[(int64_t)(c0 + c) * D + d];
+      }
+      __syncthreads();
+      const int c = tid & 63;
+      const int rg = (tid >> 6) * 4;
+      if (c < nc) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < D; ++d) {
+          const float kv = k_lds[c * kKpStride + d];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc[u] = fmaf(q_lds[rg + u][d], kv, acc[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) s_lds[rg + u][c0 + c] = acc[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  const int words = (a.nkb + 31) >> 5;
+  for (int u = 0; u < 4; ++u) {
+    const int rr = wave * 4 + u;
+    const int r = r0 + rr;
+    if (r >= a.nqb) break;  // wave-uniform
+    const int64_t row = row_base + r;
+    uint64_t key[NPL];
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+      const int i = lane * NPL + e;
+      key[e] = i < a.nkb ? sort_key(s_lds[rr][i], i) : ~0ull;
+    }
+    if (a.scores_out) {
+      for (int c = lane; c < a.nkb; c += 64) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
+    }
+    wave_bitonic_sort<NPL>(key, lane);
+    for (int w = lane; w < words; w += 64) bits[rr][w] = 0u;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+#pragma unroll
+    for (int e = 0; e < NPL; ++e) {
+      const int i = lane * NPL + e;
+      if (i < a.topk && i < a.nkb) {
+        const int c = (int)(uint32_t)key[e];
+        atomicOr(&bits[rr][c >> 5], 1u << (c & 31));
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    // Union with text rows/columns and the local window, then ballot-compact in order.
+    const bool text_row = r < a.n_text;
+    const uint8_t* loc = a.local ? a.local + (int64_t)r * a.nkb : nullptr;
+    int32_t* out = a.kv_idx + row * a.max_cnt;
+    int total = 0;
+    for (int c0 = 0; c0 < a.nkb; c0 += 64) {
+      const int c = c0 + lane;
+      bool on = false;
+      if (c < a.nkb) {
+        on = text_row || c < a.n_text || ((bits[rr][c >> 5] >> (c & 31)) & 1u);
+        if (loc) on = on || loc[c] != 0;
+        if (a.mask_out) a.mask_out[row * a.nkb + c] = on ? 1 : 0;
+      }
+      const uint64_t bal = __ballot(on);
+      const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+      if (on && total + pre < a.max_cnt) out[total + pre] = c;
+      total += __popcll(bal);
+    }
+    if (lane == 0) a.kv_cnt[row] = total < a.max_cnt ? total : a.max_cnt;
+  }
+}
+
+}  // namespace
+
+extern "C" int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                             const int64_t k_strides[3], int B, int H, int L, int D, int block,
+                             float* q_pooled, float* k_pooled, void* stream) {
+  SA_REQUIRE(q && q_strides && q_pooled, "sa_block_pool: null pointer");
+  SA_REQUIRE(!k || (k_strides && k_pooled), "sa_block_pool: k given without k_strides/k_pooled");
+  SA_REQUIRE(B > 0 && H > 0 && L > 0 && block > 0, "sa_block_pool: bad shape B=%d H=%d L=%d block=%d", B, H, L, block);
+  if (D != kPoolD) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_pool: head_dim %d (only 64)", D);
+  const uint16_t* xs[2] = {q, k};
+  const int64_t* ss[2] = {q_strides, k_strides};
+  for (int t = 0; t < 2; ++t) {
+    if (!xs[t]) continue;
+    if (reinterpret_cast<uintptr_t>(xs[t]) % 16)
+      return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_pool: tensor base not 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if (ss[t][i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_pool: strides must be multiples of 8");
+  }
+  PoolArgs a;
+  a.H = H; a.L = L; a.block = block; a.nb = sa::cdiv(L, block);
+  a.total_blocks = (int64_t)B * H * a.nb;
+  const int nt = k ? 2 : 1;
+  for (int t = 0; t < 2; ++t) {
+    const int s = t < nt ? t : 0;
+    a.x[t] = xs[s]; a.sb[t] = ss[s][0]; a.sh[t] = ss[s][1]; a.sl[t] = ss[s][2];
+    a.out[t] = s == 0 ? q_pooled : k_pooled;
+  }
+  const int64_t grid = (a.total_blocks * 8 + 255) / 256;
+  SA_REQUIRE(grid < (1LL << 31), "sa_block_pool: grid too large");
+  hipLaunchKernelGGL(pool_kernel, dim3((unsigned)grid, nt), dim3(256), 0, sa::as_stream(stream), a);
+  return sa::check_launch("sa_block_pool");
+}
+
+extern "C" int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const float* scores_in,
+                                     int BH, int nqb, int nkb, int D, int topk, int n_text_blocks,
+                                     const uint8_t* local_bitmap, int32_t* kv_idx, int max_cnt,
+                                     int32_t* kv_cnt, uint8_t* mask_out, float* scores_out, void* stream) {
+  SA_REQUIRE(kv_idx && kv_cnt, "sa_block_topk_kv_list: null kv list");
+  SA_REQUIRE(scores_in || (q_pooled && k_pooled), "sa_block_topk_kv_list: need scores_in or q/k pooled");
+  SA_REQUIRE(BH > 0 && nqb > 0 && nkb > 0, "sa_block_topk_kv_list: bad shape BH=%d nqb=%d nkb=%d", BH, nqb, nkb);
+  SA_REQUIRE(topk >= 0 && n_text_blocks >= 0, "sa_block_topk_kv_list: negative topk/n_text_blocks");
+  SA_REQUIRE(max_cnt >= nkb, "sa_block_topk_kv_list: max_cnt=%d < nkb=%d", max_cnt, nkb);
+  if (!scores_in && D != kPoolD) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_topk_kv_list: D=%d (only 64)", D);
+  if (nkb > 1024) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_topk_kv_list: nkb=%d > 1024", nkb);
+  TopkArgs a;
+  a.qp = q_pooled; a.kp = k_pooled; a.scores_in = scores_in;
+  a.nqb = nqb; a.nkb = nkb; a.D = D; a.topk = topk; a.n_text = n_text_blocks;
+  a.local = local_bitmap; a.kv_idx = kv_idx; a.max_cnt = max_cnt; a.kv_cnt = kv_cnt;
+  a.mask_out = mask_out; a.scores_out = scores_out;
+  a.row_groups = sa::cdiv(nqb, kRowsPerWG);
+  const int64_t grid = (int64_t)BH * a.row_groups;
+  SA_REQUIRE(grid < (1LL << 31), "sa_block_topk_kv_list: grid too large");
+  hipStream_t s = sa::as_stream(stream);
+  if (nkb <= 256) {
+    hipLaunchKernelGGL(topk_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  } else if (nkb <= 512) {
+    hipLaunchKernelGGL(topk_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(topk_kernel<16>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  }
+  return sa::check_launch("sa_block_topk_kv_list");
+}
