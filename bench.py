@@ -1,0 +1,205 @@
+"""Benchmark of the sparse-attention hot path on one MI355X.
+
+Workload ("C2"): one CogVideoX-2B attention layer, B=2, H=30,
+L=17776 (226 text + 13x30x45 video), d=64, bf16, synthetic q/k/v (seed 0). One step is one
+call of the block_mask_attn processor: mean-pool block scores + top-55/278 kv lists + text
+rows/columns (mask kernels), then block-sparse attention. Inputs are resident in HBM
+before timing.
+
+Prints ONE JSON line: value = effective TFLOP/s over the whole step (FLOPs of computed
+tiles only: 4*d*valid pairs), plus the attention kernel's roofline (HIP events around its
+launches in the timed steps) and a CPU baseline (the oracle's dense-masked fp32 attention,
+the reference's own correctness recipe, on a bounded sample of heads).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (AMD datasheet)
+HBM_PEAK_GBS = 8000.0
+METRIC = "ms/call + effective TFLOP/s (% MFMA peak), CogVideoX-2B attn B=2 H=30 L=17776"
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_fn(fn, iters=10, warmup=2):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def load_traffic():
+    """HBM bytes per attention launch measured with rocprofv3 --pmc (profiles/)."""
+    path = os.path.join(ROOT, "profiles", "attn_c2_pmc_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=4):
+    """Times the oracle's dense-masked fp32 attention (kron mask -> masked_fill -> softmax ->
+    matmul, block_sparse_attn_kernel.py:326-334) on `n_heads_sample` (b, h) heads on the host
+    and scales to the full call."""
+    from oracle.attention import masked_attention
+
+    threads = torch.get_num_threads()
+    mask = kv.to_mask().cpu()
+    B, H = q.shape[:2]
+    heads = [(i % B, (7 * i) % H) for i in range(n_heads_sample)]
+    qc, kc, vc = (t.cpu() for t in (q, k, v))
+    t0 = time.perf_counter()
+    masked_attention(qc, kc, vc, mask, sm_scale, dtype=torch.float32, heads=heads, row_chunk=1024)
+    dt = time.perf_counter() - t0
+    scale = (B * H) / len(heads)
+    ms_full = dt * 1e3 * scale
+    return {
+        "value": round(eff_flops_total / (ms_full * 1e-3) / 1e12, 6),
+        "unit": "TFLOP/s",
+        "ms_per_call": round(ms_full, 1),
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(heads)} of {B * H} (b,h) heads of the C2 call, fp32 dense-masked, "
+                  f"{dt:.1f} s, scaled x{scale:.0f}",
+        "cpu": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the dense comparators")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (the hot path is single-GPU; see "
+              "DESIGN.md for how it would shard); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention
+    from sparseattnfunctions_amd.workloads import COGVIDEOX_2B, cogvideox_qkv
+
+    dev = torch.device("cuda:0")
+    geom = COGVIDEOX_2B
+    qc, kc, vc = cogvideox_qkv(0)
+    q, k, v = qc.to(dev), kc.to(dev), vc.to(dev)
+    del qc, kc, vc
+    proc = BlockSparseAttention(64, keep_ratio=0.2, geometry=geom)
+    B, H, L, D = q.shape
+
+    # Attention launches are bracketed by events on the same (current) stream.
+    attn_ms = []
+
+    def step(record):
+        kv = proc.build_kv_list(q, k)
+        if record:
+            e0, e1 = _events()
+            e0.record()
+        out = block_sparse_attention(q, k, v, kv, proc.sm_scale, n_text_blocks=geom.n_text_blocks)
+        if record:
+            e1.record()
+            attn_ms.append((e0, e1))
+        return kv, out
+
+    for _ in range(args.warmup):
+        kv, _ = step(False)
+    torch.cuda.synchronize()
+    pairs = kv.computed_pairs(L, L)
+    eff_flops = 4 * D * pairs
+    density = kv.cnt.sum().item() / (kv.rows * kv.nkb)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g0, g1 = _events()
+    g0.record()
+    for _ in range(args.steps):
+        step(True)
+    g1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = g0.elapsed_time(g1) / args.steps
+    attn_kernel_ms = sum(a.elapsed_time(b) for a, b in attn_ms) / len(attn_ms)
+
+    result = {
+        "metric": METRIC,
+        "value": round(eff_flops / (ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: CogVideoX-2B attention, mean-pool top-k block mask (55/278 + text) + block-sparse attention",
+            "B": B, "H": H, "L": L, "d": D, "block": 64, "topk": 55, "text_blocks": geom.n_text_blocks,
+            "block_density": round(density, 4), "effective_tflop_per_call": round(eff_flops / 1e12, 4),
+        },
+        "roofline": {
+            "kernel": "bsa_fwd_kernel",
+            "bound": "mfma",
+            "achieved": round(eff_flops / (attn_kernel_ms * 1e-3) / 1e12, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(eff_flops / (attn_kernel_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": load_traffic(),
+            "kernel_ms": round(attn_kernel_ms, 4),
+        },
+        "mask_ms": round(ms - attn_kernel_ms, 4),
+        "wall_ms_per_step": round(wall_ms, 4),
+    }
+
+    if not args.no_extra:
+        dense_sdpa_ms = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v), iters=5)
+        dense_hip_ms = time_fn(lambda: proc.forward_dense(q, k, v), iters=3)
+        result["dense"] = {
+            "torch_sdpa_ms": round(dense_sdpa_ms, 3),
+            "hip_all_blocks_ms": round(dense_hip_ms, 3),
+            "speedup_vs_torch_sdpa": round(dense_sdpa_ms / ms, 3),
+            "speedup_vs_hip_dense": round(dense_hip_ms / ms, 3),
+        }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(q, k, v, kv, proc.sm_scale, eff_flops)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

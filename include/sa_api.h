@@ -72,6 +72,8 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
  *   key_bias  nullable fp32, element [b*bias_strides[0] + h*bias_strides[1] + key]:
  *             added to the scaled scores (proportional attention, MergeAttention.py:33-48).
  *   sm_scale  > 0 and finite.
+ *   work_order nullable int32 [n_slots] from sa_attn_work_order (device copy): dispatch
+ *             slot -> list row, -1 = idle. NULL visits rows in index order.
  */
 int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                         const int64_t k_strides[3], const uint16_t* v,
@@ -79,7 +81,18 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
                         const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
                         const float* key_bias, const int64_t bias_strides[2], float sm_scale,
-                        void* stream);
+                        const int32_t* work_order, int64_t n_slots, void* stream);
+
+/*
+ * (host) Dispatch order of the attention work items (one per list row) for a GPU whose
+ * workgroups are dealt round-robin to n_xcd XCDs (8 on MI355X): each XCD gets a
+ * contiguous range of (b, h) heads, so their K/V stay in that XCD's L2, and within it the
+ * text block rows (longest lists) come first. No counterpart in the reference, whose grid
+ * is (ceil(Lq/64), B*H) in launch order (block_sparse_attn_kernel.py:229).
+ *   order     NULL to query *n_slots only; else int32 [*n_slots] filled on the host.
+ */
+int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int n_xcd, int32_t* order,
+                       int64_t* n_slots);
 
 /*
  * Block means of q and k: pooled[(b*H + h)*nb + blk][d] = mean over the block's tokens,

@@ -34,8 +34,10 @@ _PROTOTYPES = {
     "sa_block_topk_kv_list": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P]),
     "sa_block_sparse_fwd": (
         _I,
-        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P],
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,
+         ctypes.c_int64, _P],
     ),
+    "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -8,26 +8,43 @@
 // from a compacted per-row list (kv_idx/kv_cnt) instead of a scan of the dense mask; the
 // softmax runs in the exp2 domain with log2(e) folded into the scale; an empty row writes 0.
 //
-// Work decomposition: one workgroup of two wave64s per (b, h, 64-row query block). Each
-// wave owns 32 query rows and computes S^T = K Q^T and O^T = V^T P^T with
-// v_mfma_f32_32x32x16_bf16, so every lane holds one query column of S^T and the row max
-// needs a single cross-half exchange. K (row-major) and V (transposed) tiles of 64 keys are
-// staged through double-buffered LDS; the global loads of tile i+1 are in flight while
-// tile i is computed.
+// Work decomposition. One wave64 owns one (b, h, 64-row query block) work item; a
+// workgroup holds 4 independent waves (no workgroup barriers). Per 64-key tile a wave
+// computes S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 (2 query groups of
+// 32 rows x 2 key chunks x 4 d-steps, then 2 d-chunks x 2 query groups x 4 key-steps:
+// 32 MFMAs = 1 MFLOP). Each lane holds one query column of S^T, so row statistics need
+// one cross-half exchange. K is loaded from global memory straight into MFMA A-operand
+// registers; V is loaded coalesced and written transposed into a wave-private LDS tile,
+// read back as V^T A-operands. The loads of tile i+1 are issued while tile i is computed.
+//
+// Softmax economy (VALU is the co-bottleneck at d = 64): the running max is only raised
+// when a tile exceeds it by more than kRescaleLog2 (then p <= 2^kRescaleLog2), so the
+// accumulator rescale is rare; row sums accumulate the bf16-rounded P pairs with
+// v_dot2c_f32_bf16; maxima use v_max3_f32.
+//
+// Scheduling: a host-built work order maps dispatch slots to items so that each XCD
+// (workgroups round-robin over 8 XCDs) processes a contiguous range of heads, longest
+// (text) rows first.
 #include <math.h>
 
+#include <algorithm>
 #include <cmath>
+#include <vector>
 
 #include "sa_common.h"
 
 namespace {
 
-constexpr int kBlock = 64;     // query rows per block == keys per key block
-constexpr int kHeadDim = 64;   // head dimension handled by this kernel
-constexpr int kThreads = 128;  // two wave64s
-constexpr int kRowPad = 72;    // LDS row stride in bf16 elements (K rows, V^T rows)
-constexpr int kTileElems = kBlock * kRowPad;
+constexpr int kBlock = 64;       // query rows per block == keys per key block
+constexpr int kHeadDim = 64;     // head dimension handled by this kernel
+constexpr int kWaves = 4;        // independent waves per workgroup
+constexpr int kVtStride = 68;    // LDS row stride (bf16) of the V^T tile: 32 rows hit 64 banks once
+constexpr int kVtElems = kHeadDim * kVtStride;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleLog2 = 8.0f;
+#ifndef SA_ATTN_MIN_WAVES
+#define SA_ATTN_MIN_WAVES 2
+#endif
 
 struct FwdArgs {
   const uint16_t* q;
@@ -38,7 +55,10 @@ struct FwdArgs {
   int64_t k_sb, k_sh, k_sl;
   int64_t v_sb, v_sh, v_sl;
   int64_t o_sb, o_sh, o_sl;
-  int H, Lq, Lk, nqb, nkb, BH;
+  int H, Lq, Lk, nqb, nkb;
+  int n_items;             // B*H*nqb
+  const int32_t* order;    // dispatch slot -> item (bh*nqb + qb), -1 = idle; may be null
+  int n_slots;
   const int32_t* kv_idx;
   const int32_t* kv_cnt;
   int max_cnt;
@@ -47,7 +67,7 @@ struct FwdArgs {
   float scale_log2;  // sm_scale * log2(e)
 };
 
-__device__ inline sa_bf16x8 as_bf16x8(sa_u16x8 x) { return __builtin_bit_cast(sa_bf16x8, x); }
+__device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
 
 __device__ inline sa_f32x16 mfma32(sa_bf16x8 a, sa_bf16x8 b, sa_f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -55,108 +75,157 @@ __device__ inline sa_f32x16 mfma32(sa_bf16x8 a, sa_bf16x8 b, sa_f32x16 c) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Per-thread staging registers of one K/V tile between the global load and the LDS store.
-struct TileRegs {
-  uint4 k[4];
-  uint4 v[4];
-  float bias;
-};
-
-// Global -> registers for key block kb (zero-filled past Lk or for an invalid kb).
-template <bool kBias>
-__device__ inline void load_tile(const FwdArgs& a, const uint16_t* kbase, const uint16_t* vbase,
-                                 const float* bbase, int kb, int tid, TileRegs& r) {
-  const bool kb_ok = (unsigned)kb < (unsigned)a.nkb;
-  const int key0 = kb * kBlock;
-  // K: 512 16-byte chunks, thread t takes keys (t>>3)+16i, dims 8*(t&7)..+7.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = (tid >> 3) + 16 * i;
-    const int kg = key0 + key;
-    if (kb_ok && kg < a.Lk) {
-      r.k[i] = *reinterpret_cast<const uint4*>(kbase + (int64_t)kg * a.k_sl + 8 * (tid & 7));
-    } else {
-      r.k[i] = make_uint4(0, 0, 0, 0);
-    }
-  }
-  // V: thread t takes keys 4*(t&15)..+3, dims 8*(t>>4)..+7, to be written transposed.
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int kg = key0 + 4 * (tid & 15) + e;
-    if (kb_ok && kg < a.Lk) {
-      r.v[e] = *reinterpret_cast<const uint4*>(vbase + (int64_t)kg * a.v_sl + 8 * (tid >> 4));
-    } else {
-      r.v[e] = make_uint4(0, 0, 0, 0);
-    }
-  }
-  if (kBias) {
-    r.bias = 0.f;
-    if (tid < kBlock) {
-      const int kg = key0 + tid;
-      r.bias = (kb_ok && kg < a.Lk) ? bbase[kg] * kLog2e : 0.f;
-    }
-  }
-}
-
 __device__ inline uint32_t word(const uint4& x, int j) {
   return j == 0 ? x.x : (j == 1 ? x.y : (j == 2 ? x.z : x.w));
 }
 
-// Byte select: {lo16(a), lo16(b)} for kHi = false, {hi16(a), hi16(b)} for kHi = true.
+// Byte select: {lo16(a), lo16(b)} (kHi = false) or {hi16(a), hi16(b)} (kHi = true).
 template <bool kHi>
 __device__ inline uint32_t pack_halves(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, kHi ? 0x07060302u : 0x05040100u);
 }
 
-template <bool kBias>
-__device__ inline void store_tile(uint16_t* k_lds, uint16_t* vt_lds, float* b_lds, int tid,
-                                  const TileRegs& r) {
+typedef __bf16 sa_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> packed bf16 pair (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ inline uint32_t cvt_pk_bf16(float a, float b) {
+  sa_bf16x2 r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ inline float dot2_bf16_ones(uint32_t pair, float acc) {
+  const sa_bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(sa_bf16x2, pair), ones, acc, false);
+}
+
+// All loads below are unconditional with row indices clamped into [0, L): a per-lane
+// condition would become an exec-masked branch, and the compiler then cannot count the
+// loads in flight and waits for all of them (s_waitcnt vmcnt(0)) before any use. Rows
+// clamped past Lk belong to keys whose scores are masked to -inf (their V rows meet p = 0;
+// clamped data is finite), and clamped Q rows past Lq are never stored.
+
+// K tile as MFMA A operands: kr[c][s] = K[key0 + 32c + col][16s + 8hh .. +7].
+__device__ inline void load_k(const FwdArgs& a, const uint16_t* kbase, int key0, int col, int hh,
+                              uint4 (&kr)[2][4]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = (tid >> 3) + 16 * i;
-    *reinterpret_cast<uint4*>(k_lds + key * kRowPad + 8 * (tid & 7)) = r.k[i];
-  }
-  // V^T: row d8+x gets keys key4..key4+3 (one 8-byte store per d).
-  const int key4 = 4 * (tid & 15);
-  const int d8 = 8 * (tid >> 4);
+  for (int c = 0; c < 2; ++c) {
+    const int key = min(key0 + 32 * c + col, a.Lk - 1);
+    const uint16_t* p = kbase + (int64_t)key * a.k_sl + 8 * hh;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t w0 = word(r.v[0], j), w1 = word(r.v[1], j);
-    const uint32_t w2 = word(r.v[2], j), w3 = word(r.v[3], j);
-    *reinterpret_cast<uint2*>(vt_lds + (d8 + 2 * j) * kRowPad + key4) =
-        make_uint2(pack_halves<false>(w0, w1), pack_halves<false>(w2, w3));
-    *reinterpret_cast<uint2*>(vt_lds + (d8 + 2 * j + 1) * kRowPad + key4) =
-        make_uint2(pack_halves<true>(w0, w1), pack_halves<true>(w2, w3));
-  }
-  if (kBias) {
-    if (tid < kBlock) b_lds[tid] = r.bias;
+    for (int s = 0; s < 4; ++s) kr[c][s] = *reinterpret_cast<const uint4*>(p + 16 * s);
   }
 }
 
+// V tile rows for the transposed LDS write: vr[p][e] = V[key0 + 4kq + e][8(dg + 4p) .. +7].
+__device__ inline void load_v(const FwdArgs& a, const uint16_t* vbase, int key0, int lane,
+                              uint4 (&vr)[2][4]) {
+  const int kq = lane & 15, dg = lane >> 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int key = min(key0 + 4 * kq + e, a.Lk - 1);
+    const uint16_t* p = vbase + (int64_t)key * a.v_sl + 8 * dg;
+#pragma unroll
+    for (int p2 = 0; p2 < 2; ++p2) vr[p2][e] = *reinterpret_cast<const uint4*>(p + 32 * p2);
+  }
+}
+
+__device__ inline void store_vt(uint16_t* vt, int lane, const uint4 (&vr)[2][4]) {
+  const int kq = lane & 15, dg = lane >> 4;
+#pragma unroll
+  for (int p2 = 0; p2 < 2; ++p2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w0 = word(vr[p2][0], j), w1 = word(vr[p2][1], j);
+      const uint32_t w2 = word(vr[p2][2], j), w3 = word(vr[p2][3], j);
+      const int d = 8 * (dg + 4 * p2) + 2 * j;
+      *reinterpret_cast<uint2*>(vt + d * kVtStride + 4 * kq) =
+          make_uint2(pack_halves<false>(w0, w1), pack_halves<false>(w2, w3));
+      *reinterpret_cast<uint2*>(vt + (d + 1) * kVtStride + 4 * kq) =
+          make_uint2(pack_halves<true>(w0, w1), pack_halves<true>(w2, w3));
+    }
+  }
+}
+
+// V^T A operand for d-chunk dc, key step (c, u): V^T[32dc + col][32c + 16u + 4hh + {0..3, 8..11}].
+__device__ inline sa_bf16x8 read_vt(const uint16_t* vt, int dc, int c, int u, int col, int hh) {
+  const uint16_t* r = vt + (32 * dc + col) * kVtStride + 32 * c + 16 * u + 4 * hh;
+  const uint2 lo = *reinterpret_cast<const uint2*>(r);
+  const uint2 hi = *reinterpret_cast<const uint2*>(r + 8);
+  return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// Softmax of one query group's 16 S^T values of a 32-key half (element i -> key
+// 8(i/4) + 4hh + (i%4) of the half) into 8 packed bf16 P pairs; updates the running max m
+// (log2 domain, scaled) and the lane-partial row sum l. Returns true (wave-uniform) when
+// the running max was raised; then *alpha is the factor for the accumulator.
 template <bool kBias>
-__global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kTileElems];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][kTileElems];
-  __shared__ float b_lds[2][kBlock];
+__device__ inline bool softmax16(sa_f32x16& s, const float (&bl)[16], float scale_log2, float& m, float& l,
+                                 uint32_t (&pk)[8], float& alpha) {
+  if (kBias) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = fmaf(s[i], scale_log2, bl[i]);
+  }
+  float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+  for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
+  mx = fmaxf(mx, s[15]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float cand = kBias ? mx : mx * scale_log2;  // scale_log2 > 0
+  // Raise the running max only when this half-tile exceeds it by more than the threshold
+  // (always on the first one, where m = -inf).
+  const bool raise = __ballot(cand > m + kRescaleLog2) != 0;
+  if (raise) {
+    const float m_new = fmaxf(m, cand);
+    alpha = fast_exp2(m - m_new);  // 0 when m = -inf
+    l *= alpha;
+    m = m_new;
+  }
+  const float m_use = (m == -INFINITY) ? 0.f : m;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    float p0, p1;
+    if (kBias) {
+      p0 = fast_exp2(s[i] - m_use);
+      p1 = fast_exp2(s[i + 1] - m_use);
+    } else {
+      p0 = fast_exp2(fmaf(s[i], scale_log2, -m_use));
+      p1 = fast_exp2(fmaf(s[i + 1], scale_log2, -m_use));
+    }
+    pk[i >> 1] = cvt_pk_bf16(p0, p1);
+    l = dot2_bf16_ones(pk[i >> 1], l);
+  }
+  return raise;
+}
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 31;  // query row within the wave (MFMA n index)
+// P^T B operand for key step u of a half: elements 8u..8u+7.
+__device__ inline sa_bf16x8 p_operand(const uint32_t (&pk)[8], int u) {
+  return as_bf16x8(make_uint4(pk[4 * u], pk[4 * u + 1], pk[4 * u + 2], pk[4 * u + 3]));
+}
+
+template <bool kBias>
+__global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kWaves][kVtElems];
+
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform values are made provably uniform (readfirstlane) so that the list and
+  // order reads below are scalar loads: a vector load would need s_waitcnt vmcnt(0),
+  // which would also wait for the K/V prefetches in flight.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31;  // query column within a 32-row group (MFMA n index)
   const int hh = lane >> 5;   // lane half (MFMA k group)
-
-  // Query blocks are visited block-row major, so the text rows (longest lists, block
-  // rows 0..3 for CogVideoX) are dispatched first.
-  const int wg = blockIdx.x;
-  const int qb = wg / a.BH;
-  const int bh = wg - qb * a.BH;
+  const int slot = blockIdx.x * kWaves + wave;
+  if (slot >= a.n_slots) return;
+  const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[slot] : slot);
+  if (item < 0 || item >= a.n_items) return;  // idle slot (no workgroup barriers below)
+  const int bh = item / a.nqb;
+  const int qb = item - bh * a.nqb;
   const int b = bh / a.H;
   const int h = bh - b * a.H;
+  uint16_t* vt = vt_lds[wave];
 
-  const int64_t list_row = (int64_t)bh * a.nqb + qb;
-  int cnt = a.kv_cnt[list_row];
+  int cnt = a.kv_cnt[item];
   cnt = cnt < 0 ? 0 : (cnt > a.max_cnt ? a.max_cnt : cnt);
-  const int32_t* list = a.kv_idx + list_row * a.max_cnt;
+  const int32_t* list = a.kv_idx + (int64_t)item * a.max_cnt;
 
   const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kbase = a.k + b * a.k_sb + h * a.k_sh;
@@ -164,201 +233,172 @@ __global__ __launch_bounds__(kThreads) void bsa_fwd_kernel(FwdArgs a) {
   uint16_t* obase = a.o + b * a.o_sb + h * a.o_sh;
   const float* bbase = kBias ? a.bias + b * a.bias_sb + h * a.bias_sh : nullptr;
 
-  // Q^T fragments (MFMA B operand): lane holds q[row][16s + 8hh .. +7] for s = 0..3.
-  const int qrow = qb * kBlock + wave * 32 + col;
-  sa_bf16x8 qf[4];
+  // Q^T B operands: qf[g][s] = q[qb*64 + 32g + col][16s + 8hh .. +7].
+  sa_bf16x8 qf[2][4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    sa_u16x8 t = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (qrow < a.Lq) t = *reinterpret_cast<const sa_u16x8*>(qbase + (int64_t)qrow * a.q_sl + 16 * s + 8 * hh);
-    qf[s] = as_bf16x8(t);
+  for (int g = 0; g < 2; ++g) {
+    const int row = min(qb * kBlock + 32 * g + col, a.Lq - 1);
+    const uint16_t* p = qbase + (int64_t)row * a.q_sl + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[g][s] = as_bf16x8(*reinterpret_cast<const uint4*>(p + 16 * s));
   }
 
-  sa_f32x16 acc0 = {}, acc1 = {};
-  float m_i = -INFINITY;
-  float l_i = 0.f;
+  sa_f32x16 acc[2][2];  // [dc][g]
+#pragma unroll
+  for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+    for (int g = 0; g < 2; ++g) acc[dc][g] = sa_f32x16{};
+  float m[2] = {-INFINITY, -INFINITY};
+  float l[2] = {0.f, 0.f};
 
-  TileRegs regs;
-  int kb_cur = 0;
-  if (cnt > 0) {
-    kb_cur = list[0];
-    load_tile<kBias>(a, kbase, vbase, bbase, kb_cur, tid, regs);
-    store_tile<kBias>(k_lds[0], vt_lds[0], b_lds[0], tid, regs);
+  // Skip list entries outside the key-block grid.
+  auto next_valid = [&](int it) {
+    while (it < cnt && (unsigned)list[it] >= (unsigned)a.nkb) ++it;
+    return it;
+  };
+
+  int it = next_valid(0);
+  uint4 kr[2][4];
+  uint4 vr[2][4];
+  int kb_cur = it < cnt ? list[it] : 0;
+  if (it < cnt) {
+    load_k(a, kbase, kb_cur * kBlock, col, hh, kr);
+    load_v(a, vbase, kb_cur * kBlock, lane, vr);
+    store_vt(vt, lane, vr);
   }
-  __syncthreads();
+  int it_next = next_valid(it + 1);
+  // Prefetches are issued every iteration (past the end of the list they re-load the
+  // current block) so the loop body has the same loads in flight on every path.
+  int kb_next = it_next < cnt ? list[it_next] : kb_cur;
+  if (it < cnt) load_v(a, vbase, kb_next * kBlock, lane, vr);
 
-  for (int it = 0; it < cnt; ++it) {
-    const int buf = it & 1;
-    int kb_next = 0;
-    if (it + 1 < cnt) {
-      kb_next = list[it + 1];
-      load_tile<kBias>(a, kbase, vbase, bbase, kb_next, tid, regs);
-    }
-
-    // ---- S^T = K Q^T for keys [0,32) and [32,64) of the tile.
-    const uint16_t* kl = k_lds[buf];
-    sa_f32x16 s0 = {}, s1 = {};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const sa_bf16x8 a0 = as_bf16x8(*reinterpret_cast<const sa_u16x8*>(kl + col * kRowPad + 16 * st + 8 * hh));
-      const sa_bf16x8 a1 = as_bf16x8(*reinterpret_cast<const sa_u16x8*>(kl + (32 + col) * kRowPad + 16 * st + 8 * hh));
-      s0 = mfma32(a0, qf[st], s0);
-      s1 = mfma32(a1, qf[st], s1);
-    }
-    // Element i of s_c is key 32c + 8(i/4) + 4hh + (i%4) of the tile, query `col`.
-
-    const bool kb_ok = (unsigned)kb_cur < (unsigned)a.nkb;
-    const int nvalid = kb_ok ? min(kBlock, a.Lk - kb_cur * kBlock) : 0;
-    if (nvalid < kBlock) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = 8 * (i >> 2) + 4 * hh + (i & 3);
-        if (key >= nvalid) s0[i] = -INFINITY;
-        if (key + 32 >= nvalid) s1[i] = -INFINITY;
-      }
-    }
-
-    float m_new;
-    if (kBias) {
-      const float* bl = b_lds[buf];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = 8 * (i >> 2) + 4 * hh + (i & 3);
-        s0[i] = fmaf(s0[i], a.scale_log2, bl[key]);
-        s1[i] = fmaf(s1[i], a.scale_log2, bl[key + 32]);
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fmaxf(s0[i], s1[i]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      m_new = fmaxf(m_i, mx);
-    } else {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fmaxf(s0[i], s1[i]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      m_new = fmaxf(m_i, mx * a.scale_log2);
-    }
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = fast_exp2(m_i - m_use);
-    float psum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (kBias) {
-        s0[i] = fast_exp2(s0[i] - m_use);
-        s1[i] = fast_exp2(s1[i] - m_use);
-      } else {
-        s0[i] = fast_exp2(fmaf(s0[i], a.scale_log2, -m_use));
-        s1[i] = fast_exp2(fmaf(s1[i], a.scale_log2, -m_use));
-      }
-      psum += s0[i] + s1[i];
-    }
-    l_i = l_i * alpha + psum;
-    m_i = m_new;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      acc0[i] *= alpha;
-      acc1[i] *= alpha;
-    }
-
-    // P^T as MFMA B operands: step (c, u) holds keys 32c + 16u + [0, 16).
-    sa_bf16x8 pb[2][2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        pb[0][u][j] = (__bf16)s0[8 * u + j];
-        pb[1][u][j] = (__bf16)s1[8 * u + j];
-      }
-    }
-
-    // ---- O^T += V^T P^T. A operand: V^T[d][keys 32c+16u+4hh+{0..3}, +8+{0..3}].
-    const uint16_t* vl = vt_lds[buf];
+  while (it < cnt) {
+    const int key0 = kb_cur * kBlock;
+    const int nvalid = min(kBlock, a.Lk - key0);
+    // Two 32-key halves per tile keep one half's S (32 VGPRs) and P (16) live at a time.
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
+      sa_f32x16 s[2];  // [g]: S^T of keys 32c.., query group g
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        sa_f32x16 t = {};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) t = mfma32(as_bf16x8(kr[c][st]), qf[g][st], t);
+        s[g] = t;
+      }
+      if (c == 1) load_k(a, kbase, kb_next * kBlock, col, hh, kr);
+
+      if (nvalid < kBlock) {  // keys past Lk in the last (partial) block
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = 32 * c + 8 * (i >> 2) + 4 * hh + (i & 3);
+          if (key >= nvalid) {
+            s[0][i] = -INFINITY;
+            s[1][i] = -INFINITY;
+          }
+        }
+      }
+      float bl[16];
+      if (kBias) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int key = key0 + 32 * c + 8 * q4 + 4 * hh;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bl[4 * q4 + j] = bbase[min(key + j, a.Lk - 1)] * kLog2e;
+        }
+      }
+
+      uint32_t pk[2][8];
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        float alpha = 1.f;
+        if (softmax16<kBias>(s[g], bl, a.scale_log2, m[g], l[g], pk[g], alpha)) {
+#pragma unroll
+          for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
+        }
+      }
+      // O^T += V^T P^T over this half's two 16-key steps.
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int kofs = 32 * c + 16 * u + 4 * hh;
-        const uint16_t* r0 = vl + col * kRowPad + kofs;
-        const uint16_t* r1 = vl + (32 + col) * kRowPad + kofs;
-        const sa_u16x4 lo0 = *reinterpret_cast<const sa_u16x4*>(r0);
-        const sa_u16x4 hi0 = *reinterpret_cast<const sa_u16x4*>(r0 + 8);
-        const sa_u16x4 lo1 = *reinterpret_cast<const sa_u16x4*>(r1);
-        const sa_u16x4 hi1 = *reinterpret_cast<const sa_u16x4*>(r1 + 8);
-        const sa_u16x8 v0 = {lo0[0], lo0[1], lo0[2], lo0[3], hi0[0], hi0[1], hi0[2], hi0[3]};
-        const sa_u16x8 v1 = {lo1[0], lo1[1], lo1[2], lo1[3], hi1[0], hi1[1], hi1[2], hi1[3]};
-        acc0 = mfma32(as_bf16x8(v0), pb[c][u], acc0);
-        acc1 = mfma32(as_bf16x8(v1), pb[c][u], acc1);
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc) {
+          const sa_bf16x8 va = read_vt(vt, dc, c, u, col, hh);
+#pragma unroll
+          for (int g = 0; g < 2; ++g) acc[dc][g] = mfma32(va, p_operand(pk[g], u), acc[dc][g]);
+        }
       }
     }
 
-    if (it + 1 < cnt) store_tile<kBias>(k_lds[buf ^ 1], vt_lds[buf ^ 1], b_lds[buf ^ 1], tid, regs);
-    __syncthreads();
+    // ---- V^T of the next tile into the (now free) LDS tile; prefetch the one after.
+    // LDS accesses of one wave execute in order and the compiler keeps the program order
+    // of these aliasing accesses, so no fence is needed (a fence would also wait for the
+    // global prefetches).
+    it = it_next;
     kb_cur = kb_next;
+    store_vt(vt, lane, vr);
+    it_next = next_valid(it + 1);
+    kb_next = it_next < cnt ? list[it_next] : kb_cur;
+    load_v(a, vbase, kb_next * kBlock, lane, vr);
   }
 
-  // ---- Epilogue: out = acc / l; each lane half holds a partial l over its keys.
-  const float l_tot = l_i + __shfl_xor(l_i, 32);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qrow < a.Lq) {
-    uint16_t* orow = obase + (int64_t)qrow * a.o_sl;
+  // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      sa_bf16x4 w0, w1;
+  for (int g = 0; g < 2; ++g) {
+    const float l_tot = l[g] + __shfl_xor(l[g], 32);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const int row = qb * kBlock + 32 * g + col;
+    if (row < a.Lq) {
+      uint16_t* orow = obase + (int64_t)row * a.o_sl;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        w0[j] = (__bf16)(acc0[4 * g + j] * inv);
-        w1[j] = (__bf16)(acc1[4 * g + j] * inv);
+      for (int dc = 0; dc < 2; ++dc) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const sa_f32x16& A = acc[dc][g];
+          // element 4q4 + j is d = 32dc + 8q4 + 4hh + j
+          *reinterpret_cast<uint2*>(orow + 32 * dc + 8 * q4 + 4 * hh) =
+              make_uint2(cvt_pk_bf16(A[4 * q4] * inv, A[4 * q4 + 1] * inv),
+                         cvt_pk_bf16(A[4 * q4 + 2] * inv, A[4 * q4 + 3] * inv));
+        }
       }
-      // acc_dc element 4g+j is d = 32dc + 8g + 4hh + j.
-      *reinterpret_cast<sa_bf16x4*>(orow + 8 * g + 4 * hh) = w0;
-      *reinterpret_cast<sa_bf16x4*>(orow + 32 + 8 * g + 4 * hh) = w1;
     }
   }
-}
-
-// One wave per list row: ballot-compact the set entries of mask row (b, h, m).
-__global__ __launch_bounds__(256) void mask_to_list_kernel(const uint8_t* __restrict__ mask, int64_t s0,
-                                                          int64_t s1, int64_t s2, int64_t s3, int H,
-                                                          int nqb, int nkb, int64_t rows,
-                                                          int32_t* __restrict__ kv_idx, int max_cnt,
-                                                          int32_t* __restrict__ kv_cnt) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  if (row >= rows) return;
-  const int lane = threadIdx.x & 63;
-  const int64_t bh = row / nqb;
-  const int m = (int)(row - bh * nqb);
-  const int64_t b = bh / H;
-  const int64_t h = bh - b * H;
-  const uint8_t* base = mask + b * s0 + h * s1 + (int64_t)m * s2;
-  int32_t* out = kv_idx + row * max_cnt;
-  int total = 0;
-  for (int n0 = 0; n0 < nkb; n0 += 64) {
-    const int n = n0 + lane;
-    const bool on = n < nkb && base[(int64_t)n * s3] != 0;
-    const uint64_t bal = __ballot(on);
-    const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
-    if (on) out[total + pre] = n;
-    total += __popcll(bal);
-  }
-  if (lane == 0) kv_cnt[row] = total;
 }
 
 }  // namespace
 
-extern "C" int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B, int H,
-                                  int nqb, int nkb, int32_t* kv_idx, int max_cnt, int32_t* kv_cnt,
-                                  void* stream) {
-  SA_REQUIRE(mask && mask_strides && kv_idx && kv_cnt, "sa_mask_to_kv_list: null pointer");
-  SA_REQUIRE(B > 0 && H > 0 && nqb > 0 && nkb > 0, "sa_mask_to_kv_list: bad shape B=%d H=%d nqb=%d nkb=%d", B, H, nqb, nkb);
-  SA_REQUIRE(max_cnt >= nkb, "sa_mask_to_kv_list: max_cnt=%d < nkb=%d", max_cnt, nkb);
-  const int64_t rows = (int64_t)B * H * nqb;
-  const int64_t blocks = (rows + 3) / 4;
-  SA_REQUIRE(blocks < (1LL << 31), "sa_mask_to_kv_list: too many rows");
-  hipLaunchKernelGGL(mask_to_list_kernel, dim3((unsigned)blocks), dim3(256), 0, sa::as_stream(stream), mask,
-                     mask_strides[0], mask_strides[1], mask_strides[2], mask_strides[3], H, nqb, nkb, rows,
-                     kv_idx, max_cnt, kv_cnt);
-  return sa::check_launch("sa_mask_to_kv_list");
+extern "C" int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int n_xcd, int32_t* order,
+                                  int64_t* n_slots) {
+  SA_REQUIRE(n_slots, "sa_attn_work_order: null n_slots");
+  SA_REQUIRE(B > 0 && H > 0 && nqb > 0 && n_text_blocks >= 0 && n_xcd > 0,
+             "sa_attn_work_order: bad arguments B=%d H=%d nqb=%d n_text=%d n_xcd=%d", B, H, nqb, n_text_blocks, n_xcd);
+  const int64_t n_items = (int64_t)B * H * nqb;
+  SA_REQUIRE(n_items < (1LL << 30), "sa_attn_work_order: too many items");
+  // Contiguous bh-major chunks of (nearly) equal size, one per XCD.
+  std::vector<int64_t> lo(n_xcd + 1);
+  for (int x = 0; x <= n_xcd; ++x) lo[x] = n_items * x / n_xcd;
+  int64_t max_chunk = 0;
+  for (int x = 0; x < n_xcd; ++x) max_chunk = std::max<int64_t>(max_chunk, lo[x + 1] - lo[x]);
+  const int64_t wg_per_xcd = (max_chunk + kWaves - 1) / kWaves;
+  const int64_t total = wg_per_xcd * n_xcd * kWaves;
+  *n_slots = total;
+  if (!order) return sa::ok();
+  for (int64_t i = 0; i < total; ++i) order[i] = -1;
+  std::vector<int32_t> chunk;
+  for (int x = 0; x < n_xcd; ++x) {
+    chunk.clear();
+    // Text rows (longest lists) first, then the rest; bh-major within each class.
+    for (int pass = 0; pass < 2; ++pass)
+      for (int64_t it = lo[x]; it < lo[x + 1]; ++it) {
+        const bool text = (it % nqb) < n_text_blocks;
+        if (text == (pass == 0)) chunk.push_back((int32_t)it);
+      }
+    // Workgroup w of this XCD is dispatch index w*n_xcd + x (round-robin dispatch).
+    for (size_t p = 0; p < chunk.size(); ++p) {
+      const int64_t w = (int64_t)p / kWaves;
+      order[(w * n_xcd + x) * kWaves + (int64_t)p % kWaves] = chunk[p];
+    }
+  }
+  return sa::ok();
 }
 
 extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
@@ -366,7 +406,7 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
                                    uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
                                    int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
                                    const float* key_bias, const int64_t bias_strides[2], float sm_scale,
-                                   void* stream) {
+                                   const int32_t* work_order, int64_t n_slots, void* stream) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "sa_block_sparse_fwd: null pointer");
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "sa_block_sparse_fwd: bad shape B=%d H=%d Lq=%d Lk=%d", B, H, Lq, Lk);
@@ -376,6 +416,13 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   const int nkb = sa::cdiv(Lk, kBlock);
   SA_REQUIRE(max_cnt > 0, "sa_block_sparse_fwd: max_cnt must be > 0");
   SA_REQUIRE(!key_bias || bias_strides, "sa_block_sparse_fwd: key_bias without bias_strides");
+  const int64_t n_items = (int64_t)B * H * nqb;
+  SA_REQUIRE(n_items < (1LL << 30), "sa_block_sparse_fwd: too many query blocks");
+  if (work_order) {
+    SA_REQUIRE(n_slots > 0 && n_slots % kWaves == 0, "sa_block_sparse_fwd: n_slots must be a positive multiple of 4");
+  } else {
+    n_slots = (n_items + kWaves - 1) / kWaves * kWaves;
+  }
   // 16-byte vector accesses: base pointers 16-byte aligned, row strides multiples of 8 elements.
   const void* ptrs[4] = {q, k, v, out};
   for (const void* p : ptrs) {
@@ -389,7 +436,7 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
         return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd: strides must be multiples of 8 elements");
     }
   }
-  const int64_t grid = (int64_t)B * H * nqb;
+  const int64_t grid = n_slots / kWaves;
   SA_REQUIRE(grid < (1LL << 31), "sa_block_sparse_fwd: grid too large");
 
   FwdArgs a;
@@ -398,7 +445,10 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   a.k_sb = k_strides[0]; a.k_sh = k_strides[1]; a.k_sl = k_strides[2];
   a.v_sb = v_strides[0]; a.v_sh = v_strides[1]; a.v_sl = v_strides[2];
   a.o_sb = out_strides[0]; a.o_sh = out_strides[1]; a.o_sl = out_strides[2];
-  a.H = H; a.Lq = Lq; a.Lk = Lk; a.nqb = nqb; a.nkb = nkb; a.BH = B * H;
+  a.H = H; a.Lq = Lq; a.Lk = Lk; a.nqb = nqb; a.nkb = nkb;
+  a.n_items = (int)n_items;
+  a.order = work_order;
+  a.n_slots = (int)n_slots;
   a.kv_idx = kv_idx; a.kv_cnt = kv_cnt; a.max_cnt = max_cnt;
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
@@ -407,9 +457,9 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
 
   hipStream_t s = sa::as_stream(stream);
   if (key_bias) {
-    hipLaunchKernelGGL(bsa_fwd_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(bsa_fwd_kernel<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, s, a);
   } else {
-    hipLaunchKernelGGL(bsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(bsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, s, a);
   }
   return sa::check_launch("sa_block_sparse_fwd");
 }

@@ -16,6 +16,7 @@ Differences from the reference, by design:
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -35,11 +36,34 @@ def _prep_qkv(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None):
+N_XCD = 8  # MI355X: workgroups are dealt round-robin to 8 XCDs, each with its own L2
+
+_ORDER_CACHE = {}
+
+
+def work_order(B: int, H: int, nqb: int, n_text_blocks: int, device) -> torch.Tensor:
+    """Device copy of the attention dispatch order (`sa_attn_work_order`), cached per shape."""
+    key = (B, H, nqb, n_text_blocks, str(device))
+    order = _ORDER_CACHE.get(key)
+    if order is None:
+        lib = _lib.load()
+        n = ctypes.c_int64(0)
+        _lib.check(lib.sa_attn_work_order(B, H, nqb, n_text_blocks, N_XCD, None, ctypes.byref(n)), "sa_attn_work_order")
+        host = torch.empty(n.value, dtype=torch.int32)
+        _lib.check(lib.sa_attn_work_order(B, H, nqb, n_text_blocks, N_XCD, host.data_ptr(), ctypes.byref(n)),
+                   "sa_attn_work_order")
+        order = host.to(device)
+        _ORDER_CACHE[key] = order
+    return order
+
+
+def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None,
+                           n_text_blocks: int = 0):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
     q [B,H,Lq,64], k/v [B,H,Lk,64] bf16 on the GPU; key_bias optional fp32 [B,H,Lk] (any
-    strides with a contiguous key axis, stride 0 to broadcast).
+    strides with a contiguous key axis, stride 0 to broadcast). `n_text_blocks` only
+    affects scheduling (those block rows are dispatched first).
     """
     _lib.require_gpu(q, k, v)
     q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
@@ -57,6 +81,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
             raise ValueError("key_bias must be fp32 [B,H,Lk] with a contiguous key axis")
         key_bias = key_bias.expand(B, H, Lk)
         bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
+    order = work_order(B, H, math.ceil(Lq / BLOCK), n_text_blocks, q.device)
     lib = _lib.load()
     with torch.cuda.device(q.device):
         rc = lib.sa_block_sparse_fwd(
@@ -67,6 +92,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
             B, H, Lq, Lk, D,
             kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt,
             bias_ptr, bias_strides, float(sm_scale),
+            order.data_ptr(), order.numel(),
             _lib.stream_of(q),
         )
     _lib.check(rc, "sa_block_sparse_fwd")

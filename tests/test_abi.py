@@ -43,7 +43,7 @@ def test_null_pointers_rejected(lib):
     assert b"null" in lib.sa_last_error()
     s3 = _lib.i64(0, 0, 0)
     rc = lib.sa_block_sparse_fwd(None, s3, None, s3, None, s3, None, s3, 1, 1, 64, 64, 64,
-                                 None, None, 1, None, None, 0.125, None)
+                                 None, None, 1, None, None, 0.125, None, 0, None)
     assert rc == _lib.SA_ERR_INVALID
 
 
@@ -51,11 +51,11 @@ def test_bad_shapes_rejected(lib):
     dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     s3 = _lib.i64(0, 0, 0)
     args = [dummy, s3, dummy, s3, dummy, s3, dummy, s3]
-    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 128, dummy, dummy, 2, None, None, 0.125, None)
+    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 128, dummy, dummy, 2, None, None, 0.125, None, 0, None)
     assert rc == _lib.SA_ERR_UNSUPPORTED and b"head_dim" in lib.sa_last_error()
-    rc = lib.sa_block_sparse_fwd(*args, 0, 1, 64, 64, 64, dummy, dummy, 2, None, None, 0.125, None)
+    rc = lib.sa_block_sparse_fwd(*args, 0, 1, 64, 64, 64, dummy, dummy, 2, None, None, 0.125, None, 0, None)
     assert rc == _lib.SA_ERR_INVALID
-    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 64, dummy, dummy, 2, None, None, -1.0, None)
+    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 64, dummy, dummy, 2, None, None, -1.0, None, 0, None)
     assert rc == _lib.SA_ERR_INVALID and b"sm_scale" in lib.sa_last_error()
     st = _lib.i64(0, 0, 0, 0)
     rc = lib.sa_mask_to_kv_list(dummy, st, 1, 1, 2, 5, dummy, 4, dummy, None)
@@ -70,3 +70,24 @@ def test_check_maps_codes_to_exceptions(lib):
         _lib.check(_lib.SA_ERR_UNSUPPORTED, "x")
     with pytest.raises(_lib.SAError):
         _lib.check(_lib.SA_ERR_HIP, "x")
+
+
+def test_work_order_is_a_permutation(lib):
+    import ctypes
+    import torch
+    for B, H, nqb, nt in [(2, 30, 278, 4), (1, 1, 1, 0), (1, 3, 5, 2), (2, 30, 705, 4)]:
+        n = ctypes.c_int64(0)
+        assert lib.sa_attn_work_order(B, H, nqb, nt, 8, None, ctypes.byref(n)) == 0
+        assert n.value % 4 == 0 and n.value >= B * H * nqb
+        order = torch.empty(n.value, dtype=torch.int32)
+        assert lib.sa_attn_work_order(B, H, nqb, nt, 8, order.data_ptr(), ctypes.byref(n)) == 0
+        items = order[order >= 0]
+        assert torch.equal(items.sort().values, torch.arange(B * H * nqb, dtype=torch.int32))
+        # Within each XCD (dispatch index % 8), text rows come before video rows.
+        slots = torch.arange(n.value)
+        for x in range(8):
+            mine = order[((slots // 4) % 8) == x]
+            mine = mine[mine >= 0]
+            text = (mine % nqb) < nt
+            if text.any() and (~text).any():
+                assert text.nonzero().max() < (~text).nonzero().min()
