@@ -22,7 +22,7 @@ namespace {
 constexpr int kPoolD = 64;        // head dim handled by the pooling kernel
 constexpr int kRowsPerWG = 16;    // score rows per top-k workgroup (4 per wave)
 constexpr int kColChunk = 64;     // key blocks staged in LDS per step
-constexpr int kKpStride = 65;     // LDS stride (floats) of a staged pooled-K row
+constexpr int kKpStride = 68;     // LDS stride (floats) of a staged pooled-K row (float4, conflict-free)
 
 // ---------------------------------------------------------------------------------------
 // Pooling: wave = 8 blocks; lane = (block lane>>3, dims 8*(lane&7)..+7); each lane sums its
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Top-k: workgroup = 16 score rows of one (b, h); wave w sorts rows 4w..4w+3.
+// Top-k: workgroup = 16 score rows of one (b, h); wave w selects rows 4w..4w+3.
 struct TopkArgs {
   const float* qp;         // [BH][nqb][D] (null when scores_in is given)
   const float* kp;         // [BH][nkb][D]
@@ -98,61 +98,17 @@ __device__ inline uint32_t order_bits(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Ascending 64-bit key: (score descending, index ascending).
-__device__ inline uint64_t sort_key(float score, int idx) {
-  return ((uint64_t)(~order_bits(score)) << 32) | (uint32_t)idx;
-}
-
-__device__ inline uint64_t shfl_xor_u64(uint64_t x, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)x, m);
-  const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), m);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-// Bitonic sort (ascending) of 64*NPL keys held as element i = lane*NPL + e.
-template <int NPL>
-__device__ inline void wave_bitonic_sort(uint64_t (&x)[NPL], int lane) {
-  constexpr int N = 64 * NPL;
-#pragma unroll
-  for (int k = 2; k <= N; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j >= NPL) {
-        const int m = j / NPL;
-        const bool lower = (lane & m) == 0;
-#pragma unroll
-        for (int e = 0; e < NPL; ++e) {
-          const int i = lane * NPL + e;
-          const bool asc = (i & k) == 0;
-          const uint64_t o = shfl_xor_u64(x[e], m);
-          const bool take_min = (lower == asc);
-          x[e] = take_min ? (o < x[e] ? o : x[e]) : (o > x[e] ? o : x[e]);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < NPL; ++e) {
-          const int p = e ^ j;
-          if (p > e) {
-            const int i = lane * NPL + e;
-            const bool asc = (i & k) == 0;
-            const uint64_t lo = x[e] < x[p] ? x[e] : x[p];
-            const uint64_t hi = x[e] < x[p] ? x[p] : x[e];
-            x[e] = asc ? lo : hi;
-            x[p] = asc ? hi : lo;
-          }
-        }
-      }
-    }
-  }
-}
-
-template <int NPL>
+// Selection per row (one wave): the k-th largest 32-bit ordered score T is found by a
+// 32-step bitwise search (each step counts keys >= candidate with ballots), then one pass
+// in ascending column order keeps every key > T and the lowest-index keys == T until k are
+// kept -- exactly the first k columns in (score descending, column ascending) order -- and
+// writes the union with text rows/columns and the local window as the ascending kv list.
+template <int NCH>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
-  constexpr int NPAD = 64 * NPL;
+  constexpr int NPAD = 64 * NCH;
   __shared__ float s_lds[kRowsPerWG][NPAD];
-  __shared__ float q_lds[kRowsPerWG][kPoolD];
-  __shared__ float k_lds[kColChunk * kKpStride];
-  __shared__ uint32_t bits[kRowsPerWG][NPAD / 32];
+  __shared__ __attribute__((aligned(16))) float q_lds[kRowsPerWG][kPoolD];
+  __shared__ __attribute__((aligned(16))) float k_lds[kColChunk * kKpStride];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -167,28 +123,40 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       if (r0 + rr < a.nqb) s_lds[rr][c] = a.scores_in[(row_base + r0 + rr) * a.nkb + c];
     }
   } else {
-    const int D = a.D;
-    for (int e = tid; e < kRowsPerWG * D; e += 256) {
-      const int rr = e / D, d = e - rr * D;
-      q_lds[rr][d] = (r0 + rr < a.nqb) ? a.qp[(row_base + r0 + rr) * D + d] : 0.f;
+    // q rows and 64-column chunks of pooled K staged as float4; score = fmaf chain over
+    // d ascending (the same order as the oracle), 4 rows per thread.
+    for (int e = tid; e < kRowsPerWG * (kPoolD / 4); e += 256) {
+      const int rr = e >> 4, d4 = e & 15;
+      const float4 v = (r0 + rr < a.nqb)
+                           ? *reinterpret_cast<const float4*>(a.qp + (row_base + r0 + rr) * kPoolD + 4 * d4)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4*>(&q_lds[rr][4 * d4]) = v;
     }
-    const float* kpb = a.kp + (int64_t)bh * a.nkb * D;
+    const float* kpb = a.kp + (int64_t)bh * a.nkb * kPoolD;
     for (int c0 = 0; c0 < a.nkb; c0 += kColChunk) {
       __syncthreads();
       const int nc = min(kColChunk, a.nkb - c0);
-      for (int e = tid; e < nc * D; e += 256) {
-        const int c = e / D, d = e - c * D;
-        k_lds[c * kKpStride + d] = kpb[(int64_t)(c0 + c) * D + d];
+      for (int e = tid; e < nc * (kPoolD / 4); e += 256) {
+        const int c = e >> 4, d4 = e & 15;
+        *reinterpret_cast<float4*>(&k_lds[c * kKpStride + 4 * d4]) =
+            *reinterpret_cast<const float4*>(kpb + (int64_t)(c0 + c) * kPoolD + 4 * d4);
       }
       __syncthreads();
       const int c = tid & 63;
       const int rg = (tid >> 6) * 4;
       if (c < nc) {
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int d = 0; d < D; ++d) {
-          const float kv = k_lds[c * kKpStride + d];
+#pragma unroll 4
+        for (int d = 0; d < kPoolD; d += 4) {
+          const float4 kv = *reinterpret_cast<const float4*>(&k_lds[c * kKpStride + d]);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) acc[u] = fmaf(q_lds[rg + u][d], kv, acc[u]);
+          for (int u = 0; u < 4; ++u) {
+            const float4 qv = *reinterpret_cast<const float4*>(&q_lds[rg + u][d]);
+            acc[u] = fmaf(qv.x, kv.x, acc[u]);
+            acc[u] = fmaf(qv.y, kv.y, acc[u]);
+            acc[u] = fmaf(qv.z, kv.z, acc[u]);
+            acc[u] = fmaf(qv.w, kv.w, acc[u]);
+          }
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) s_lds[rg + u][c0 + c] = acc[u];
@@ -197,45 +165,53 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   }
   __syncthreads();
 
-  const int words = (a.nkb + 31) >> 5;
+  const int nch = (a.nkb + 63) >> 6;
   for (int u = 0; u < 4; ++u) {
     const int rr = wave * 4 + u;
     const int r = r0 + rr;
     if (r >= a.nqb) break;  // wave-uniform
     const int64_t row = row_base + r;
-    uint64_t key[NPL];
+    // Ordered keys of this lane's columns c = 64e + lane (0 = below every real key's use).
+    uint32_t key[NCH];
 #pragma unroll
-    for (int e = 0; e < NPL; ++e) {
-      const int i = lane * NPL + e;
-      key[e] = i < a.nkb ? sort_key(s_lds[rr][i], i) : ~0ull;
+    for (int e = 0; e < NCH; ++e) {
+      const int c = 64 * e + lane;
+      key[e] = (e < nch && c < a.nkb) ? order_bits(s_lds[rr][c]) : 0u;
+      if (a.scores_out && e < nch && c < a.nkb) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
     }
-    if (a.scores_out) {
-      for (int c = lane; c < a.nkb; c += 64) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
-    }
-    wave_bitonic_sort<NPL>(key, lane);
-    for (int w = lane; w < words; w += 64) bits[rr][w] = 0u;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const int k = a.topk < a.nkb ? a.topk : a.nkb;
+    uint32_t thr = 0u;   // the k-th largest key (0 when k == 0: then nothing is selected)
+    int need = 0;        // keys equal to thr to keep, lowest columns first
+    if (k > 0) {
+      for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = thr | (1u << bit);
+        int count = 0;
 #pragma unroll
-    for (int e = 0; e < NPL; ++e) {
-      const int i = lane * NPL + e;
-      if (i < a.topk && i < a.nkb) {
-        const int c = (int)(uint32_t)key[e];
-        atomicOr(&bits[rr][c >> 5], 1u << (c & 31));
+        for (int e = 0; e < NCH; ++e) count += __popcll(__ballot(key[e] >= cand));
+        if (count >= k) thr = cand;
       }
+      int gt = 0;
+#pragma unroll
+      for (int e = 0; e < NCH; ++e) gt += __popcll(__ballot(key[e] > thr));
+      need = k - gt;
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    // Union with text rows/columns and the local window, then ballot-compact in order.
     const bool text_row = r < a.n_text;
     const uint8_t* loc = a.local ? a.local + (int64_t)r * a.nkb : nullptr;
     int32_t* out = a.kv_idx + row * a.max_cnt;
     int total = 0;
-    for (int c0 = 0; c0 < a.nkb; c0 += 64) {
-      const int c = c0 + lane;
+    int ties = 0;
+#pragma unroll
+    for (int e = 0; e < NCH; ++e) {
+      const int c = 64 * e + lane;
+      const bool valid = e < nch && c < a.nkb;
+      const bool tie = valid && k > 0 && key[e] == thr;
+      const uint64_t tb = __ballot(tie);
+      const int tie_rank = ties + __builtin_amdgcn_mbcnt_hi((uint32_t)(tb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)tb, 0));
+      ties += __popcll(tb);
       bool on = false;
-      if (c < a.nkb) {
-        on = text_row || c < a.n_text || ((bits[rr][c >> 5] >> (c & 31)) & 1u);
+      if (valid) {
+        const bool sel = k > 0 && (key[e] > thr || (tie && tie_rank < need));
+        on = sel || text_row || c < a.n_text;
         if (loc) on = on || loc[c] != 0;
         if (a.mask_out) a.mask_out[row * a.nkb + c] = on ? 1 : 0;
       }
@@ -303,6 +279,8 @@ extern "C" int sa_block_topk_kv_list(const float* q_pooled, const float* k_poole
   hipStream_t s = sa::as_stream(stream);
   if (nkb <= 256) {
     hipLaunchKernelGGL(topk_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+  } else if (nkb <= 320) {
+    hipLaunchKernelGGL(topk_kernel<5>, dim3((unsigned)grid), dim3(256), 0, s, a);
   } else if (nkb <= 512) {
     hipLaunchKernelGGL(topk_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, a);
   } else {
