@@ -128,6 +128,19 @@ int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const fl
                           const uint8_t* local_bitmap, int32_t* kv_idx, int max_cnt,
                           int32_t* kv_cnt, uint8_t* mask_out, float* scores_out, void* stream);
 
+/*
+ * (host) Static local 3-D window of the combined mask, one byte per (query block, key
+ * block): 1 iff both blocks are video blocks and their centre tokens (index
+ * block*qb + block/2, clamped to L-1) lie within +-dt latent frames, +-dh patch rows and
+ * +-dw patch columns of each other. Text rows/columns are 0 here (the top-k kernel adds
+ * them). Plays the role of the static local-window masks of the reference: the 3-D tile
+ * window of generate_sta_mask (SildingTileAttention.py:18-87), the +-1-frame tridiagonal
+ * of SmartAttention.py:56-67 and the local part of LocalGlobalAttention.py:114-179.
+ *   bitmap    uint8 [nb][nb], nb = ceil(L/block); L must equal text_len + T*Hp*Wp.
+ */
+int sa_local_window_bitmap(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh,
+                           int dw, uint8_t* bitmap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,8 @@ def lib():
         L.oracle_block_score.restype = ctypes.c_float
         L.oracle_block_topk.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P]
         L.oracle_block_topk.restype = None
+        L.oracle_local_window.argtypes = [_I] * 9 + [_P]
+        L.oracle_local_window.restype = None
         _lib = L
     return _lib
 
@@ -72,3 +74,11 @@ def block_topk(qp, kp, topk: int, n_text: int, local=None, scores_in=None, nqb=N
     lib().oracle_block_topk(_p(qp), _p(kp), _p(scores_in), BH, nqb, nkb, D, topk, n_text, _p(loc),
                             _p(kv_idx), nkb, _p(kv_cnt), _p(mask), _p(scores))
     return kv_idx, kv_cnt, mask, scores
+
+
+def local_window(geom, dt: int, dh: int, dw: int) -> torch.Tensor:
+    """uint8 [nb, nb] local-window bitmap of a Geometry (text_len, T, Hp, Wp, block)."""
+    nb = -(-geom.L // geom.block)
+    out = torch.empty(nb, nb, dtype=torch.uint8)
+    lib().oracle_local_window(geom.L, geom.block, geom.text_len, geom.T, geom.Hp, geom.Wp, dt, dh, dw, _p(out))
+    return out

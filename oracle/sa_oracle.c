@@ -109,3 +109,32 @@ void oracle_block_topk(const float* qp, const float* kp, const float* scores_in,
   free(keys);
   free(keep);
 }
+
+/*
+ * Local 3-D window on block centre tokens (the combined mask's static part), restating the
+ * union of local windows used by the reference's sparse patterns (SildingTileAttention.py
+ * :18-87 tile window, SmartAttention.py:56-67 frame band, LocalGlobalAttention.py:114-179):
+ * block b is represented by token min(b*block + block/2, L-1); both blocks must be video;
+ * |dt|, |dh|, |dw| of their (t, h, w) within the radii.
+ */
+void oracle_local_window(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh, int dw,
+                         uint8_t* bitmap) {
+  (void)T;
+  const int nb = (L + block - 1) / block;
+  for (int qb = 0; qb < nb; ++qb) {
+    int cq = qb * block + block / 2;
+    if (cq > L - 1) cq = L - 1;
+    for (int kb = 0; kb < nb; ++kb) {
+      int ck = kb * block + block / 2;
+      if (ck > L - 1) ck = L - 1;
+      int on = 0;
+      if (cq >= text_len && ck >= text_len) {
+        const int vq = cq - text_len, vk = ck - text_len;
+        const int tq = vq / (Hp * Wp), hq = (vq / Wp) % Hp, wq = vq % Wp;
+        const int tk = vk / (Hp * Wp), hk = (vk / Wp) % Hp, wk = vk % Wp;
+        on = abs(tq - tk) <= dt && abs(hq - hk) <= dh && abs(wq - wk) <= dw;
+      }
+      bitmap[(int64_t)qb * nb + kb] = (uint8_t)on;
+    }
+  }
+}

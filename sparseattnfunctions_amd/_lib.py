@@ -38,6 +38,7 @@ _PROTOTYPES = {
          ctypes.c_int64, _P],
     ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
+    "sa_local_window_bitmap": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

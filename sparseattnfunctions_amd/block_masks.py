@@ -100,3 +100,23 @@ def meanpool_topk_kv_list(q, k, topk: int, n_text_blocks: int, block: int = 64,
     B, H = q.shape[:2]
     qp, kp = pool_blocks(q, k, block)
     return topk_kv_list(qp, kp, B, H, topk, n_text_blocks, local_bitmap=local_bitmap, **kw)
+
+
+_LOCAL_CACHE = {}
+
+
+def local_window_bitmap(geom, window=(1, 8, 8), device=None) -> torch.Tensor:
+    """Static local 3-D window of the combined mask, uint8 [nb, nb] on `device`, cached per
+    (geometry, window, device). Built on the host by `sa_local_window_bitmap`."""
+    key = (geom, tuple(window), str(device))
+    bm = _LOCAL_CACHE.get(key)
+    if bm is None:
+        nb = math.ceil(geom.L / geom.block)
+        host = torch.empty(nb, nb, dtype=torch.uint8)
+        dt, dh, dw = window
+        rc = _lib.load().sa_local_window_bitmap(geom.L, geom.block, geom.text_len, geom.T, geom.Hp, geom.Wp,
+                                                dt, dh, dw, host.data_ptr())
+        _lib.check(rc, "sa_local_window_bitmap")
+        bm = host.to(device) if device is not None else host
+        _LOCAL_CACHE[key] = bm
+    return bm

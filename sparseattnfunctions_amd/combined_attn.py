@@ -1,0 +1,76 @@
+"""`CombinedAttn` processor of special_attentions/combined_attn.py (:7-101), on MI355X.
+
+Keeps the reference API -- `CombinedAttn(warmup_epoch=5)`, `__call__(q, k, v,
+use_rearranger=False)`, the per-call counter `ct` with `layer_num` calls per denoising step
+and dense attention during the first `warmup_epoch` steps (:42-46) -- and computes the
+combined block mask of the MI355X build on the GPU:
+
+    keep(qb, kb) = local 3-D window (+-1 latent frame, +-8 patch rows/cols between block
+                   centre tokens, a static bitmap cached per geometry)
+                 U global top-k of the mean-pooled block scores (k = int(0.10 * nb))
+                 U text block rows and columns,
+
+then runs the block-sparse attention kernel on it. This replaces the reference's
+per-head routing between pattern attention and the SparseGen+ estimator
+(combined_attn.py:47-101, partern_attention.py:516-521), which is host-synchronising and
+1.5-5B specific. `use_rearranger=True` (the reference's 1.5-5B token permutation) is not
+supported with this rule: the local window is defined on the text-first (t, h, w) layout.
+"""
+from __future__ import annotations
+
+import math
+
+from .block_mask_attn import dense_kv_list
+from .block_masks import local_window_bitmap, meanpool_topk_kv_list
+from .utils.block_sparse_attn_kernel import block_sparse_attention
+from .workloads import COGVIDEOX_2B, Geometry, topk_count
+
+
+class CombinedAttn:
+    def __init__(self, warmup_epoch: int = 5, geometry: Geometry = COGVIDEOX_2B, global_ratio: float = 0.10,
+                 window=(1, 8, 8), layer_num: int = 42, timestep: int = 50, sm_scale: float = None):
+        self.layer_num = layer_num
+        self.timestep = timestep
+        self.counter = 0
+        self.ct = 0
+        self.warmup_epoch = warmup_epoch
+        self.geometry = geometry
+        self.global_ratio = global_ratio
+        self.window = tuple(window)
+        self.sm_scale = sm_scale
+        self.last_kv = None
+
+    def n_text_blocks(self) -> int:
+        return math.ceil(self.geometry.text_len / self.geometry.block)
+
+    def build_kv_list(self, q, k):
+        L = q.shape[2]
+        if L != self.geometry.L:
+            raise ValueError(f"sequence length {L} does not match the geometry (L={self.geometry.L})")
+        nb = math.ceil(L / 64)
+        local = local_window_bitmap(self.geometry, self.window, q.device)
+        return meanpool_topk_kv_list(q, k, topk_count(self.global_ratio, nb), self.n_text_blocks(),
+                                     local_bitmap=local)
+
+    def _scale(self, q):
+        return self.sm_scale if self.sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
+
+    def __call__(self, q, k, v, use_rearranger: bool = False):
+        if use_rearranger:
+            raise NotImplementedError(
+                "use_rearranger (the 1.5-5B token permutation, combined_attn.py:17-41) is not supported "
+                "with the combined local-window mask, which is defined on the text-first layout")
+        warm = self.ct // self.layer_num < self.warmup_epoch
+        self.ct += 1
+        if warm:
+            B, H, L, _ = q.shape
+            nb = math.ceil(L / 64)
+            kv = dense_kv_list(B, H, nb, math.ceil(k.shape[2] / 64), q.device)
+        else:
+            kv = self.build_kv_list(q, k)
+        self.last_kv = kv
+        return block_sparse_attention(q, k, v, kv, self._scale(q), n_text_blocks=self.n_text_blocks())
+
+    def sparsity(self) -> float:
+        kv = self.last_kv
+        return 1.0 - kv.cnt.sum().item() / (kv.rows * kv.nkb)

@@ -1,0 +1,100 @@
+"""GPU parity of the processor classes at the CogVideoX-2B shape (configs 2 and 3) and small
+shapes: kv lists bit-exact against the C oracle, outputs within the bf16 tolerances
+(max-abs <= 2e-2, mean-abs <= 2e-3) against the fp64 oracle on a subset of heads."""
+import math
+
+import pytest
+import torch
+
+from conftest import case
+from oracle import native
+from oracle.attention import masked_attention
+from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention
+from sparseattnfunctions_amd.combined_attn import CombinedAttn
+from sparseattnfunctions_amd.workloads import COGVIDEOX_2B, Geometry, cogvideox_qkv, topk_count
+
+pytestmark = pytest.mark.gpu
+
+HEADS = [(0, 0), (0, 13), (1, 29)]
+
+
+def _check(got, want):
+    err = (got.float().cpu().double() - want).abs()
+    assert torch.isfinite(got.float()).all()
+    assert err.max().item() <= 2e-2, err.max().item()
+    assert err.mean().item() <= 2e-3, err.mean().item()
+
+
+def _oracle_mask(q, k, topk, n_text, local=None):
+    nb = math.ceil(q.shape[2] / 64)
+    _, _, m, _ = native.block_topk(native.block_pool(q), native.block_pool(k), topk, n_text, local=local)
+    return m.reshape(q.shape[0], q.shape[1], nb, nb).bool()
+
+
+@pytest.fixture(scope="module")
+def c2_inputs():
+    return cogvideox_qkv(0)
+
+
+def test_block_mask_attn_config2(dev, c2_inputs):
+    case("BlockSparseAttention config 2")
+    q, k, v = c2_inputs
+    proc = BlockSparseAttention(64, keep_ratio=0.2)
+    out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    mask = _oracle_mask(q, k, 55, 4)
+    assert torch.equal(proc.last_kv.to_mask().cpu(), mask)
+    assert 0.75 < proc.sparsity() < 0.80
+    want = masked_attention(q, k, v, mask, 1 / 8, heads=HEADS)
+    for b, h in HEADS:
+        _check(out[b, h], want[b, h])
+
+
+def test_combined_attn_config3(dev, c2_inputs):
+    case("CombinedAttn config 3")
+    q, k, v = c2_inputs
+    proc = CombinedAttn(warmup_epoch=0)
+    out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    nb = COGVIDEOX_2B.nb
+    local = native.local_window(COGVIDEOX_2B, 1, 8, 8)
+    mask = _oracle_mask(q, k, topk_count(0.1, nb), 4, local=local)
+    assert torch.equal(proc.last_kv.to_mask().cpu(), mask)
+    assert 0.80 < proc.sparsity() < 0.88, proc.sparsity()
+    want = masked_attention(q, k, v, mask, 1 / 8, heads=HEADS)
+    for b, h in HEADS:
+        _check(out[b, h], want[b, h])
+
+
+def test_combined_attn_warmup_is_dense(dev):
+    case("CombinedAttn warmup dense + counter")
+    geom = Geometry(text_len=226, T=2, Hp=10, Wp=15)
+    q, k, v = cogvideox_qkv(1, B=1, H=2, geom=geom)
+    proc = CombinedAttn(warmup_epoch=1, geometry=geom, layer_num=2)
+    dense = torch.ones(1, 1, 9, 9, dtype=torch.bool)
+    for call in range(3):
+        out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
+        if call < 2:  # first layer_num calls are the warmup step
+            _check(out, masked_attention(q, k, v, dense, 1 / 8))
+            assert proc.sparsity() == 0.0
+        else:
+            local = native.local_window(geom, 1, 8, 8)
+            mask = _oracle_mask(q, k, topk_count(0.1, 9), 4, local=local)
+            assert torch.equal(proc.last_kv.to_mask().cpu(), mask)
+            _check(out, masked_attention(q, k, v, mask, 1 / 8))
+    assert proc.ct == 3
+    with pytest.raises(NotImplementedError):
+        proc(q.to(dev), k.to(dev), v.to(dev), use_rearranger=True)
+
+
+def test_block_mask_attn_small_and_dense(dev):
+    case("BlockSparseAttention small + forward_dense")
+    geom = Geometry(text_len=226, T=3, Hp=10, Wp=15)
+    q, k, v = cogvideox_qkv(2, B=2, H=3, geom=geom)
+    proc = BlockSparseAttention(64, keep_ratio=0.3, geometry=geom)
+    out = proc(q.to(dev), k.to(dev), v.to(dev))
+    nb = math.ceil(geom.L / 64)
+    mask = _oracle_mask(q, k, topk_count(0.3, nb), 4)
+    _check(out, masked_attention(q, k, v, mask, 1 / 8))
+    dense = proc.forward_dense(q.to(dev), k.to(dev), v.to(dev))
+    _check(dense, masked_attention(q, k, v, torch.ones(1, 1, nb, nb, dtype=torch.bool), 1 / 8))
+    with pytest.raises(NotImplementedError):
+        proc.forward_backup(q, k, v)

@@ -1,0 +1,54 @@
+"""Pins the local-window oracle and checks the library's host bitmap against it (CPU)."""
+import torch
+
+from oracle import native
+from sparseattnfunctions_amd.block_masks import local_window_bitmap
+from sparseattnfunctions_amd.workloads import COGVIDEOX_2B, COGVIDEOX_15_5B, Geometry
+
+
+def _brute(geom, dt, dh, dw):
+    # Independent formulation: coordinates from explicit enumeration of the token grid.
+    coords = {}
+    tok = geom.text_len
+    for t in range(geom.T):
+        for h in range(geom.Hp):
+            for w in range(geom.Wp):
+                coords[tok] = (t, h, w)
+                tok += 1
+    nb = -(-geom.L // geom.block)
+    centre = [min(b * geom.block + geom.block // 2, geom.L - 1) for b in range(nb)]
+    out = torch.zeros(nb, nb, dtype=torch.uint8)
+    for i, ci in enumerate(centre):
+        for j, cj in enumerate(centre):
+            if ci in coords and cj in coords:
+                a, b = coords[ci], coords[cj]
+                out[i, j] = abs(a[0] - b[0]) <= dt and abs(a[1] - b[1]) <= dh and abs(a[2] - b[2]) <= dw
+    return out
+
+
+def test_oracle_matches_brute_force_small():
+    for geom, win in [(Geometry(text_len=10, T=3, Hp=4, Wp=5, block=8), (1, 1, 1)),
+                      (Geometry(text_len=226, T=2, Hp=10, Wp=15), (1, 2, 3)),
+                      (Geometry(text_len=0, T=4, Hp=6, Wp=6, block=16), (0, 1, 1))]:
+        assert torch.equal(native.local_window(geom, *win), _brute(geom, *win))
+
+
+def test_library_host_bitmap_matches_oracle():
+    for geom in (COGVIDEOX_2B, COGVIDEOX_15_5B, Geometry(text_len=226, T=2, Hp=10, Wp=15)):
+        for win in ((1, 8, 8), (0, 2, 2)):
+            assert torch.equal(local_window_bitmap(geom, win), native.local_window(geom, *win))
+
+
+def test_cogvideox_density_and_invariants():
+    geom = COGVIDEOX_2B
+    bm = native.local_window(geom, 1, 8, 8).bool()
+    nb = bm.shape[0]
+    assert nb == 278
+    assert torch.equal(bm, bm.T)                          # the window is symmetric
+    assert bm[4:, 4:].diagonal().all()                    # every video block sees itself
+    assert not bm[:4].any() and not bm[:, :4].any()       # text handled by the text rule
+    text = torch.zeros(nb, nb, dtype=torch.bool)
+    text[:4] = True
+    text[:, :4] = True
+    # Density of local U text with the centre-token rule (independently computed as 0.0680).
+    assert abs((bm | text).float().mean().item() - 0.0680) < 5e-4
