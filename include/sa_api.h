@@ -141,6 +141,84 @@ int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const fl
 int sa_local_window_bitmap(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh,
                            int dw, uint8_t* bitmap);
 
+/* ---- Token merging (ToMe bipartite soft matching) ----------------------------------- */
+
+/*
+ * Matching maps of one call, all caller-owned device buffers; G matching groups (one per
+ * batch item for the head-averaged metric, one per (b, h) for the per-head metric), N
+ * video tokens after text_len text tokens, L = text_len + N, Lm = L - r merged rows laid
+ * out [text | unm (edge order) | dst (partition order)] as in merge_unmerge.py:128.
+ */
+typedef struct sa_tome_maps {
+  int G, N, text_len, n_src, n_dst, r, L, Lm;
+  const int32_t* a_idx;  /* [n_src] video-token index of each src (partition, all groups) */
+  const int32_t* b_idx;  /* [n_dst] video-token index of each dst */
+  int32_t* node_idx;     /* [G][n_src] best dst of each src (merge_unmerge.py:108) */
+  float* node_max;       /* [G][n_src] its cosine score */
+  int32_t* rank;         /* [G][n_src] position of each src in the edge order */
+  int32_t* edge;         /* [G][n_src] edge order: src_idx = edge[:r], unm_idx = edge[r:] (:109-111) */
+  int32_t* dst_idx;      /* [G][r] dst of the e-th merged src (:112) */
+  int32_t* dst_cnt;      /* [G][n_dst] srcs merged into each dst (size - 1, :113-116) */
+  int32_t* dst_cursor;   /* [G][n_dst] scratch */
+  int32_t* dst_ptr;      /* [G][n_dst + 1] CSR offsets of the members of each dst */
+  int32_t* members;      /* [G][r] edge positions grouped by dst, ascending */
+  int32_t* row_of_token; /* [G][L] merged row holding each token (the unmerge map, :137-154) */
+  float* key_bias;       /* [G][Lm] log(size) rounded to bf16, 0 for text/unm (MergeAttention.py:163-167) */
+} sa_tome_maps;
+
+/*
+ * (host) src/dst partition of the video tokens of bipartite_soft_matching_video
+ * (utils/merge_unmerge.py:62-92): every token of the first frame is dst; frames 1..T-1
+ * are cut into (st, sy, sx) cells with one dst per cell at offset cell_choice[cell]
+ * (cells [ (T-1)/st ][ Hp/sy ][ Wp/sx ], offset = (dt*sy + dy)*sx + dx; NULL = 0, the
+ * reference's no_rand top-left); tokens outside whole cells are src. Within each class
+ * tokens are in ascending order (the reference's argsort of the {-1, 0} buffer, made
+ * stable). With a_idx = b_idx = NULL only the counts are returned.
+ */
+int sa_tome_partition(int T, int Hp, int Wp, int sx, int sy, int st, const int32_t* cell_choice,
+                      int32_t* a_idx, int32_t* b_idx, int* n_src, int* n_dst);
+
+/*
+ * Cosine-normalised matching metric of the video tokens (tokens >= text_len).
+ *   mode 0: per batch item, the sum over heads of k (the head mean up to 1/H) -> [B][N][64];
+ *   mode 1: per head, (k, |k|, v, |v|) of MergeAttention.py:26-31 -> [B*H][N][130].
+ * Each row is divided by its L2 norm (merge_unmerge.py:100). fp32 output, contiguous.
+ */
+int sa_tome_metric(const uint16_t* k, const int64_t k_strides[3], const uint16_t* v,
+                   const int64_t v_strides[3], int B, int H, int L, int D, int text_len, int mode,
+                   float* metric, void* stream);
+
+/* Row-wise L2 normalisation of a caller-supplied metric [rows][C] fp32 (merge_unmerge.py:100),
+ * the same arithmetic as sa_tome_metric's last step. */
+int sa_tome_normalize(const float* metric, int64_t rows, int C, float* out, void* stream);
+
+/* Workspace bytes needed by sa_tome_match. */
+int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes);
+
+/*
+ * Bipartite matching and all merge/unmerge maps (merge_unmerge.py:99-116): per src the dst
+ * of highest cosine score (scores never materialised; ties -> lowest dst), edge order by
+ * score descending then src position (stable), the top r merged. metric [G][N][C] fp32,
+ * C <= 130. Fills every buffer of *maps except a_idx/b_idx, which it reads.
+ */
+int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspace,
+                  int64_t workspace_bytes, void* stream);
+
+/*
+ * merge closure for a 4-D [B,H,L,64] tensor (merge_unmerge.py:119-128): out [B,H,Lm,64] =
+ * [text | unm | dst], each dst row the mean of the dst token and its merged srcs (fp32 sum
+ * in edge order, one division, bf16 rounding). Group of head (b, h) = (b*H + h) /
+ * heads_per_group (H for the head-averaged metric, 1 for per-head maps).
+ */
+int sa_tome_merge(const uint16_t* x, const int64_t x_strides[3], int B, int H, int D,
+                  int heads_per_group, const sa_tome_maps* maps, uint16_t* out,
+                  const int64_t out_strides[3], void* stream);
+
+/* unmerge closure (merge_unmerge.py:137-154): out[b,h,t] = xm[b,h,row_of_token[t]]. */
+int sa_tome_unmerge(const uint16_t* xm, const int64_t xm_strides[3], int B, int H, int D,
+                    int heads_per_group, const sa_tome_maps* maps, uint16_t* out,
+                    const int64_t out_strides[3], void* stream);
+
 #ifdef __cplusplus
 }
 #endif

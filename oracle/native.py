@@ -37,6 +37,18 @@ def lib():
         L.oracle_block_topk.restype = None
         L.oracle_local_window.argtypes = [_I] * 9 + [_P]
         L.oracle_local_window.restype = None
+        L.oracle_tome_partition.argtypes = [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
+        L.oracle_tome_partition.restype = None
+        L.oracle_tome_metric.argtypes = [_P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _P]
+        L.oracle_tome_metric.restype = None
+        L.oracle_tome_argmax.argtypes = [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P]
+        L.oracle_tome_argmax.restype = None
+        L.oracle_tome_maps.argtypes = [_P, _P, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P]
+        L.oracle_tome_maps.restype = None
+        L.oracle_tome_match.argtypes = [_P, _I, _I, _I, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]
+        L.oracle_tome_match.restype = None
+        L.oracle_tome_merge.argtypes = [_P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _P, _P, _I, _I, _I, _P, _P, _P]
+        L.oracle_tome_merge.restype = None
         _lib = L
     return _lib
 
@@ -81,4 +93,89 @@ def local_window(geom, dt: int, dh: int, dw: int) -> torch.Tensor:
     nb = -(-geom.L // geom.block)
     out = torch.empty(nb, nb, dtype=torch.uint8)
     lib().oracle_local_window(geom.L, geom.block, geom.text_len, geom.T, geom.Hp, geom.Wp, dt, dh, dw, _p(out))
+    return out
+
+
+def tome_partition(T, Hp, Wp, sx, sy, st, choice=None):
+    """(a_idx, b_idx) int32 tensors of the video-token partition."""
+    N = T * Hp * Wp
+    a = torch.empty(N, dtype=torch.int32)
+    b = torch.empty(N, dtype=torch.int32)
+    ns, nd = ctypes.c_int(0), ctypes.c_int(0)
+    ch = None if choice is None else choice.to(torch.int32).contiguous()
+    lib().oracle_tome_partition(T, Hp, Wp, sx, sy, st, _p(ch), _p(a), _p(b), ctypes.byref(ns), ctypes.byref(nd))
+    return a[: ns.value].clone(), b[: nd.value].clone()
+
+
+def tome_metric(k, v, text_len: int, mode: int) -> torch.Tensor:
+    B, H, L, D = k.shape
+    k = k.contiguous()
+    v = v.contiguous() if v is not None else k
+    N = L - text_len
+    out = torch.empty((B, N, 64) if mode == 0 else (B * H, N, 130), dtype=torch.float32)
+    lib().oracle_tome_metric(_p(k.view(torch.int16)), _p(v.view(torch.int16)), k.stride(0), k.stride(1), k.stride(2),
+                             B, H, L, text_len, mode, _p(out))
+    return out
+
+
+def tome_match(metric, a_idx, b_idx, r: int, text_len: int):
+    """Returns a dict of the maps (node_idx, node_max, edge, dst_idx, dst_cnt, row_of_token, key_bias)."""
+    G, N, C = metric.shape
+    ns, nd = a_idx.numel(), b_idx.numel()
+    L = text_len + N
+    out = dict(node_idx=torch.empty(G, ns, dtype=torch.int32), node_max=torch.empty(G, ns),
+               edge=torch.empty(G, ns, dtype=torch.int32), dst_idx=torch.empty(G, max(r, 1), dtype=torch.int32),
+               dst_cnt=torch.empty(G, nd, dtype=torch.int32), row_of_token=torch.empty(G, L, dtype=torch.int32),
+               key_bias=torch.empty(G, L - r))
+    lib().oracle_tome_match(_p(metric.contiguous()), G, N, C, _p(a_idx), _p(b_idx), ns, nd, r, text_len,
+                            _p(out["node_idx"]), _p(out["node_max"]), _p(out["edge"]), _p(out["dst_idx"]),
+                            _p(out["dst_cnt"]), _p(out["row_of_token"]), _p(out["key_bias"]))
+    out["dst_idx"] = out["dst_idx"][:, :r]
+    return out
+
+
+def tome_merge(x, maps, a_idx, b_idx, r: int, text_len: int, heads_per_group: int) -> torch.Tensor:
+    B, H, L, D = x.shape
+    x = x.contiguous()
+    N = L - text_len
+    out = torch.empty(B, H, L - r, D, dtype=torch.bfloat16)
+    dst = maps["dst_idx"].contiguous() if r > 0 else torch.zeros(1, 1, dtype=torch.int32)
+    lib().oracle_tome_merge(_p(x.view(torch.int16)), x.stride(0), x.stride(1), x.stride(2), B, H, heads_per_group, N,
+                            text_len, _p(a_idx), _p(b_idx), a_idx.numel(), b_idx.numel(), r, _p(maps["edge"]),
+                            _p(dst), _p(out.view(torch.int16)))
+    return out
+
+
+def tome_unmerge(xm, maps, heads_per_group: int) -> torch.Tensor:
+    B, H, Lm, D = xm.shape
+    rot = maps["row_of_token"].long()
+    g = torch.arange(B * H) // heads_per_group
+    idx = rot[g].reshape(B, H, -1)
+    return torch.gather(xm, 2, idx[..., None].expand(B, H, idx.shape[-1], D))
+
+
+def tome_argmax(metric, a_subset, b_idx):
+    """(node_idx, node_max) [G, len(a_subset)] for a subset of the srcs."""
+    G, N, C = metric.shape
+    n = a_subset.numel()
+    idx = torch.empty(G, n, dtype=torch.int32)
+    mx = torch.empty(G, n)
+    lib().oracle_tome_argmax(_p(metric.contiguous()), G, N, C, _p(a_subset.contiguous()), n, _p(b_idx), b_idx.numel(),
+                             _p(idx), _p(mx))
+    return idx, mx
+
+
+def tome_maps(node_max, node_idx, N, a_idx, b_idx, r: int, text_len: int):
+    """Maps from given node_max/node_idx [G, n_src] (same dict as tome_match)."""
+    G = node_max.shape[0]
+    ns, nd = a_idx.numel(), b_idx.numel()
+    L = text_len + N
+    out = dict(node_idx=node_idx.contiguous(), node_max=node_max.contiguous(),
+               edge=torch.empty(G, ns, dtype=torch.int32), dst_idx=torch.empty(G, max(r, 1), dtype=torch.int32),
+               dst_cnt=torch.empty(G, nd, dtype=torch.int32), row_of_token=torch.empty(G, L, dtype=torch.int32),
+               key_bias=torch.empty(G, L - r))
+    lib().oracle_tome_maps(_p(out["node_max"]), _p(out["node_idx"]), G, N, _p(a_idx), _p(b_idx), ns, nd, r, text_len,
+                           _p(out["edge"]), _p(out["dst_idx"]), _p(out["dst_cnt"]), _p(out["row_of_token"]),
+                           _p(out["key_bias"]))
+    out["dst_idx"] = out["dst_idx"][:, :r]
     return out

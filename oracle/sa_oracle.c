@@ -138,3 +138,208 @@ void oracle_local_window(int L, int block, int text_len, int T, int Hp, int Wp, 
     }
   }
 }
+
+/* ---------------------------------------------------------------------------------------
+ * Token merging (utils/merge_unmerge.py:34-156, MergeAttention.py:21-49).
+ */
+
+/*
+ * Partition (merge_unmerge.py:62-92): build the {-1 = dst, 0 = src} buffer over frames
+ * 1..T-1 cell by cell (one dst per (st, sy, sx) cell at offset choice[cell], 0 = top-left),
+ * then a stable argsort puts dst before src; the first frame is prepended to dst.
+ */
+void oracle_tome_partition(int T, int Hp, int Wp, int sx, int sy, int st, const int32_t* choice, int32_t* a_idx,
+                           int32_t* b_idx, int* n_src, int* n_dst) {
+  const int frame = Hp * Wp, t1 = T - 1;
+  const int hsy = Hp / sy, wsx = Wp / sx, tst = t1 / st;
+  const int n = t1 * frame;
+  int* buf = (int*)calloc((size_t)(n > 0 ? n : 1), sizeof(int));
+  int cellno = 0;
+  for (int a = 0; a < tst; ++a)
+    for (int b = 0; b < hsy; ++b)
+      for (int c = 0; c < wsx; ++c, ++cellno) {
+        const int o = choice ? choice[cellno] : 0;
+        const int ot = o / (sy * sx), oy = (o / sx) % sy, ox = o % sx;
+        buf[((a * st + ot) * Hp + (b * sy + oy)) * Wp + (c * sx + ox)] = -1;
+      }
+  int nb = 0, na = 0;
+  for (int i = 0; i < frame; ++i) b_idx[nb++] = i;
+  for (int v = -1; v <= 0; ++v)          /* stable argsort of a {-1, 0} array */
+    for (int i = 0; i < n; ++i)
+      if (buf[i] == v) {
+        if (v < 0) b_idx[nb++] = frame + i;
+        else a_idx[na++] = frame + i;
+      }
+  *n_src = na;
+  *n_dst = nb;
+  free(buf);
+}
+
+/* Metric: mode 0 head-sum of k per batch ([B][N][64]); mode 1 per head (k,|k|,v,|v|). */
+void oracle_tome_metric(const uint16_t* k, const uint16_t* v, int64_t sb, int64_t sh, int64_t sl, int B, int H,
+                        int L, int text_len, int mode, float* out) {
+  const int N = L - text_len, D = 64;
+  if (mode == 0) {
+    for (int b = 0; b < B; ++b)
+      for (int n = 0; n < N; ++n) {
+        float m[64];
+        for (int d = 0; d < D; ++d) m[d] = 0.0f;
+        for (int h = 0; h < H; ++h)
+          for (int d = 0; d < D; ++d) m[d] = m[d] + bf16_to_f32(k[b * sb + h * sh + (int64_t)(text_len + n) * sl + d]);
+        float ss = 0.0f;
+        for (int d = 0; d < D; ++d) ss = fmaf(m[d], m[d], ss);
+        const float nrm = sqrtf(ss);
+        for (int d = 0; d < D; ++d) out[((int64_t)b * N + n) * D + d] = m[d] / nrm;
+      }
+  } else {
+    const int C = 2 * D + 2;
+    for (int b = 0; b < B; ++b)
+      for (int h = 0; h < H; ++h)
+        for (int n = 0; n < N; ++n) {
+          float ch[130];
+          const int64_t base = b * sb + h * sh + (int64_t)(text_len + n) * sl;
+          for (int d = 0; d < D; ++d) ch[d] = bf16_to_f32(k[base + d]);
+          for (int d = 0; d < D; ++d) ch[D + 1 + d] = bf16_to_f32(v[base + d]);
+          float kq = 0.0f, vq = 0.0f;
+          for (int d = 0; d < D; ++d) kq = fmaf(ch[d], ch[d], kq);
+          for (int d = 0; d < D; ++d) vq = fmaf(ch[D + 1 + d], ch[D + 1 + d], vq);
+          ch[D] = sqrtf(kq);
+          ch[2 * D + 1] = sqrtf(vq);
+          float ss = 0.0f;
+          for (int c = 0; c < C; ++c) ss = fmaf(ch[c], ch[c], ss);
+          const float nrm = sqrtf(ss);
+          float* o = out + (((int64_t)b * H + h) * N + n) * C;
+          for (int c = 0; c < C; ++c) o[c] = ch[c] / nrm;
+        }
+  }
+}
+
+static float oracle_round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* Best dst of each src (merge_unmerge.py:102, :108): fmaf-chain scores, scan over dst in
+ * order, first maximum wins. a_idx may be any subset of the srcs. */
+void oracle_tome_argmax(const float* metric, int G, int N, int C, const int32_t* a_idx, int n_a,
+                        const int32_t* b_idx, int n_dst, int32_t* node_idx, float* node_max) {
+  for (int g = 0; g < G; ++g) {
+    const float* mg = metric + (int64_t)g * N * C;
+    for (int s = 0; s < n_a; ++s) {
+      float best = -INFINITY;
+      int bi = 0;
+      for (int d = 0; d < n_dst; ++d) {
+        float acc = 0.0f;
+        for (int c = 0; c < C; ++c) acc = fmaf(mg[(int64_t)a_idx[s] * C + c], mg[(int64_t)b_idx[d] * C + c], acc);
+        if (acc > best) {
+          best = acc;
+          bi = d;
+        }
+      }
+      node_max[(int64_t)g * n_a + s] = best;
+      node_idx[(int64_t)g * n_a + s] = bi;
+    }
+  }
+}
+
+/* Maps from node_max/node_idx (merge_unmerge.py:109-116, MergeAttention.py:163-167): edge
+ * order = stable sort of node_max descending, dst_idx, dst counts, the unmerge map and the
+ * bf16 log-size key bias. */
+void oracle_tome_maps(const float* node_max, const int32_t* node_idx, int G, int N, const int32_t* a_idx,
+                      const int32_t* b_idx, int n_src, int n_dst, int r, int text_len, int32_t* edge,
+                      int32_t* dst_idx, int32_t* dst_cnt, int32_t* row_of_token, float* key_bias) {
+  const int L = text_len + N, Lm = L - r, U = n_src - r;
+  oracle_key* keys = (oracle_key*)malloc(sizeof(oracle_key) * (size_t)(n_src > 0 ? n_src : 1));
+  for (int g = 0; g < G; ++g) {
+    for (int s = 0; s < n_src; ++s) {
+      keys[s].ord = order_bits(node_max[(int64_t)g * n_src + s]);
+      keys[s].idx = s;
+    }
+    qsort(keys, (size_t)n_src, sizeof(oracle_key), cmp_key);
+    int32_t* cnt = dst_cnt + (int64_t)g * n_dst;
+    int32_t* rot = row_of_token + (int64_t)g * L;
+    for (int d = 0; d < n_dst; ++d) cnt[d] = 0;
+    for (int t = 0; t < text_len; ++t) rot[t] = t;
+    for (int e = 0; e < n_src; ++e) {
+      const int s = keys[e].idx;
+      edge[(int64_t)g * n_src + e] = s;
+      if (e < r) {
+        const int d = node_idx[(int64_t)g * n_src + s];
+        dst_idx[(int64_t)g * r + e] = d;
+        cnt[d] += 1;
+        rot[text_len + a_idx[s]] = text_len + U + d;
+      } else {
+        rot[text_len + a_idx[s]] = text_len + (e - r);
+      }
+    }
+    for (int d = 0; d < n_dst; ++d) rot[text_len + b_idx[d]] = text_len + U + d;
+    for (int j = 0; j < Lm; ++j) {
+      const int d = j - text_len - U;
+      key_bias[(int64_t)g * Lm + j] = d >= 0 ? oracle_round_bf16(logf(oracle_round_bf16((float)(1 + cnt[d])))) : 0.0f;
+    }
+  }
+  free(keys);
+}
+
+/* Matching and maps for each group (merge_unmerge.py:99-116): argmax then maps. */
+void oracle_tome_match(const float* metric, int G, int N, int C, const int32_t* a_idx, const int32_t* b_idx,
+                       int n_src, int n_dst, int r, int text_len, int32_t* node_idx, float* node_max, int32_t* edge,
+                       int32_t* dst_idx, int32_t* dst_cnt, int32_t* row_of_token, float* key_bias) {
+  oracle_tome_argmax(metric, G, N, C, a_idx, n_src, b_idx, n_dst, node_idx, node_max);
+  oracle_tome_maps(node_max, node_idx, G, N, a_idx, b_idx, n_src, n_dst, r, text_len, edge, dst_idx, dst_cnt,
+                   row_of_token, key_bias);
+}
+
+/* merge of one [B,H,L,64] bf16 tensor (merge_unmerge.py:119-128): fp32 sum of the dst then
+ * its srcs in edge order, divided by the count, rounded to bf16. out [B,H,Lm,64]. */
+void oracle_tome_merge(const uint16_t* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int heads_per_group,
+                       int N, int text_len, const int32_t* a_idx, const int32_t* b_idx, int n_src, int n_dst, int r,
+                       const int32_t* edge, const int32_t* dst_idx, uint16_t* out) {
+  const int L = text_len + N, Lm = L - r, U = n_src - r, D = 64;
+  const int G = B * H / heads_per_group;
+  /* members of each dst in edge order: stable counting sort of the edges by dst */
+  int32_t* ptr = (int32_t*)calloc((size_t)G * (n_dst + 1), sizeof(int32_t));
+  int32_t* mem = (int32_t*)malloc(sizeof(int32_t) * (size_t)G * (r > 0 ? r : 1));
+  for (int g = 0; g < G; ++g) {
+    int32_t* pg = ptr + (int64_t)g * (n_dst + 1);
+    for (int e = 0; e < r; ++e) pg[dst_idx[(int64_t)g * r + e] + 1] += 1;
+    for (int d = 0; d < n_dst; ++d) pg[d + 1] += pg[d];
+    int32_t* cur = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n_dst > 0 ? n_dst : 1));
+    memcpy(cur, pg, sizeof(int32_t) * (size_t)n_dst);
+    for (int e = 0; e < r; ++e) mem[(int64_t)g * r + cur[dst_idx[(int64_t)g * r + e]]++] = e;
+    free(cur);
+  }
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      const int g = (b * H + h) / heads_per_group;
+      const uint16_t* xb = x + b * sb + h * sh;
+      uint16_t* ob = out + ((int64_t)b * H + h) * Lm * D;
+      for (int j = 0; j < Lm; ++j) {
+        if (j < text_len + U) {
+          const int tok = j < text_len ? j : text_len + a_idx[edge[(int64_t)g * n_src + r + (j - text_len)]];
+          memcpy(ob + (int64_t)j * D, xb + (int64_t)tok * sl, D * sizeof(uint16_t));
+          continue;
+        }
+        const int d = j - text_len - U;
+        float s[64];
+        int n = 1;
+        for (int c = 0; c < D; ++c) s[c] = bf16_to_f32(xb[(int64_t)(text_len + b_idx[d]) * sl + c]);
+        for (int p = ptr[(int64_t)g * (n_dst + 1) + d]; p < ptr[(int64_t)g * (n_dst + 1) + d + 1]; ++p) {
+          const int tok = text_len + a_idx[edge[(int64_t)g * n_src + mem[(int64_t)g * r + p]]];
+          for (int c = 0; c < D; ++c) s[c] = s[c] + bf16_to_f32(xb[(int64_t)tok * sl + c]);
+          ++n;
+        }
+        for (int c = 0; c < D; ++c) {
+          float val = n > 1 ? oracle_round_bf16(s[c] / (float)n) : s[c];
+          uint32_t u;
+          memcpy(&u, &val, 4);
+          ob[(int64_t)j * D + c] = (uint16_t)(u >> 16);
+        }
+      }
+    }
+  free(ptr);
+  free(mem);
+}

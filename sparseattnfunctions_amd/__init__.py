@@ -16,6 +16,10 @@ __all__ = ["install_alias"]
 _SUBMODULES = (
     "utils",
     "utils.block_sparse_attn_kernel",
+    "utils.merge_unmerge",
+    "block_mask_attn",
+    "combined_attn",
+    "MergeAttention",
 )
 
 

@@ -39,6 +39,13 @@ _PROTOTYPES = {
     ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
     "sa_local_window_bitmap": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "sa_tome_partition": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "sa_tome_metric": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "sa_tome_normalize": (_I, [_P, ctypes.c_int64, _I, _P, _P]),
+    "sa_tome_match_workspace": (_I, [_I, _I, _I, _I64P]),
+    "sa_tome_match": (_I, [_P, _I, _P, _P, ctypes.c_int64, _P]),
+    "sa_tome_merge": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _I64P, _P]),
+    "sa_tome_unmerge": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _I64P, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -1,0 +1,648 @@
+// Token merging (ToMe bipartite soft matching) for video tokens on gfx950.
+//
+// Replaces bipartite_soft_matching_video and its merge / unmerge closures
+// (special_attentions/utils/merge_unmerge.py:34-156) as used by MergeAttention
+// (MergeAttention.py:21-49):
+//   partition  first frame all dst; later frames one dst per (st, sy, sx) cell, the rest src
+//              (:62-92), dst|src order = stable argsort of the {-1, 0} buffer (:82);
+//   metric     cosine-normalised matching metric (:100);
+//   match      scores = a @ b^T, node_max/node_idx = max over dst (:102, :108), fused so the
+//              [n_src, n_dst] score matrix is never materialised;
+//   edges      edge order = argsort(node_max, descending) (:109), src_idx = first r,
+//              unm_idx = the rest, dst_idx = node_idx[src_idx] (:110-112), sizes (:113-116);
+//   merge      [text | unm | dst] with dst = mean(dst, merged srcs) (scatter_reduce mean,
+//              include_self, :119-135);
+//   unmerge    every token reads its merged row (:137-154).
+//
+// Determinism contract (built with -ffp-contract=off, matched by oracle/sa_oracle.c):
+//   metric: head sums in head order / dot products as fmaf chains in channel order, norm
+//   = sqrtf(fmaf chain of squares), value / norm (IEEE); scores: fmaf chain over channels;
+//   argmax ties -> lowest dst position; edge order: node_max descending (total order on fp32
+//   bits) then src position ascending (a stable sort; torch's argsort order is unspecified);
+//   merged dst value: fp32 sum of the dst token then its srcs in edge order, divided by the
+//   count, rounded to bf16. Integer counters use atomics (order-independent).
+#include <math.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "sa_common.h"
+
+namespace {
+
+constexpr int kD = 64;           // head dim handled here
+constexpr int kMaxC = 2 * kD + 2;  // channels of the per-head (k, |k|, v, |v|) metric
+constexpr int kTileS = 64;       // src rows per match workgroup
+constexpr int kTileD = 64;       // dst columns per staged tile
+constexpr int kRankTile = 1024;  // keys staged per rank step
+
+__device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ inline uint32_t order_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Round-to-nearest-even fp32 -> bf16 -> fp32 (finite inputs).
+__device__ inline float round_bf16(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t r = u + 0x7fffu + ((u >> 16) & 1u);
+  return __uint_as_float(r & 0xffff0000u);
+}
+
+__device__ inline void add_row(float* acc, const uint16_t* row) {
+#pragma unroll
+  for (int c8 = 0; c8 < kD / 8; ++c8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(row + 8 * c8);
+    acc[8 * c8 + 0] += bf16lo(w.x); acc[8 * c8 + 1] += bf16hi(w.x);
+    acc[8 * c8 + 2] += bf16lo(w.y); acc[8 * c8 + 3] += bf16hi(w.y);
+    acc[8 * c8 + 4] += bf16lo(w.z); acc[8 * c8 + 5] += bf16hi(w.z);
+    acc[8 * c8 + 6] += bf16lo(w.w); acc[8 * c8 + 7] += bf16hi(w.w);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Metric. Mode 0: per batch, sum over heads of k (the head mean up to the factor 1/H, which
+// the normalisation removes) -> [B][N][64]. Mode 1: per head, (k, |k|, v, |v|) as in
+// MergeAttention.py:26-31 -> [B*H][N][130]. One thread per output row.
+struct MetricArgs {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
+  int B, H, N, text_len, mode;
+  float* out;
+};
+
+__global__ __launch_bounds__(256) void metric_kernel(MetricArgs a) {
+  const int64_t rows = a.mode == 0 ? (int64_t)a.B * a.N : (int64_t)a.B * a.H * a.N;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows) return;
+  if (a.mode == 0) {
+    const int64_t b = i / a.N;
+    const int n = (int)(i - b * a.N);
+    float m[kD];
+#pragma unroll
+    for (int d = 0; d < kD; ++d) m[d] = 0.f;
+    for (int h = 0; h < a.H; ++h) add_row(m, a.k + b * a.k_sb + h * a.k_sh + (int64_t)(a.text_len + n) * a.k_sl);
+    float ss = 0.f;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) ss = fmaf(m[d], m[d], ss);
+    const float nrm = sqrtf(ss);
+    float* o = a.out + i * kD;
+#pragma unroll
+    for (int d = 0; d < kD; d += 4) *reinterpret_cast<float4*>(o + d) = make_float4(m[d] / nrm, m[d + 1] / nrm, m[d + 2] / nrm, m[d + 3] / nrm);
+  } else {
+    const int64_t bh = i / a.N;
+    const int n = (int)(i - bh * a.N);
+    const int64_t b = bh / a.H, h = bh - b * a.H;
+    float kk[kD], vv[kD];
+#pragma unroll
+    for (int d = 0; d < kD; ++d) kk[d] = vv[d] = 0.f;
+    add_row(kk, a.k + b * a.k_sb + h * a.k_sh + (int64_t)(a.text_len + n) * a.k_sl);
+    add_row(vv, a.v + b * a.v_sb + h * a.v_sh + (int64_t)(a.text_len + n) * a.v_sl);
+    float kq = 0.f, vq = 0.f;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) kq = fmaf(kk[d], kk[d], kq);
+#pragma unroll
+    for (int d = 0; d < kD; ++d) vq = fmaf(vv[d], vv[d], vq);
+    const float kn = sqrtf(kq), vn = sqrtf(vq);
+    float ss = 0.f;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) ss = fmaf(kk[d], kk[d], ss);
+    ss = fmaf(kn, kn, ss);
+#pragma unroll
+    for (int d = 0; d < kD; ++d) ss = fmaf(vv[d], vv[d], ss);
+    ss = fmaf(vn, vn, ss);
+    const float nrm = sqrtf(ss);
+    float* o = a.out + i * kMaxC;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) o[d] = kk[d] / nrm;
+    o[kD] = kn / nrm;
+#pragma unroll
+    for (int d = 0; d < kD; ++d) o[kD + 1 + d] = vv[d] / nrm;
+    o[2 * kD + 1] = vn / nrm;
+  }
+}
+
+// Row normalisation of a caller-supplied metric [rows][C]: x / sqrtf(fmaf chain of x^2).
+__global__ __launch_bounds__(256) void normalize_kernel(const float* in, int64_t rows, int C, float* out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows) return;
+  const float* x = in + i * C;
+  float ss = 0.f;
+  for (int c = 0; c < C; ++c) ss = fmaf(x[c], x[c], ss);
+  const float nrm = sqrtf(ss);
+  for (int c = 0; c < C; ++c) out[i * C + c] = x[c] / nrm;
+}
+
+// ---------------------------------------------------------------------------------------
+// Match: for each src, the dst of largest score (fmaf chain over channels) in this
+// workgroup's dst range; ties -> lowest dst position. Workgroup = 64 src x dst range,
+// thread (ty, tx) owns src rows 4ty..4ty+3 and dst columns 4tx..4tx+3 of each staged tile.
+struct MatchArgs {
+  const float* metric;  // [G][N][C]
+  int G, N, C;
+  const int32_t* a_idx;
+  const int32_t* b_idx;
+  int n_src, n_dst;
+  int splits, dst_per_split;
+  float* part_max;  // [G][splits][n_src]
+  int32_t* part_idx;
+};
+
+__device__ inline bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
+  extern __shared__ float sm[];
+  const int C = a.C;
+  const int stride = C + 1;  // odd stride: 64 rows read at one channel hit distinct banks
+  float* As = sm;
+  float* Bs = sm + kTileS * stride;
+  const int g = blockIdx.y, split = blockIdx.z;
+  const int s0 = blockIdx.x * kTileS;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const float* mg = a.metric + (int64_t)g * a.N * C;
+  for (int e = tid; e < kTileS * C; e += 256) {
+    const int r = e / C, c = e - r * C;
+    const int s = s0 + r;
+    As[r * stride + c] = s < a.n_src ? mg[(int64_t)a.a_idx[s] * C + c] : 0.f;
+  }
+  float best[4];
+  int bidx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    best[i] = -INFINITY;
+    bidx[i] = 0;
+  }
+  const int d_lo = split * a.dst_per_split;
+  const int d_hi = min(a.n_dst, d_lo + a.dst_per_split);
+  for (int d0 = d_lo; d0 < d_hi; d0 += kTileD) {
+    __syncthreads();
+    for (int e = tid; e < kTileD * C; e += 256) {
+      const int r = e / C, c = e - r * C;
+      const int d = d0 + r;
+      Bs[r * stride + c] = d < d_hi ? mg[(int64_t)a.b_idx[d] * C + c] : 0.f;
+    }
+    __syncthreads();
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int c = 0; c < C; ++c) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[(4 * ty + i) * stride + c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[(4 * tx + j) * stride + c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = d0 + 4 * tx + j;
+      if (d < d_hi) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (better(acc[i][j], d, best[i], bidx[i])) {
+            best[i] = acc[i][j];
+            bidx[i] = d;
+          }
+        }
+      }
+    }
+  }
+  // Reduce over the 16 tx lanes sharing ty (a 16-lane DPP row group of the wave).
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ov = __shfl_xor(best[i], off, 16);
+      const int oi = __shfl_xor(bidx[i], off, 16);
+      if (better(ov, oi, best[i], bidx[i])) {
+        best[i] = ov;
+        bidx[i] = oi;
+      }
+    }
+  }
+  if (tx == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int s = s0 + 4 * ty + i;
+      if (s < a.n_src) {
+        const int64_t o = ((int64_t)g * a.splits + split) * a.n_src + s;
+        a.part_max[o] = best[i];
+        a.part_idx[o] = bidx[i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Map construction kernels (one thread per element).
+struct MapArgs {
+  sa_tome_maps m;
+  const float* part_max;
+  const int32_t* part_idx;
+  int splits;
+};
+
+// Combine dst splits in ascending order (ties keep the lower split = lower dst) and zero
+// the counters of the later passes.
+__global__ void combine_kernel(MapArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const sa_tome_maps& m = a.m;
+  if (i < (int64_t)m.G * m.n_src) {
+    const int64_t g = i / m.n_src, s = i - g * m.n_src;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int k = 0; k < a.splits; ++k) {
+      const int64_t o = (g * a.splits + k) * m.n_src + s;
+      if (better(a.part_max[o], a.part_idx[o], bv, bi)) {
+        bv = a.part_max[o];
+        bi = a.part_idx[o];
+      }
+    }
+    m.node_max[i] = bv;
+    m.node_idx[i] = bi;
+    m.rank[i] = 0;
+  }
+  if (i < (int64_t)m.G * m.n_dst) {
+    m.dst_cnt[i] = 0;
+    m.dst_cursor[i] = 0;
+  }
+}
+
+// rank[s] = #{s' : node_max[s'] ranks before node_max[s]} (descending value, then position).
+__global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, int splits) {
+  __shared__ uint32_t keys[kRankTile];
+  const int g = blockIdx.y;
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const float* nm = m.node_max + (int64_t)g * m.n_src;
+  const uint32_t mine = s < m.n_src ? order_bits(nm[s]) : 0u;
+  const int per = (m.n_src + splits - 1) / splits;
+  const int j_lo = blockIdx.z * per, j_hi = min(m.n_src, j_lo + per);
+  int count = 0;
+  for (int t0 = j_lo; t0 < j_hi; t0 += kRankTile) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kRankTile; e += 256) keys[e] = t0 + e < j_hi ? order_bits(nm[t0 + e]) : 0u;
+    __syncthreads();
+    const int n = min(kRankTile, j_hi - t0);
+    for (int e = 0; e < n; ++e) {
+      const uint32_t o = keys[e];
+      count += (o > mine) || (o == mine && t0 + e < s);
+    }
+  }
+  if (s < m.n_src && count) atomicAdd(&m.rank[(int64_t)g * m.n_src + s], count);
+}
+
+// edge[g][rank[s]] = s.
+__global__ void edge_kernel(sa_tome_maps m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)m.G * m.n_src) return;
+  const int64_t g = i / m.n_src;
+  m.edge[g * m.n_src + m.rank[i]] = (int32_t)(i - g * m.n_src);
+}
+
+// dst_idx, dst counts and the unmerge map for every token.
+__global__ void assign_kernel(sa_tome_maps m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)m.G * m.L) return;
+  const int64_t g = i / m.L;
+  const int t = (int)(i - g * m.L);
+  const int T = m.text_len, U = m.n_src - m.r;
+  int32_t* rot = m.row_of_token + g * m.L;
+  if (t < T) {
+    rot[t] = t;
+  } else if (t < T + m.n_src) {  // edge position e = t - T
+    const int e = t - T;
+    const int s = m.edge[g * m.n_src + e];
+    const int tok = T + m.a_idx[s];
+    if (e < m.r) {
+      const int d = m.node_idx[g * m.n_src + s];
+      m.dst_idx[g * m.r + e] = d;
+      atomicAdd(&m.dst_cnt[g * m.n_dst + d], 1);
+      rot[tok] = T + U + d;
+    } else {
+      rot[tok] = T + (e - m.r);
+    }
+  } else if (t < T + m.n_src + m.n_dst) {
+    const int d = t - T - m.n_src;
+    rot[T + m.b_idx[d]] = T + U + d;
+  }
+}
+
+// Per group: exclusive scan of dst counts -> dst_ptr; key bias of every merged row.
+__global__ __launch_bounds__(1024) void scan_kernel(sa_tome_maps m) {
+  __shared__ int32_t part[1024];
+  const int g = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = m.n_dst;
+  const int per = (n + 1023) / 1024;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  const int32_t* cnt = m.dst_cnt + (int64_t)g * n;
+  int sum = 0;
+  for (int d = lo; d < hi; ++d) sum += cnt[d];
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = tid > 0 ? part[tid - 1] : 0;
+  int32_t* ptr = m.dst_ptr + (int64_t)g * (n + 1);
+  for (int d = lo; d < hi; ++d) {
+    ptr[d] = run;
+    run += cnt[d];
+  }
+  if (tid == 1023) ptr[n] = part[1023];
+  // Proportional-attention bias log(size) rounded to bf16 (MergeAttention.py:163-167).
+  const int T = m.text_len, U = m.n_src - m.r;
+  float* kb = m.key_bias + (int64_t)g * m.Lm;
+  for (int j = tid; j < m.Lm; j += 1024) {
+    const int d = j - T - U;
+    kb[j] = d >= 0 ? round_bf16(logf(round_bf16((float)(1 + cnt[d])))) : 0.f;
+  }
+}
+
+__global__ void fill_kernel(sa_tome_maps m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)m.G * m.r) return;
+  const int64_t g = i / m.r;
+  const int e = (int)(i - g * m.r);
+  const int d = m.dst_idx[i];
+  const int p = atomicAdd(&m.dst_cursor[g * m.n_dst + d], 1);
+  m.members[g * m.r + m.dst_ptr[g * (m.n_dst + 1) + d] + p] = e;
+}
+
+// Members of each dst in ascending edge order (insertion sort of its short segment).
+__global__ void sort_kernel(sa_tome_maps m) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)m.G * m.n_dst) return;
+  const int64_t g = i / m.n_dst;
+  const int d = (int)(i - g * m.n_dst);
+  const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1);
+  int32_t* mem = m.members + g * m.r;
+  const int lo = ptr[d], hi = ptr[d + 1];
+  for (int x = lo + 1; x < hi; ++x) {
+    const int v = mem[x];
+    int y = x - 1;
+    while (y >= lo && mem[y] > v) {
+      mem[y + 1] = mem[y];
+      --y;
+    }
+    mem[y + 1] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Merge: out[b, h, j] = mean of the tokens of merged row j. 8 lanes per row (16 B each).
+struct MergeArgs {
+  sa_tome_maps m;
+  const uint16_t* x;
+  int64_t x_sb, x_sh, x_sl;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_sl;
+  int B, H, heads_per_group;
+};
+
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const sa_tome_maps& m = a.m;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+  const int c8 = threadIdx.x & 7;
+  if (row >= (int64_t)a.B * a.H * m.Lm) return;
+  const int64_t bh = row / m.Lm;
+  const int j = (int)(row - bh * m.Lm);
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int64_t g = bh / a.heads_per_group;
+  const int T = m.text_len, U = m.n_src - m.r;
+  const uint16_t* xb = a.x + b * a.x_sb + h * a.x_sh + 8 * c8;
+  uint4 res;
+  if (j < T + U) {
+    const int tok = j < T ? j : T + m.a_idx[m.edge[g * m.n_src + m.r + (j - T)]];
+    res = *reinterpret_cast<const uint4*>(xb + (int64_t)tok * a.x_sl);
+  } else {
+    const int d = j - T - U;
+    const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1);
+    const int lo = ptr[d], hi = ptr[d + 1];
+    const uint4 w0 = *reinterpret_cast<const uint4*>(xb + (int64_t)(T + m.b_idx[d]) * a.x_sl);
+    if (lo == hi) {
+      res = w0;
+    } else {
+      float s[8] = {bf16lo(w0.x), bf16hi(w0.x), bf16lo(w0.y), bf16hi(w0.y),
+                    bf16lo(w0.z), bf16hi(w0.z), bf16lo(w0.w), bf16hi(w0.w)};
+      for (int p = lo; p < hi; ++p) {
+        const int e = m.members[g * m.r + p];
+        const int tok = T + m.a_idx[m.edge[g * m.n_src + e]];
+        const uint4 w = *reinterpret_cast<const uint4*>(xb + (int64_t)tok * a.x_sl);
+        s[0] += bf16lo(w.x); s[1] += bf16hi(w.x); s[2] += bf16lo(w.y); s[3] += bf16hi(w.y);
+        s[4] += bf16lo(w.z); s[5] += bf16hi(w.z); s[6] += bf16lo(w.w); s[7] += bf16hi(w.w);
+      }
+      const float n = (float)(1 + hi - lo);
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo16 = __float_as_uint(round_bf16(s[2 * q] / n)) >> 16;
+        const uint32_t hi16 = __float_as_uint(round_bf16(s[2 * q + 1] / n)) & 0xffff0000u;
+        o[q] = lo16 | hi16;
+      }
+      res = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  *reinterpret_cast<uint4*>(a.out + b * a.o_sb + h * a.o_sh + (int64_t)j * a.o_sl + 8 * c8) = res;
+}
+
+// Unmerge: out[b, h, t] = xm[b, h, row_of_token[t]].
+__global__ __launch_bounds__(256) void unmerge_kernel(MergeArgs a) {
+  const sa_tome_maps& m = a.m;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+  const int c8 = threadIdx.x & 7;
+  if (row >= (int64_t)a.B * a.H * m.L) return;
+  const int64_t bh = row / m.L;
+  const int t = (int)(row - bh * m.L);
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int64_t g = bh / a.heads_per_group;
+  const int src_row = m.row_of_token[g * m.L + t];
+  const uint4 w = *reinterpret_cast<const uint4*>(a.x + b * a.x_sb + h * a.x_sh + (int64_t)src_row * a.x_sl + 8 * c8);
+  *reinterpret_cast<uint4*>(a.out + b * a.o_sb + h * a.o_sh + (int64_t)t * a.o_sl + 8 * c8) = w;
+}
+
+int check_maps(const sa_tome_maps* m, const char* fn) {
+  SA_REQUIRE(m, "%s: null maps", fn);
+  SA_REQUIRE(m->G > 0 && m->N > 0 && m->text_len >= 0 && m->n_src >= 0 && m->n_dst > 0 &&
+                 m->n_src + m->n_dst == m->N && m->r >= 0 && m->r <= m->n_src && m->L == m->text_len + m->N &&
+                 m->Lm == m->L - m->r,
+             "%s: inconsistent map sizes", fn);
+  SA_REQUIRE(m->a_idx && m->b_idx && m->node_idx && m->node_max && m->rank && m->edge && m->dst_cnt &&
+                 m->dst_cursor && m->dst_ptr && m->row_of_token && m->key_bias && (m->r == 0 || (m->dst_idx && m->members)),
+             "%s: null map buffer", fn);
+  return SA_OK;
+}
+
+inline unsigned grid256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+extern "C" int sa_tome_partition(int T, int Hp, int Wp, int sx, int sy, int st, const int32_t* cell_choice,
+                                 int32_t* a_idx, int32_t* b_idx, int* n_src, int* n_dst) {
+  SA_REQUIRE(n_src && n_dst, "sa_tome_partition: null count pointers");
+  SA_REQUIRE(T >= 1 && Hp > 0 && Wp > 0 && sx > 0 && sy > 0 && st > 0, "sa_tome_partition: bad geometry");
+  const int frame = Hp * Wp;
+  const int t1 = T - 1;  // frames after the first
+  const int hs = Hp / sy, ws = Wp / sx, ts = t1 / st;
+  const int cell = st * sy * sx;
+  // buffer over frames 1..T-1: 1 = dst, 0 = src (merge_unmerge.py:71-79).
+  std::vector<uint8_t> is_dst((size_t)t1 * frame, 0);
+  for (int ct = 0; ct < ts; ++ct)
+    for (int ch = 0; ch < hs; ++ch)
+      for (int cw = 0; cw < ws; ++cw) {
+        const int idx = cell_choice ? cell_choice[((int64_t)ct * hs + ch) * ws + cw] : 0;
+        SA_REQUIRE(idx >= 0 && idx < cell, "sa_tome_partition: cell_choice %d outside [0, %d)", idx, cell);
+        const int dt = idx / (sy * sx), dy = (idx / sx) % sy, dx = idx % sx;
+        is_dst[((size_t)(ct * st + dt) * Hp + (ch * sy + dy)) * Wp + (cw * sx + dx)] = 1;
+      }
+  int nd = frame, ns = 0;
+  for (size_t i = 0; i < is_dst.size(); ++i) (is_dst[i] ? nd : ns) += 1;
+  *n_src = ns;
+  *n_dst = nd;
+  if (!a_idx && !b_idx) return sa::ok();
+  SA_REQUIRE(a_idx && b_idx, "sa_tome_partition: need both a_idx and b_idx");
+  int pb = 0, pa = 0;
+  for (int t = 0; t < frame; ++t) b_idx[pb++] = t;  // first frame: all dst (:83, :91)
+  for (size_t i = 0; i < is_dst.size(); ++i)          // stable dst|src split (:82)
+    if (is_dst[i]) b_idx[pb++] = frame + (int)i;
+  for (size_t i = 0; i < is_dst.size(); ++i)
+    if (!is_dst[i]) a_idx[pa++] = frame + (int)i;
+  return sa::ok();
+}
+
+extern "C" int sa_tome_metric(const uint16_t* k, const int64_t k_strides[3], const uint16_t* v,
+                              const int64_t v_strides[3], int B, int H, int L, int D, int text_len, int mode,
+                              float* metric, void* stream) {
+  SA_REQUIRE(k && k_strides && metric, "sa_tome_metric: null pointer");
+  SA_REQUIRE(mode == 0 || mode == 1, "sa_tome_metric: mode must be 0 (head-sum k) or 1 (per-head k,|k|,v,|v|)");
+  SA_REQUIRE(mode == 0 || (v && v_strides), "sa_tome_metric: mode 1 needs v");
+  SA_REQUIRE(B > 0 && H > 0 && L > text_len && text_len >= 0, "sa_tome_metric: bad shape");
+  if (D != kD) return sa::fail(SA_ERR_UNSUPPORTED, "sa_tome_metric: head_dim %d (only 64)", D);
+  const uint16_t* ps[2] = {k, v};
+  const int64_t* ss[2] = {k_strides, v_strides};
+  for (int t = 0; t < (mode == 1 ? 2 : 1); ++t) {
+    if (reinterpret_cast<uintptr_t>(ps[t]) % 16) return sa::fail(SA_ERR_UNSUPPORTED, "sa_tome_metric: base not 16-byte aligned");
+    for (int i = 0; i < 3; ++i)
+      if (ss[t][i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "sa_tome_metric: strides must be multiples of 8");
+  }
+  MetricArgs a;
+  a.k = k; a.v = v;
+  a.k_sb = k_strides[0]; a.k_sh = k_strides[1]; a.k_sl = k_strides[2];
+  a.v_sb = v ? v_strides[0] : 0; a.v_sh = v ? v_strides[1] : 0; a.v_sl = v ? v_strides[2] : 0;
+  a.B = B; a.H = H; a.N = L - text_len; a.text_len = text_len; a.mode = mode; a.out = metric;
+  const int64_t rows = mode == 0 ? (int64_t)B * a.N : (int64_t)B * H * a.N;
+  hipLaunchKernelGGL(metric_kernel, dim3(grid256(rows)), dim3(256), 0, sa::as_stream(stream), a);
+  return sa::check_launch("sa_tome_metric");
+}
+
+extern "C" int sa_tome_normalize(const float* metric, int64_t rows, int C, float* out, void* stream) {
+  SA_REQUIRE(metric && out && rows > 0 && C > 0, "sa_tome_normalize: bad arguments");
+  hipLaunchKernelGGL(normalize_kernel, dim3(grid256(rows)), dim3(256), 0, sa::as_stream(stream), metric, rows, C, out);
+  return sa::check_launch("sa_tome_normalize");
+}
+
+extern "C" int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes) {
+  SA_REQUIRE(bytes && G > 0 && n_src >= 0 && n_dst > 0, "sa_tome_match_workspace: bad arguments");
+  const int splits = std::max(1, std::min(16, n_dst / 256));
+  *bytes = (int64_t)G * splits * std::max(n_src, 1) * 8;
+  return sa::ok();
+}
+
+extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspace, int64_t ws_bytes,
+                             void* stream) {
+  int rc = check_maps(maps, "sa_tome_match");
+  if (rc) return rc;
+  SA_REQUIRE(metric && workspace, "sa_tome_match: null metric/workspace");
+  SA_REQUIRE(C > 0 && C <= kMaxC, "sa_tome_match: C=%d outside [1, %d]", C, kMaxC);
+  const sa_tome_maps& m = *maps;
+  int64_t need = 0;
+  sa_tome_match_workspace(m.G, m.n_src, m.n_dst, &need);
+  SA_REQUIRE(ws_bytes >= need, "sa_tome_match: workspace %lld < %lld bytes", (long long)ws_bytes, (long long)need);
+  hipStream_t s = sa::as_stream(stream);
+  const int splits = std::max(1, std::min(16, m.n_dst / 256));
+  float* part_max = reinterpret_cast<float*>(workspace);
+  int32_t* part_idx = reinterpret_cast<int32_t*>(part_max + (int64_t)m.G * splits * std::max(m.n_src, 1));
+  if (m.n_src > 0) {
+    MatchArgs a;
+    a.metric = metric; a.G = m.G; a.N = m.N; a.C = C; a.a_idx = m.a_idx; a.b_idx = m.b_idx;
+    a.n_src = m.n_src; a.n_dst = m.n_dst; a.splits = splits;
+    a.dst_per_split = (m.n_dst + splits - 1) / splits;
+    a.part_max = part_max; a.part_idx = part_idx;
+    const size_t lds = (size_t)(kTileS + kTileD) * (C + 1) * sizeof(float);
+    if (lds > 65536) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(match_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return sa::fail(SA_ERR_HIP, "sa_tome_match: LDS attribute: %s", hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kTileS - 1) / kTileS, m.G, splits), dim3(256), lds, s, a);
+    if ((rc = sa::check_launch("sa_tome_match/match"))) return rc;
+  }
+  MapArgs ma;
+  ma.m = m; ma.part_max = part_max; ma.part_idx = part_idx; ma.splits = splits;
+  const int64_t n0 = (int64_t)m.G * std::max(m.n_src, m.n_dst);
+  hipLaunchKernelGGL(combine_kernel, dim3(grid256(n0)), dim3(256), 0, s, ma);
+  if (m.n_src > 0) {
+    const int rsplit = std::max(1, std::min(16, m.n_src / 1024));
+    hipLaunchKernelGGL(rank_kernel, dim3((m.n_src + 255) / 256, m.G, rsplit), dim3(256), 0, s, m, rsplit);
+    hipLaunchKernelGGL(edge_kernel, dim3(grid256((int64_t)m.G * m.n_src)), dim3(256), 0, s, m);
+  }
+  hipLaunchKernelGGL(assign_kernel, dim3(grid256((int64_t)m.G * m.L)), dim3(256), 0, s, m);
+  hipLaunchKernelGGL(scan_kernel, dim3(m.G), dim3(1024), 0, s, m);
+  if (m.r > 0) {
+    hipLaunchKernelGGL(fill_kernel, dim3(grid256((int64_t)m.G * m.r)), dim3(256), 0, s, m);
+    hipLaunchKernelGGL(sort_kernel, dim3(grid256((int64_t)m.G * m.n_dst)), dim3(256), 0, s, m);
+  }
+  return sa::check_launch("sa_tome_match");
+}
+
+namespace {
+int launch_merge(bool unmerge, const uint16_t* x, const int64_t xs[3], int B, int H, int D, int heads_per_group,
+                 const sa_tome_maps* maps, uint16_t* out, const int64_t os[3], void* stream) {
+  const char* fn = unmerge ? "sa_tome_unmerge" : "sa_tome_merge";
+  int rc = check_maps(maps, fn);
+  if (rc) return rc;
+  SA_REQUIRE(x && xs && out && os, "%s: null pointer", fn);
+  SA_REQUIRE(B > 0 && H > 0 && heads_per_group > 0 && H % heads_per_group == 0, "%s: bad B/H/heads_per_group", fn);
+  SA_REQUIRE((int64_t)B * H / heads_per_group == maps->G, "%s: B*H/heads_per_group != maps->G", fn);
+  if (D != kD) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (only 64)", fn, D);
+  const void* ptrs[2] = {x, out};
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) % 16) return sa::fail(SA_ERR_UNSUPPORTED, "%s: base not 16-byte aligned", fn);
+  for (int i = 0; i < 3; ++i)
+    if (xs[i] % 8 || os[i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "%s: strides must be multiples of 8", fn);
+  MergeArgs a;
+  a.m = *maps; a.x = x; a.x_sb = xs[0]; a.x_sh = xs[1]; a.x_sl = xs[2];
+  a.out = out; a.o_sb = os[0]; a.o_sh = os[1]; a.o_sl = os[2];
+  a.B = B; a.H = H; a.heads_per_group = heads_per_group;
+  const int64_t rows = (int64_t)B * H * (unmerge ? maps->L : maps->Lm);
+  hipStream_t s = sa::as_stream(stream);
+  if (unmerge)
+    hipLaunchKernelGGL(unmerge_kernel, dim3(grid256(rows * 8)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(merge_kernel, dim3(grid256(rows * 8)), dim3(256), 0, s, a);
+  return sa::check_launch(fn);
+}
+}  // namespace
+
+extern "C" int sa_tome_merge(const uint16_t* x, const int64_t x_strides[3], int B, int H, int D, int heads_per_group,
+                             const sa_tome_maps* maps, uint16_t* out, const int64_t out_strides[3], void* stream) {
+  return launch_merge(false, x, x_strides, B, H, D, heads_per_group, maps, out, out_strides, stream);
+}
+
+extern "C" int sa_tome_unmerge(const uint16_t* xm, const int64_t xm_strides[3], int B, int H, int D,
+                               int heads_per_group, const sa_tome_maps* maps, uint16_t* out,
+                               const int64_t out_strides[3], void* stream) {
+  return launch_merge(true, xm, xm_strides, B, H, D, heads_per_group, maps, out, out_strides, stream);
+}

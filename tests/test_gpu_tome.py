@@ -1,0 +1,157 @@
+"""GPU parity of token merging: metric, matching maps, merge and unmerge bit-exact against
+the C oracle; MergeAttention outputs within the bf16 tolerances of the fp64 oracle."""
+import math
+
+import pytest
+import torch
+
+from conftest import case
+from oracle import native
+from oracle.attention import masked_attention
+from sparseattnfunctions_amd import _tome
+from sparseattnfunctions_amd.MergeAttention import REFERENCE_MERGE_CONFIG, MergeAttention
+from sparseattnfunctions_amd.utils import merge_unmerge
+from sparseattnfunctions_amd.workloads import Geometry, cogvideox_qkv
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, want):
+    err = (got.float().cpu().double() - want).abs()
+    assert torch.isfinite(got.float()).all()
+    assert err.max().item() <= 2e-2, err.max().item()
+    assert err.mean().item() <= 2e-3, err.mean().item()
+
+
+def _maps_equal(maps, want, fields=("node_idx", "node_max", "edge", "dst_idx", "dst_cnt", "row_of_token", "key_bias")):
+    for f in fields:
+        got = getattr(maps, f).cpu()
+        if f in ("node_idx", "node_max", "edge"):
+            got = got[:, : maps.n_src]
+        if f == "dst_idx":
+            got = got[:, : maps.r]
+        assert torch.equal(got, want[f]), f
+
+
+def _check_members(maps):
+    # CSR members: for each dst, its merged srcs in ascending edge order.
+    ptr, mem, dst = maps.dst_ptr.cpu(), maps.members.cpu(), maps.dst_idx.cpu()
+    for g in range(maps.G):
+        assert torch.equal(ptr[g, 1:] - ptr[g, :-1], maps.dst_cnt.cpu()[g])
+        for d in range(0, maps.n_dst, max(1, maps.n_dst // 50)):
+            seg = mem[g, ptr[g, d]:ptr[g, d + 1]]
+            want = (dst[g, : maps.r] == d).nonzero().flatten().int()
+            assert torch.equal(seg, want)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_small_pipeline_bit_exact(dev, mode):
+    case(f"tome small mode={mode}")
+    geom = Geometry(text_len=226, T=4, Hp=6, Wp=10)
+    q, k, v = cogvideox_qkv(5, B=2, H=3, geom=geom)
+    metric = _tome.metric_from_qkv(k.to(dev), v.to(dev), geom.text_len, mode)
+    om = native.tome_metric(k, v, geom.text_len, mode)
+    assert torch.equal(metric.cpu(), om)
+    a, b = _tome.partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1, dev)
+    oa, ob = native.tome_partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1)
+    for r in (0, 37, oa.numel()):
+        maps = _tome.match(metric, a, b, r, geom.text_len)
+        want = native.tome_match(om, oa, ob, r, geom.text_len)
+        _maps_equal(maps, want)
+        _check_members(maps)
+        hpg = 3 if mode == 0 else 1
+        for x in (q, k, v):
+            xm = _tome.merge(x.to(dev), maps, hpg)
+            assert torch.equal(xm.cpu(), native.tome_merge(x, want, oa, ob, r, geom.text_len, hpg))
+            assert torch.equal(_tome.unmerge(xm, maps, hpg).cpu(), native.tome_unmerge(xm.cpu(), want, hpg))
+
+
+def test_config4_maps_bit_exact(dev):
+    case("tome config 4 full shape maps")
+    q, k, v = cogvideox_qkv(3)
+    metric = _tome.metric_from_qkv(k.to(dev), None, 226, 0)
+    om = native.tome_metric(k, None, 226, 0)
+    assert torch.equal(metric.cpu(), om)
+    a, b = _tome.partition(13, 30, 45, 2, 2, 1, dev)
+    assert (a.numel(), b.numel()) == (12240, 5310)
+    maps = _tome.match(metric, a, b, 4000, 226)
+    oa, ob = a.cpu(), b.cpu()
+    # argmax spot check on 256 srcs per group (each src's argmax is independent)
+    sub = torch.arange(0, 12240, 48, dtype=torch.int32)
+    idx, mx = native.tome_argmax(om, oa[sub.long()], ob)
+    assert torch.equal(maps.node_idx.cpu()[:, sub.long()], idx)
+    assert torch.equal(maps.node_max.cpu()[:, sub.long()], mx)
+    # every other map from the GPU's (spot-checked) node_max / node_idx
+    want = native.tome_maps(maps.node_max.cpu(), maps.node_idx.cpu(), 17550, oa, ob, 4000, 226)
+    _maps_equal(maps, want, ("edge", "dst_idx", "dst_cnt", "row_of_token", "key_bias"))
+    _check_members(maps)
+    assert maps.Lm == 13776 and int(maps.sizes.sum(1)[0]) == 5310 + 4000
+
+
+def test_merge_attention_config4(dev):
+    case("MergeAttention config 4 end to end")
+    q, k, v = cogvideox_qkv(3)
+    proc = MergeAttention()
+    out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    maps = proc.maps
+    want_maps = {f: getattr(maps, f).cpu() for f in ("edge", "row_of_token", "key_bias")}
+    want_maps["dst_idx"] = maps.dst_idx.cpu()[:, :4000]
+    a, b = maps.a_idx.cpu(), maps.b_idx.cpu()
+    heads = [(0, 0), (1, 21)]
+    for bb, hh in heads:
+        sel = lambda x: x[bb:bb + 1, hh:hh + 1]
+        sub = {f: t[bb:bb + 1] for f, t in want_maps.items()}
+        qm, km, vm = (native.tome_merge(sel(x), sub, a, b, 4000, 226, 1) for x in (q, k, v))
+        bias = sub["key_bias"].reshape(1, 1, -1).double()
+        om = masked_attention(qm, km, vm, torch.ones(1, 1, 1, 1, dtype=torch.bool).expand(1, 1, 216, 216),
+                              1 / 8, key_bias=bias)
+        want = native.tome_unmerge(om, sub, 1)[0, 0]
+        _check(out[bb, hh], want)
+
+
+def test_merge_attention_reference_setting(dev):
+    # The reference's own configuration: per-head (k,|k|,v,|v|) metric, 3x3x4 cells,
+    # k/v-only merge (MergeAttention.py:16-48), on a smaller grid.
+    case("MergeAttention per-head, k/v merge")
+    geom = Geometry(text_len=226, T=5, Hp=6, Wp=9)
+    q, k, v = cogvideox_qkv(6, B=2, H=2, geom=geom)
+    cfg = dict(REFERENCE_MERGE_CONFIG, w=9, h=6, t=5, r=60)
+    proc = MergeAttention(cfg, full_merge=False, metric="kv_norm")
+    out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    assert out.shape == q.shape
+    maps = proc.maps
+    a, b = maps.a_idx.cpu(), maps.b_idx.cpu()
+    want = native.tome_match(native.tome_metric(k, v, 226, 1), a, b, 60, 226)
+    _maps_equal(maps, want)
+    km = native.tome_merge(k, want, a, b, 60, 226, 1)
+    vm = native.tome_merge(v, want, a, b, 60, 226, 1)
+    Lm = km.shape[2]
+    bias = want["key_bias"].reshape(2, 2, Lm).double()
+    nb_q, nb_k = math.ceil(q.shape[2] / 64), math.ceil(Lm / 64)
+    ref = masked_attention(q, km, vm, torch.ones(1, 1, nb_q, nb_k, dtype=torch.bool), 1 / 8, key_bias=bias)
+    _check(out, ref)
+    # gap > 1 reuses the maps between re-matches
+    proc.gap = 2
+    proc(q.to(dev), k.to(dev), v.to(dev))
+    assert proc.maps is not maps or proc.calls % 2 == 0
+
+
+def test_reference_api_closures(dev):
+    case("bipartite_soft_matching_video API")
+    geom = Geometry(text_len=226, T=4, Hp=6, Wp=10)
+    q, k, v = cogvideox_qkv(7, B=1, H=2, geom=geom)
+    kd = k.to(dev)
+    metric = kd[:, :, 226:].reshape(2, geom.n_video, 64).float()
+    merge, unmerge = merge_unmerge.bipartite_soft_matching_video(metric, 10, 6, 4, 2, 2, 1, r=30, no_rand=True)
+    assert merge_unmerge.counter.shape == (2, merge.maps.n_dst, 1)
+    assert merge_unmerge.counter.dtype == torch.int64
+    xm = merge(kd)
+    assert xm.shape == (1, 2, geom.L - 30, 64)
+    back = unmerge(xm)
+    assert back.shape == kd.shape
+    assert torch.equal(merge(kd.reshape(2, geom.L, 64)), xm.reshape(2, geom.L - 30, 64))
+    ident = merge_unmerge.bipartite_soft_matching_video(metric, 10, 6, 4, 2, 2, 1, r=0)
+    assert ident[0] is merge_unmerge.do_nothing
+    g = torch.Generator(device="cpu").manual_seed(0)
+    m2, _ = merge_unmerge.bipartite_soft_matching_video(metric, 10, 6, 4, 2, 2, 1, r=30, generator=g)
+    assert m2.maps.n_dst == merge.maps.n_dst
