@@ -86,6 +86,82 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=4):
     }
 
 
+def _tflops(flops, ms):
+    return round(flops / (ms * 1e-3) / 1e12, 2)
+
+
+def other_configs(q, k, v, dev):
+    """The other BASELINE configurations, each timed with HIP events (reported, not `value`)."""
+    from sparseattnfunctions_amd import _tome
+    from sparseattnfunctions_amd.combined_attn import CombinedAttn
+    from sparseattnfunctions_amd.MergeAttention import MergeAttention
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention, block_sparse_triton_fn
+    from sparseattnfunctions_amd.workloads import COGVIDEOX_2B, cogvideox_qkv, config1_inputs
+
+    out = {}
+    B, H, L, D = q.shape
+
+    # C1: the reference's CPU-runnable case (B=1, H=2, L=2048, random block mask), in bf16.
+    q1, k1, v1, m1, s1 = config1_inputs()
+    q1, k1, v1, m1 = (t.to(dev) for t in (q1.bfloat16(), k1.bfloat16(), v1.bfloat16(), m1))
+    ms = time_fn(lambda: block_sparse_triton_fn(q1, k1, v1, m1, s1), iters=20)
+    from oracle.attention import flops_of_mask
+    out["c1"] = {"ms": round(ms, 4), "tflops": _tflops(flops_of_mask(m1.cpu(), 2048, 2048), ms),
+                 "block_density": round(m1.float().mean().item(), 4)}
+
+    # C3: combined mask (local window U global top-10% U text) + attention.
+    proc = CombinedAttn(warmup_epoch=0)
+    proc(q, k, v)
+    kv3 = proc.last_kv
+    f3 = 4 * D * kv3.computed_pairs(L, L)
+    ms3 = time_fn(lambda: proc(q, k, v), iters=10)
+    ms3_attn = time_fn(lambda: block_sparse_attention(q, k, v, kv3, 0.125, n_text_blocks=4), iters=10)
+    out["c3"] = {"ms": round(ms3, 4), "tflops": _tflops(f3, ms3), "attn_ms": round(ms3_attn, 4),
+                 "attn_tflops": _tflops(f3, ms3_attn), "sparsity": round(proc.sparsity(), 4),
+                 "effective_tflop_per_call": round(f3 / 1e12, 4)}
+
+    # C4: token merging (seed 3), r = 4000 -> 13776 tokens, biased dense attention, unmerge.
+    q4, k4, v4 = (t.to(dev) for t in cogvideox_qkv(3))
+    mp = MergeAttention()
+    mp(q4, k4, v4)
+    maps = mp.maps
+    Lm = maps.Lm
+    f4 = 4 * B * H * Lm * Lm * D
+    ms4 = time_fn(lambda: mp(q4, k4, v4), iters=10)
+    ms_match = time_fn(lambda: mp.build_maps(k4, v4), iters=10)
+    ms_merge = time_fn(lambda: [_tome.merge(x, maps, H) for x in (q4, k4, v4)], iters=10)
+    qm = _tome.merge(q4, maps, H)
+    ms_unmerge = time_fn(lambda: _tome.unmerge(qm, maps, H), iters=10)
+    row = D * 2
+    merge_bytes = 3 * (B * H * L * row + B * H * Lm * row)
+    unmerge_bytes = B * H * Lm * row + B * H * L * row
+    out["c4"] = {"ms": round(ms4, 4), "tflops": _tflops(f4, ms4), "merged_tokens": Lm,
+                 "match_ms": round(ms_match, 4), "merge_qkv_ms": round(ms_merge, 4),
+                 "merge_gbs": round(merge_bytes / (ms_merge * 1e-3) / 1e9, 1),
+                 "unmerge_ms": round(ms_unmerge, 4),
+                 "unmerge_gbs": round(unmerge_bytes / (ms_unmerge * 1e-3) / 1e9, 1),
+                 "attention_tflop_per_call": round(f4 / 1e12, 4)}
+    del q4, k4, v4, qm
+
+    # C5: one denoising step = 30 layers of config-3 attention, each with its own inputs
+    # (seed = layer index, drawn on the GPU generator).
+    layers = [cogvideox_qkv(i, device=str(dev)) for i in range(30)]
+    procs = [CombinedAttn(warmup_epoch=0) for _ in range(30)]
+    for p, (a, b_, c) in zip(procs, layers):
+        p(a, b_, c)
+    f5 = sum(4 * D * p.last_kv.computed_pairs(L, L) for p in procs)
+
+    def step():
+        for p, (a, b_, c) in zip(procs, layers):
+            p(a, b_, c)
+
+    ms5 = time_fn(step, iters=3, warmup=1)
+    out["c5"] = {"ms_per_step": round(ms5, 3), "tflops": _tflops(f5, ms5),
+                 "effective_tflop_per_step": round(f5 / 1e12, 3)}
+    del layers
+    return out
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -103,7 +179,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the dense comparators")
+    ap.add_argument("--no-extra", action="store_true", help="skip the dense comparators and other configs")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one plain 1 GiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (the hot path is single-GPU; see "
@@ -187,7 +265,16 @@ def main():
         "wall_ms_per_step": round(wall_ms, 4),
     }
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = src.numel() * src.element_size()
+        del src, dst
     if not args.no_extra:
+        result["other_configs"] = other_configs(q, k, v, dev)
         dense_sdpa_ms = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v), iters=5)
         dense_hip_ms = time_fn(lambda: proc.forward_dense(q, k, v), iters=3)
         result["dense"] = {

@@ -78,17 +78,19 @@ def position_code(geom: Geometry, d: int = 64) -> torch.Tensor:
 
 
 def cogvideox_qkv(seed: int, B: int = 2, H: int = 30, geom: Geometry = COGVIDEOX_2B, d: int = 64,
-                  amp: float = 2.0, heads: Tuple[int, int] = None) -> Tuple[torch.Tensor, ...]:
-    """q, k, v bf16 [B, H, L, d] on the CPU (configs 2-5).
+                  amp: float = 2.0, heads: Tuple[int, int] = None, device: str = "cpu") -> Tuple[torch.Tensor, ...]:
+    """q, k, v bf16 [B, H, L, d] (configs 2-5), drawn on the CPU generator by default.
 
     `heads=(h0, h1)` returns only heads h0..h1-1 of the same draw (all heads are drawn so
-    that the values do not depend on the slice)."""
-    g = torch.Generator(device="cpu").manual_seed(seed)
+    that the values do not depend on the slice). `device="cuda"` draws with that device's
+    generator instead (same distribution, different values; used where the CPU draw of many
+    layers would dominate the run time)."""
+    g = torch.Generator(device=device).manual_seed(seed)
     shape = (B, H, geom.L, d)
-    code = position_code(geom, d)
+    code = position_code(geom, d).to(device)
     out = []
     for i in range(3):
-        x = torch.randn(shape, generator=g, dtype=torch.float32)
+        x = torch.randn(shape, generator=g, dtype=torch.float32, device=device)
         if i < 2:
             x.add_(code, alpha=amp)
         if heads is not None:
