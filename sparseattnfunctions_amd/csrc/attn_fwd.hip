@@ -205,6 +205,8 @@ __device__ inline sa_bf16x8 p_operand(const uint32_t (&pk)[8], int u) {
 template <bool kBias>
 __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kWaves][kVtElems];
+  // Key bias of the current tile (log2 domain), staged with V: one load per lane.
+  __shared__ __attribute__((aligned(16))) float bias_lds[kBias ? kWaves : 1][kBlock];
 
   const int lane = threadIdx.x & 63;
   // Wave-uniform values are made provably uniform (readfirstlane) so that the list and
@@ -260,17 +262,27 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   int it = next_valid(0);
   uint4 kr[2][4];
   uint4 vr[2][4];
+  float bv = 0.f;  // bias of key `lane` of the prefetched tile (kBias only)
+  float* bl_lds = bias_lds[kBias ? wave : 0];
+  auto load_bias = [&](int key0) {
+    if (kBias) bv = bbase[min(key0 + lane, a.Lk - 1)] * kLog2e;
+  };
   int kb_cur = it < cnt ? list[it] : 0;
   if (it < cnt) {
     load_k(a, kbase, kb_cur * kBlock, col, hh, kr);
     load_v(a, vbase, kb_cur * kBlock, lane, vr);
+    load_bias(kb_cur * kBlock);
     store_vt(vt, lane, vr);
+    if (kBias) bl_lds[lane] = bv;
   }
   int it_next = next_valid(it + 1);
   // Prefetches are issued every iteration (past the end of the list they re-load the
   // current block) so the loop body has the same loads in flight on every path.
   int kb_next = it_next < cnt ? list[it_next] : kb_cur;
-  if (it < cnt) load_v(a, vbase, kb_next * kBlock, lane, vr);
+  if (it < cnt) {
+    load_v(a, vbase, kb_next * kBlock, lane, vr);
+    load_bias(kb_next * kBlock);
+  }
 
   while (it < cnt) {
     const int key0 = kb_cur * kBlock;
@@ -303,8 +315,11 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int key = key0 + 32 * c + 8 * q4 + 4 * hh;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bl[4 * q4 + j] = bbase[min(key + j, a.Lk - 1)] * kLog2e;
+          const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + (key - key0));
+          bl[4 * q4 + 0] = b4.x;
+          bl[4 * q4 + 1] = b4.y;
+          bl[4 * q4 + 2] = b4.z;
+          bl[4 * q4 + 3] = b4.w;
         }
       }
 
@@ -336,9 +351,11 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
     it = it_next;
     kb_cur = kb_next;
     store_vt(vt, lane, vr);
+    if (kBias) bl_lds[lane] = bv;
     it_next = next_valid(it + 1);
     kb_next = it_next < cnt ? list[it_next] : kb_cur;
     load_v(a, vbase, kb_next * kBlock, lane, vr);
+    load_bias(kb_next * kBlock);
   }
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
