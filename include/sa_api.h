@@ -84,6 +84,24 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         const int32_t* work_order, int64_t n_slots, void* stream);
 
 /*
+ * Block-sparse attention with token-level masks inside cut blocks: as sa_block_sparse_fwd,
+ * plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
+ * bitmask in tile_masks (uint64 [slots][64]: bit c of word r = query r of the block may
+ * attend key c). Replaces flex_attention with a BlockMask built from a mask_mod
+ * (SildingTileAttention.py:88-106, 146), which also masks element-wise inside partial blocks.
+ * lists_shared != 0: one set of lists (nqb rows) is used by every (b, h), as the
+ * reference's B=H=1 BlockMask broadcasts.
+ */
+int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                 const int64_t k_strides[3], const uint16_t* v,
+                                 const int64_t v_strides[3], uint16_t* out,
+                                 const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                                 const int32_t* kv_idx, const int32_t* kv_cnt, const int32_t* kv_slot,
+                                 int max_cnt, int lists_shared, const uint64_t* tile_masks,
+                                 float sm_scale, const int32_t* work_order, int64_t n_slots,
+                                 void* stream);
+
+/*
  * (host) Dispatch order of the attention work items (one per list row) for a GPU whose
  * workgroups are dealt round-robin to n_xcd XCDs (8 on MI355X): each XCD gets a
  * contiguous range of (b, h) heads, so their K/V stay in that XCD's L2, and within it the
@@ -140,6 +158,29 @@ int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const fl
  */
 int sa_local_window_bitmap(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh,
                            int dw, uint8_t* bitmap);
+
+/*
+ * (host) Tile-major token order of sliding-tile attention (SildingTileAttention.py:111-131):
+ * perm[j] = natural token at position j; text tokens stay first, video tokens are grouped
+ * "(nt tt nh th nw tw) -> (nt nh nw tt th tw)" for tile = {tt, th, tw} dividing (T, Hp, Wp).
+ */
+int sa_sta_permutation(int text_len, int T, int Hp, int Wp, const int tile[3], int32_t* perm);
+
+/*
+ * (host) The sliding-tile mask (sta_mask_3d, SildingTileAttention.py:18-87: video pairs
+ * within the kernel-sized window of tiles around the query tile, the centre clamped to the
+ * canvas; video->text; text->all), on the tile-major layout, as 64x64 block lists: kv_idx /
+ * kv_cnt / kv_slot [nb][nb] per query block (non-empty key blocks ascending; slot -1 for a
+ * full block) and the bitmasks of the partial blocks. kv_idx = NULL: count *n_slots only.
+ */
+int sa_sta_block_masks(int text_len, int T, int Hp, int Wp, const int tile[3], const int kernel[3],
+                       int32_t* kv_idx, int32_t* kv_cnt, int32_t* kv_slot, uint64_t* masks,
+                       int* n_slots);
+
+/* Token gather out[b,h,j] = x[b,h,idx[j]] for j < L_out (layout permutations). */
+int sa_gather_tokens(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L_in, int D,
+                     const int32_t* idx, int L_out, uint16_t* out, const int64_t out_strides[3],
+                     void* stream);
 
 /* ---- Token merging (ToMe bipartite soft matching) ----------------------------------- */
 

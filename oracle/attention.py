@@ -25,13 +25,15 @@ def expand_block_mask(block_mask: torch.Tensor, Lq: int, Lk: int, block: int = 6
 
 
 def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 64,
-                     dtype=torch.float64, row_chunk: int = 2048, heads=None):
+                     dtype=torch.float64, row_chunk: int = 2048, heads=None, token_mask=None):
     """Dense-masked attention on CPU tensors; returns [B, H, Lq, D] in `dtype`.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] (any float dtype; converted to `dtype`);
     block_mask broadcastable to [B, H, >=ceil(Lq/block), >=ceil(Lk/block)];
     key_bias broadcastable to [B, H, Lk] or None. `heads` optionally restricts the
     computation to a list of (b, h) pairs (the rest of the output stays zero).
+    `token_mask(rows)` optionally returns a bool [len(rows), Lk] token-level mask that is
+    intersected with the block mask (flex_attention's mask_mod semantics).
     """
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
@@ -55,6 +57,8 @@ def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 
                 s = s + bias[None, :]
             rows = torch.arange(r0, r1) // block
             allowed = bm[b, h][rows].repeat_interleave(block, dim=-1)[:, :Lk]
+            if token_mask is not None:
+                allowed = allowed & token_mask(torch.arange(r0, r1))
             s = s.masked_fill(~allowed, float("-inf"))
             empty = ~allowed.any(dim=-1)
             s[empty] = 0.0

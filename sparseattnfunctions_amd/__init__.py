@@ -20,6 +20,7 @@ _SUBMODULES = (
     "block_mask_attn",
     "combined_attn",
     "MergeAttention",
+    "SildingTileAttention",
 )
 
 

@@ -37,7 +37,15 @@ _PROTOTYPES = {
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,
          ctypes.c_int64, _P],
     ),
+    "sa_block_sparse_fwd_tilemask": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P,
+         ctypes.c_int64, _P],
+    ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
+    "sa_sta_permutation": (_I, [_I, _I, _I, _I, _P, _P]),
+    "sa_sta_block_masks": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "sa_gather_tokens": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _I64P, _P]),
     "sa_local_window_bitmap": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "sa_tome_partition": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "sa_tome_metric": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _P, _P]),

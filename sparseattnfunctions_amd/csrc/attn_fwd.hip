@@ -65,6 +65,9 @@ struct FwdArgs {
   const float* bias;
   int64_t bias_sb, bias_sh;
   float scale_log2;  // sm_scale * log2(e)
+  int list_bh_stride;          // list row = bh * list_bh_stride + qb (0: lists shared by heads)
+  const int32_t* kv_slot;      // [rows][max_cnt] tile-mask slot of each entry, -1 = full tile
+  const uint64_t* tile_masks;  // [slots][64] bit k of row r: query r may attend key k
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
@@ -202,7 +205,7 @@ __device__ inline sa_bf16x8 p_operand(const uint32_t (&pk)[8], int u) {
   return as_bf16x8(make_uint4(pk[4 * u], pk[4 * u + 1], pk[4 * u + 2], pk[4 * u + 3]));
 }
 
-template <bool kBias>
+template <bool kBias, bool kMask>
 __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kWaves][kVtElems];
   // Key bias of the current tile (log2 domain), staged with V: one load per lane.
@@ -225,9 +228,11 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   const int h = bh - b * a.H;
   uint16_t* vt = vt_lds[wave];
 
-  int cnt = a.kv_cnt[item];
+  const int64_t list_row = (int64_t)bh * a.list_bh_stride + qb;
+  int cnt = a.kv_cnt[list_row];
   cnt = cnt < 0 ? 0 : (cnt > a.max_cnt ? a.max_cnt : cnt);
-  const int32_t* list = a.kv_idx + (int64_t)item * a.max_cnt;
+  const int32_t* list = a.kv_idx + list_row * a.max_cnt;
+  const int32_t* slots = kMask ? a.kv_slot + list_row * a.max_cnt : nullptr;
 
   const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kbase = a.k + b * a.k_sb + h * a.k_sh;
@@ -267,13 +272,28 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   auto load_bias = [&](int key0) {
     if (kBias) bv = bbase[min(key0 + lane, a.Lk - 1)] * kLog2e;
   };
+  // Tile masks (kMask only): rows 32g + col of the current / prefetched tile's mask.
+  uint64_t mw_cur[2] = {~0ull, ~0ull}, mw_next[2] = {~0ull, ~0ull};
+  int slot_cur = -1, slot_next = -1;
+  auto load_mask = [&](int it_) {
+    if (kMask) {
+      slot_next = it_ < cnt ? slots[it_] : -1;
+      const uint64_t* mrow = a.tile_masks + (int64_t)max(slot_next, 0) * kBlock;
+      mw_next[0] = mrow[col];
+      mw_next[1] = mrow[32 + col];
+    }
+  };
   int kb_cur = it < cnt ? list[it] : 0;
   if (it < cnt) {
     load_k(a, kbase, kb_cur * kBlock, col, hh, kr);
     load_v(a, vbase, kb_cur * kBlock, lane, vr);
     load_bias(kb_cur * kBlock);
+    load_mask(it);
     store_vt(vt, lane, vr);
     if (kBias) bl_lds[lane] = bv;
+    slot_cur = slot_next;
+    mw_cur[0] = mw_next[0];
+    mw_cur[1] = mw_next[1];
   }
   int it_next = next_valid(it + 1);
   // Prefetches are issued every iteration (past the end of the list they re-load the
@@ -282,6 +302,7 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   if (it < cnt) {
     load_v(a, vbase, kb_next * kBlock, lane, vr);
     load_bias(kb_next * kBlock);
+    load_mask(it_next);
   }
 
   while (it < cnt) {
@@ -307,6 +328,17 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
           if (key >= nvalid) {
             s[0][i] = -INFINITY;
             s[1][i] = -INFINITY;
+          }
+        }
+      }
+      if (kMask && slot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const uint32_t half = (uint32_t)(mw_cur[g] >> (32 * c));
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = 8 * (i >> 2) + 4 * hh + (i & 3);
+            if (!((half >> key) & 1u)) s[g][i] = -INFINITY;
           }
         }
       }
@@ -352,10 +384,14 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
     kb_cur = kb_next;
     store_vt(vt, lane, vr);
     if (kBias) bl_lds[lane] = bv;
+    slot_cur = slot_next;
+    mw_cur[0] = mw_next[0];
+    mw_cur[1] = mw_next[1];
     it_next = next_valid(it + 1);
     kb_next = it_next < cnt ? list[it_next] : kb_cur;
     load_v(a, vbase, kb_next * kBlock, lane, vr);
     load_bias(kb_next * kBlock);
+    load_mask(it_next);
   }
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
@@ -418,25 +454,27 @@ extern "C" int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int 
   return sa::ok();
 }
 
-extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
-                                   const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
-                                   uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
-                                   int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
-                                   const float* key_bias, const int64_t bias_strides[2], float sm_scale,
-                                   const int32_t* work_order, int64_t n_slots, void* stream) {
+namespace {
+
+int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
+               const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B,
+               int H, int Lq, int Lk, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+               bool lists_shared, const int32_t* kv_slot, const uint64_t* tile_masks, const float* key_bias,
+               const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
+               void* stream, const char* fn) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
-             "sa_block_sparse_fwd: null pointer");
-  SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "sa_block_sparse_fwd: bad shape B=%d H=%d Lq=%d Lk=%d", B, H, Lq, Lk);
-  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd: head_dim %d (only 64)", D);
-  SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f, "sa_block_sparse_fwd: sm_scale must be finite and > 0");
+             "%s: null pointer", fn);
+  SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
+  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (only 64)", fn, D);
+  SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f, "%s: sm_scale must be finite and > 0", fn);
   const int nqb = sa::cdiv(Lq, kBlock);
   const int nkb = sa::cdiv(Lk, kBlock);
-  SA_REQUIRE(max_cnt > 0, "sa_block_sparse_fwd: max_cnt must be > 0");
-  SA_REQUIRE(!key_bias || bias_strides, "sa_block_sparse_fwd: key_bias without bias_strides");
+  SA_REQUIRE(max_cnt > 0, "%s: max_cnt must be > 0", fn);
+  SA_REQUIRE(!key_bias || bias_strides, "%s: key_bias without bias_strides", fn);
   const int64_t n_items = (int64_t)B * H * nqb;
-  SA_REQUIRE(n_items < (1LL << 30), "sa_block_sparse_fwd: too many query blocks");
+  SA_REQUIRE(n_items < (1LL << 30), "%s: too many query blocks", fn);
   if (work_order) {
-    SA_REQUIRE(n_slots > 0 && n_slots % kWaves == 0, "sa_block_sparse_fwd: n_slots must be a positive multiple of 4");
+    SA_REQUIRE(n_slots > 0 && n_slots % kWaves == 0, "%s: n_slots must be a positive multiple of 4", fn);
   } else {
     n_slots = (n_items + kWaves - 1) / kWaves * kWaves;
   }
@@ -444,17 +482,16 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   const void* ptrs[4] = {q, k, v, out};
   for (const void* p : ptrs) {
     if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
-      return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd: tensor base not 16-byte aligned");
+      return sa::fail(SA_ERR_UNSUPPORTED, "%s: tensor base not 16-byte aligned", fn);
   }
   const int64_t* strides[4] = {q_strides, k_strides, v_strides, out_strides};
   for (const int64_t* s : strides) {
     for (int i = 0; i < 3; ++i) {
-      if (s[i] % 8 != 0)
-        return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd: strides must be multiples of 8 elements");
+      if (s[i] % 8 != 0) return sa::fail(SA_ERR_UNSUPPORTED, "%s: strides must be multiples of 8 elements", fn);
     }
   }
   const int64_t grid = n_slots / kWaves;
-  SA_REQUIRE(grid < (1LL << 31), "sa_block_sparse_fwd: grid too large");
+  SA_REQUIRE(grid < (1LL << 31), "%s: grid too large", fn);
 
   FwdArgs a;
   a.q = q; a.k = k; a.v = v; a.o = out;
@@ -471,12 +508,45 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   a.bias_sb = key_bias ? bias_strides[0] : 0;
   a.bias_sh = key_bias ? bias_strides[1] : 0;
   a.scale_log2 = sm_scale * kLog2e;
+  a.list_bh_stride = lists_shared ? 0 : nqb;
+  a.kv_slot = kv_slot;
+  a.tile_masks = tile_masks;
 
   hipStream_t s = sa::as_stream(stream);
-  if (key_bias) {
-    hipLaunchKernelGGL(bsa_fwd_kernel<true>, dim3((unsigned)grid), dim3(64 * kWaves), 0, s, a);
+  const dim3 g((unsigned)grid), blk(64 * kWaves);
+  if (kv_slot) {
+    if (key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
+    hipLaunchKernelGGL((bsa_fwd_kernel<false, true>), g, blk, 0, s, a);
+  } else if (key_bias) {
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, false>), g, blk, 0, s, a);
   } else {
-    hipLaunchKernelGGL(bsa_fwd_kernel<false>, dim3((unsigned)grid), dim3(64 * kWaves), 0, s, a);
+    hipLaunchKernelGGL((bsa_fwd_kernel<false, false>), g, blk, 0, s, a);
   }
-  return sa::check_launch("sa_block_sparse_fwd");
+  return sa::check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                   const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                   uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                   int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                   const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                   const int32_t* work_order, int64_t n_slots, void* stream) {
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, stream,
+                    "sa_block_sparse_fwd");
+}
+
+extern "C" int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                            const int64_t k_strides[3], const uint16_t* v,
+                                            const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3],
+                                            int B, int H, int Lq, int Lk, int D, const int32_t* kv_idx,
+                                            const int32_t* kv_cnt, const int32_t* kv_slot, int max_cnt,
+                                            int lists_shared, const uint64_t* tile_masks, float sm_scale,
+                                            const int32_t* work_order, int64_t n_slots, void* stream) {
+  SA_REQUIRE(kv_slot && tile_masks, "sa_block_sparse_fwd_tilemask: null kv_slot/tile_masks");
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, lists_shared != 0, kv_slot, tile_masks, nullptr, nullptr, sm_scale, work_order, n_slots,
+                    stream, "sa_block_sparse_fwd_tilemask");
 }
