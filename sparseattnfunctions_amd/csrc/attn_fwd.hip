@@ -9,18 +9,27 @@
 // softmax runs in the exp2 domain with log2(e) folded into the scale; an empty row writes 0.
 //
 // Work decomposition. One wave64 owns one (b, h, 64-row query block) work item; a
-// workgroup holds 4 independent waves (no workgroup barriers). Per 64-key tile a wave
-// computes S^T = K Q^T and O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 (2 query groups of
-// 32 rows x 2 key chunks x 4 d-steps, then 2 d-chunks x 2 query groups x 4 key-steps:
-// 32 MFMAs = 1 MFLOP). Each lane holds one query column of S^T, so row statistics need
-// one cross-half exchange. K is loaded from global memory straight into MFMA A-operand
-// registers; V is loaded coalesced and written transposed into a wave-private LDS tile,
-// read back as V^T A-operands. The loads of tile i+1 are issued while tile i is computed.
+// workgroup holds 4 independent waves (no workgroup barriers) and two workgroups share a
+// CU (2 waves per SIMD). Per 64-key tile a wave computes S^T = K Q^T and O^T = V^T P^T
+// with v_mfma_f32_32x32x16_bf16 (16 + 16 MFMAs = 1 MFLOP); each lane holds one query
+// column of S^T, so row statistics need one cross-half exchange.
 //
-// Softmax economy (VALU is the co-bottleneck at d = 64): the running max is only raised
-// when a tile exceeds it by more than kRescaleLog2 (then p <= 2^kRescaleLog2), so the
-// accumulator rescale is rare; row sums accumulate the bf16-rounded P pairs with
-// v_dot2c_f32_bf16; maxima use v_max3_f32.
+// Data movement. An MFMA operand load straight from global memory puts a different row in
+// every lane, so each 1 KB load costs the address unit ~64 cache-line lookups; that, not
+// bandwidth, bounded the previous design. Here each K and V tile (64 rows x 128 B) is copied
+// by 8 coalesced buffer_load ... lds instructions each (8 lanes per 128-byte row) into a
+// wave-private LDS buffer with a 16-byte-chunk XOR swizzle, then read as operands: K with
+// ds_read_b128, V^T with the transposing ds_read_b64_tr_b16 (V stays [key][d] in memory).
+// The swizzle makes both read patterns bank-conflict free. One K and one V buffer per wave:
+// the next tile's K is requested as soon as this tile's K operands are in registers, the
+// next V as soon as the V operands are, so each copy has a full tile of compute to land.
+// Rows past Lk read as zero (the buffer descriptor's size ends at the last row).
+//
+// Softmax economy: the running max is only raised when a tile exceeds it by more than
+// kRescaleLog2 (then p <= 2^kRescaleLog2), so the accumulator rescale is rare; row sums
+// accumulate the bf16-rounded P pairs with v_dot2c_f32_bf16; maxima use v_max3_f32. The
+// MFMA blocks run at raised wave priority so that the two waves of a SIMD tend to overlap
+// one's MFMAs with the other's softmax.
 //
 // Scheduling: a host-built work order maps dispatch slots to items so that each XCD
 // (workgroups round-robin over 8 XCDs) processes a contiguous range of heads, longest
@@ -28,6 +37,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <vector>
 
@@ -38,13 +48,14 @@ namespace {
 constexpr int kBlock = 64;       // query rows per block == keys per key block
 constexpr int kHeadDim = 64;     // head dimension handled by this kernel
 constexpr int kWaves = 4;        // independent waves per workgroup
-constexpr int kVtStride = 68;    // LDS row stride (bf16) of the V^T tile: 32 rows hit 64 banks once
-constexpr int kVtElems = kHeadDim * kVtStride;
+constexpr int kTileBytes = kBlock * kHeadDim * 2;  // one K or V tile: 64 rows x 128 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
-#ifndef SA_ATTN_MIN_WAVES
-#define SA_ATTN_MIN_WAVES 2
-#endif
+constexpr int kMfmaPrio = 3;
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef short sa_i16x4v __attribute__((ext_vector_type(4)));
+typedef unsigned sa_u32x4v __attribute__((ext_vector_type(4)));
 
 struct FwdArgs {
   const uint16_t* q;
@@ -64,6 +75,7 @@ struct FwdArgs {
   int max_cnt;
   const float* bias;
   int64_t bias_sb, bias_sh;
+  float sm_scale;
   float scale_log2;  // sm_scale * log2(e)
   int list_bh_stride;          // list row = bh * list_bh_stride + qb (0: lists shared by heads)
   const int32_t* kv_slot;      // [rows][max_cnt] tile-mask slot of each entry, -1 = full tile
@@ -71,22 +83,13 @@ struct FwdArgs {
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
+__device__ inline sa_bf16x8 as_bf16x8(sa_u32x4v x) { return __builtin_bit_cast(sa_bf16x8, x); }
 
 __device__ inline sa_f32x16 mfma32(sa_bf16x8 a, sa_bf16x8 b, sa_f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ inline uint32_t word(const uint4& x, int j) {
-  return j == 0 ? x.x : (j == 1 ? x.y : (j == 2 ? x.z : x.w));
-}
-
-// Byte select: {lo16(a), lo16(b)} (kHi = false) or {hi16(a), hi16(b)} (kHi = true).
-template <bool kHi>
-__device__ inline uint32_t pack_halves(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, kHi ? 0x07060302u : 0x05040100u);
-}
 
 typedef __bf16 sa_bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -101,120 +104,67 @@ __device__ inline float dot2_bf16_ones(uint32_t pair, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(sa_bf16x2, pair), ones, acc, false);
 }
 
-// All loads below are unconditional with row indices clamped into [0, L): a per-lane
-// condition would become an exec-masked branch, and the compiler then cannot count the
-// loads in flight and waits for all of them (s_waitcnt vmcnt(0)) before any use. Rows
-// clamped past Lk belong to keys whose scores are masked to -inf (their V rows meet p = 0;
-// clamped data is finite), and clamped Q rows past Lq are never stored.
-
-// K tile as MFMA A operands: kr[c][s] = K[key0 + 32c + col][16s + 8hh .. +7].
-__device__ inline void load_k(const FwdArgs& a, const uint16_t* kbase, int key0, int col, int hh,
-                              uint4 (&kr)[2][4]) {
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int key = min(key0 + 32 * c + col, a.Lk - 1);
-    const uint16_t* p = kbase + (int64_t)key * a.k_sl + 8 * hh;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) kr[c][s] = *reinterpret_cast<const uint4*>(p + 16 * s);
-  }
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap: no LDS traffic).
+__device__ inline float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// V tile rows for the transposed LDS write: vr[p][e] = V[key0 + 4kq + e][8(dg + 4p) .. +7].
-__device__ inline void load_v(const FwdArgs& a, const uint16_t* vbase, int key0, int lane,
-                              uint4 (&vr)[2][4]) {
-  const int kq = lane & 15, dg = lane >> 4;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int key = min(key0 + 4 * kq + e, a.Lk - 1);
-    const uint16_t* p = vbase + (int64_t)key * a.v_sl + 8 * dg;
-#pragma unroll
-    for (int p2 = 0; p2 < 2; ++p2) vr[p2][e] = *reinterpret_cast<const uint4*>(p + 32 * p2);
-  }
+// 16-byte chunk swizzle of LDS tile row r (depends on r mod 16). Chunk c of row r is stored
+// at chunk c ^ swz(r). With 64 or 32 LDS banks it makes conflict-free (a) the K operand
+// reads, 16 lanes reading 16 consecutive rows at one chunk, and (b) the transposed V reads,
+// 32 lanes reading 4 consecutive rows x 4 chunks.
+__device__ inline int swz(int r) {
+  const int j = (r >> 1) & 7;
+  return (((j & 1) << 2) | (j >> 1)) ^ ((r & 1) << 1);
 }
 
-__device__ inline void store_vt(uint16_t* vt, int lane, const uint4 (&vr)[2][4]) {
-  const int kq = lane & 15, dg = lane >> 4;
-#pragma unroll
-  for (int p2 = 0; p2 < 2; ++p2) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t w0 = word(vr[p2][0], j), w1 = word(vr[p2][1], j);
-      const uint32_t w2 = word(vr[p2][2], j), w3 = word(vr[p2][3], j);
-      const int d = 8 * (dg + 4 * p2) + 2 * j;
-      *reinterpret_cast<uint2*>(vt + d * kVtStride + 4 * kq) =
-          make_uint2(pack_halves<false>(w0, w1), pack_halves<false>(w2, w3));
-      *reinterpret_cast<uint2*>(vt + (d + 1) * kVtStride + 4 * kq) =
-          make_uint2(pack_halves<true>(w0, w1), pack_halves<true>(w2, w3));
-    }
-  }
+__device__ inline sa_u32x4v lds_read_b128(const lds_u8* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) sa_u32x4v*>(p);
+}
+// ds_read_b64_tr_b16: within each 16-lane group, lane i points at 4 consecutive bf16 (row
+// i/4, columns 4(i%4)..+3 of a 4 x 16 block); lane j receives column j of that block.
+__device__ inline uint2 lds_read_tr16(const lds_u8* p) {
+  const sa_i16x4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sa_i16x4v*)(p));
+  return __builtin_bit_cast(uint2, v);
 }
 
-// V^T A operand for d-chunk dc, key step (c, u): V^T[32dc + col][32c + 16u + 4hh + {0..3, 8..11}].
-__device__ inline sa_bf16x8 read_vt(const uint16_t* vt, int dc, int c, int u, int col, int hh) {
-  const uint16_t* r = vt + (32 * dc + col) * kVtStride + 32 * c + 16 * u + 4 * hh;
-  const uint2 lo = *reinterpret_cast<const uint2*>(r);
-  const uint2 hi = *reinterpret_cast<const uint2*>(r + 8);
-  return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+// Copy one 64-row tile into LDS: instruction i, lane l -> row 8i + l/8 (tile-relative),
+// 16-byte slot l of the i-th KB of `dst`. goff[p] = lane offset for rows with (row/8) odd
+// (p = 1) or even (p = 0); it holds the swizzle. Offsets at or past `bytes` read as zero.
+__device__ inline void dma_tile(const void* base, uint32_t bytes, uint32_t tile_off, uint32_t row_bytes,
+                                const uint32_t (&goff)[2], lds_u8* dst) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                                                        (int)bytes, 0x00020000);
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_u8*)(dst + 1024 * i), 16,
+                                             tile_off + 8 * i * row_bytes + goff[i & 1], 0, 0, 0);
 }
 
-// Softmax of one query group's 16 S^T values of a 32-key half (element i -> key
-// 8(i/4) + 4hh + (i%4) of the half) into 8 packed bf16 P pairs; updates the running max m
-// (log2 domain, scaled) and the lane-partial row sum l. Returns true (wave-uniform) when
-// the running max was raised; then *alpha is the factor for the accumulator.
-template <bool kBias>
-__device__ inline bool softmax16(sa_f32x16& s, const float (&bl)[16], float scale_log2, float& m, float& l,
-                                 uint32_t (&pk)[8], float& alpha) {
-  if (kBias) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = fmaf(s[i], scale_log2, bl[i]);
-  }
-  float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-  for (int i = 3; i < 15; i += 2) mx = fmaxf(fmaxf(mx, s[i]), s[i + 1]);
-  mx = fmaxf(mx, s[15]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
-  const float cand = kBias ? mx : mx * scale_log2;  // scale_log2 > 0
-  // Raise the running max only when this half-tile exceeds it by more than the threshold
-  // (always on the first one, where m = -inf).
-  const bool raise = __ballot(cand > m + kRescaleLog2) != 0;
-  if (raise) {
-    const float m_new = fmaxf(m, cand);
-    alpha = fast_exp2(m - m_new);  // 0 when m = -inf
-    l *= alpha;
-    m = m_new;
-  }
-  const float m_use = (m == -INFINITY) ? 0.f : m;
-#pragma unroll
-  for (int i = 0; i < 16; i += 2) {
-    float p0, p1;
-    if (kBias) {
-      p0 = fast_exp2(s[i] - m_use);
-      p1 = fast_exp2(s[i + 1] - m_use);
-    } else {
-      p0 = fast_exp2(fmaf(s[i], scale_log2, -m_use));
-      p1 = fast_exp2(fmaf(s[i + 1], scale_log2, -m_use));
-    }
-    pk[i >> 1] = cvt_pk_bf16(p0, p1);
-    l = dot2_bf16_ones(pk[i >> 1], l);
-  }
-  return raise;
-}
-
-// P^T B operand for key step u of a half: elements 8u..8u+7.
-__device__ inline sa_bf16x8 p_operand(const uint32_t (&pk)[8], int u) {
-  return as_bf16x8(make_uint4(pk[4 * u], pk[4 * u + 1], pk[4 * u + 2], pk[4 * u + 3]));
-}
+// s_waitcnt encodings (gfx9): vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+constexpr int kWaitLgkm0 = 0xC07F;
 
 template <bool kBias, bool kMask>
-__global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kWaves][kVtElems];
-  // Key bias of the current tile (log2 domain), staged with V: one load per lane.
-  __shared__ __attribute__((aligned(16))) float bias_lds[kBias ? kWaves : 1][kBlock];
+__global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
+  // Separate LDS objects for K, V and bias so that the compiler's own wait analysis can
+  // tell a copy into one from a read of another.
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kWaves * kTileBytes];
+  __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * kBlock : 4];
+  // Vector-memory operations per tile, in issue order: group K = [mask rows (2)] [K (8)],
+  // group V = [bias (1)] [V (8)]. The waits below count them.
+  constexpr int kGroupK = 8 + (kMask ? 2 : 0);
+  constexpr int kGroupV = 8 + (kBias ? 1 : 0);
 
   const int lane = threadIdx.x & 63;
-  // Wave-uniform values are made provably uniform (readfirstlane) so that the list and
-  // order reads below are scalar loads: a vector load would need s_waitcnt vmcnt(0),
-  // which would also wait for the K/V prefetches in flight.
+  // Wave-uniform values are made provably uniform (readfirstlane) so that the list, slot
+  // and order reads are scalar loads, which leave the vector-memory counter alone.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 31;  // query column within a 32-row group (MFMA n index)
   const int hh = lane >> 5;   // lane half (MFMA k group)
@@ -226,21 +176,62 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   const int qb = item - bh * a.nqb;
   const int b = bh / a.H;
   const int h = bh - b * a.H;
-  uint16_t* vt = vt_lds[wave];
 
   const int64_t list_row = (int64_t)bh * a.list_bh_stride + qb;
   int cnt = a.kv_cnt[list_row];
   cnt = cnt < 0 ? 0 : (cnt > a.max_cnt ? a.max_cnt : cnt);
-  const int32_t* list = a.kv_idx + list_row * a.max_cnt;
-  const int32_t* slots = kMask ? a.kv_slot + list_row * a.max_cnt : nullptr;
+  // Constant address space: the compiler may use scalar loads (nothing here writes them).
+  const __attribute__((address_space(4))) int32_t* list =
+      (const __attribute__((address_space(4))) int32_t*)(a.kv_idx + list_row * a.max_cnt);
+  const __attribute__((address_space(4))) int32_t* slots =
+      kMask ? (const __attribute__((address_space(4))) int32_t*)(a.kv_slot + list_row * a.max_cnt) : nullptr;
 
   const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh;
-  const uint16_t* kbase = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vbase = a.v + b * a.v_sb + h * a.v_sh;
+  const uint16_t* khead = a.k + b * a.k_sb + h * a.k_sh;
+  const uint16_t* vhead = a.v + b * a.v_sb + h * a.v_sh;
   uint16_t* obase = a.o + b * a.o_sb + h * a.o_sh;
-  const float* bbase = kBias ? a.bias + b * a.bias_sb + h * a.bias_sh : nullptr;
+  const float* bhead = kBias ? a.bias + b * a.bias_sb + h * a.bias_sh : nullptr;
+  const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
+  const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
+  const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
+  lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes;
+  lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes;
+  float* bl_lds = b_lds + (kBias ? wave * kBlock : 0);
 
-  // Q^T B operands: qf[g][s] = q[qb*64 + 32g + col][16s + 8hh .. +7].
+  // Lane constants: copy offsets, K operand read offsets, V^T transposed read offsets.
+  uint32_t kgo[2], vgo[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int r = 8 * p + (lane >> 3);
+    const int chunk = (lane & 7) ^ swz(r);
+    kgo[p] = (lane >> 3) * krow + 16 * chunk;
+    vgo[p] = (lane >> 3) * vrow + 16 * chunk;
+  }
+  // K A-operand of (key chunk c, d-step s): K[32c + col][16s + 8hh .. +7] = row 32c + col,
+  // chunk 2s + hh (+ 4096 c).
+  int kro[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kro[s] = 128 * col + 16 * ((2 * s + hh) ^ swz(col));
+  // V^T A-operand of (d-chunk dc, key step 32c + 16u): two transposed reads t = 0, 1 of rows
+  // 32c + 16u + 8t + 4hq + 0..3 at d = 32dc + 16dg + 4(i%4) (lane = 16(2hq + dg) + i); lane
+  // 16(2hq + dg) + j receives d = 32dc + 16dg + j, keys 16u + 8t + 4hq + 0..3, the key slots
+  // of the P^T B operand (S^T rows 8(e/4) + 4hh + e%4).
+  int vro[2][2];
+  {
+    const int i = lane & 15, g4 = lane >> 4;
+    const int hq = g4 >> 1, dg = g4 & 1;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = 8 * t + 4 * hq + (i >> 2);
+        const int chunk = 4 * dc + 2 * dg + ((i & 3) >> 1);
+        vro[dc][t] = 128 * r + 16 * (chunk ^ swz(r)) + 8 * (i & 1);
+      }
+  }
+
+  // Q^T B operands: qf[g][s] = q[qb*64 + 32g + col][16s + 8hh .. +7] (rows clamped into Lq;
+  // clamped rows are never stored).
   sa_bf16x8 qf[2][4];
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
@@ -258,146 +249,197 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
   float m[2] = {-INFINITY, -INFINITY};
   float l[2] = {0.f, 0.f};
 
-  // Skip list entries outside the key-block grid.
-  auto next_valid = [&](int it) {
-    while (it < cnt && (unsigned)list[it] >= (unsigned)a.nkb) ++it;
-    return it;
-  };
-
-  int it = next_valid(0);
-  uint4 kr[2][4];
-  uint4 vr[2][4];
-  float bv = 0.f;  // bias of key `lane` of the prefetched tile (kBias only)
-  float* bl_lds = bias_lds[kBias ? wave : 0];
-  auto load_bias = [&](int key0) {
-    if (kBias) bv = bbase[min(key0 + lane, a.Lk - 1)] * kLog2e;
-  };
-  // Tile masks (kMask only): rows 32g + col of the current / prefetched tile's mask.
-  uint64_t mw_cur[2] = {~0ull, ~0ull}, mw_next[2] = {~0ull, ~0ull};
-  int slot_cur = -1, slot_next = -1;
-  auto load_mask = [&](int it_) {
+  // An entry outside [0, nkb) copies block 0 and is masked out entirely.
+  auto entry = [&](int it) -> int { return it < cnt ? list[it] : -1; };
+  auto block_ok = [&](int kb) { return (unsigned)kb < (unsigned)a.nkb; };
+  uint64_t mw[2] = {~0ull, ~0ull};  // tile-mask rows 32g + col of the tile in flight
+  int mslot = -1;
+  // Group K of tile `kb` (list position it): mask rows, K copy.
+  auto issue_k = [&](int kb, int it) {
+    const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
     if (kMask) {
-      slot_next = it_ < cnt ? slots[it_] : -1;
-      const uint64_t* mrow = a.tile_masks + (int64_t)max(slot_next, 0) * kBlock;
-      mw_next[0] = mrow[col];
-      mw_next[1] = mrow[32 + col];
+      mslot = it < cnt ? slots[it] : -1;
+      const uint64_t* mrow = a.tile_masks + (int64_t)max(mslot, 0) * kBlock;
+      mw[0] = mrow[col];
+      mw[1] = mrow[32 + col];
     }
+    dma_tile(khead, kbytes, kb0 * krow, krow, kgo, kl);
   };
-  int kb_cur = it < cnt ? list[it] : 0;
-  if (it < cnt) {
-    load_k(a, kbase, kb_cur * kBlock, col, hh, kr);
-    load_v(a, vbase, kb_cur * kBlock, lane, vr);
-    load_bias(kb_cur * kBlock);
-    load_mask(it);
-    store_vt(vt, lane, vr);
-    if (kBias) bl_lds[lane] = bv;
-    slot_cur = slot_next;
-    mw_cur[0] = mw_next[0];
-    mw_cur[1] = mw_next[1];
-  }
-  int it_next = next_valid(it + 1);
-  // Prefetches are issued every iteration (past the end of the list they re-load the
-  // current block) so the loop body has the same loads in flight on every path.
-  int kb_next = it_next < cnt ? list[it_next] : kb_cur;
-  if (it < cnt) {
-    load_v(a, vbase, kb_next * kBlock, lane, vr);
-    load_bias(kb_next * kBlock);
-    load_mask(it_next);
-  }
+  // Group V of tile `kb`: bias copy (keys past Lk read as zero), V copy.
+  auto issue_v = [&](int kb) {
+    const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
+    if (kBias) {
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bhead), (short)0,
+                                                                          a.Lk * 4, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_u8*)bl_lds, 4, (kb0 + lane) * 4, 0, 0, 0);
+    }
+    dma_tile(vhead, vbytes, kb0 * vrow, vrow, vgo, vl);
+  };
 
+  int it = 0;
+  int kb = entry(0);
+  if (cnt > 0) {
+    issue_k(kb, 0);
+    issue_v(kb);
+  }
   while (it < cnt) {
-    const int key0 = kb_cur * kBlock;
-    const int nvalid = min(kBlock, a.Lk - key0);
-    // Two 32-key halves per tile keep one half's S (32 VGPRs) and P (16) live at a time.
+    // Past the end of the list the copies re-load the current block, so every iteration
+    // has the same operations in flight.
+    const int it_next = it + 1 < cnt ? it + 1 : it;
+    const int kb_next = entry(it_next);
+    const int nvalid = block_ok(kb) ? min(kBlock, a.Lk - kb * kBlock) : 0;
+    const uint64_t mw_cur[2] = {mw[0], mw[1]};
+    const int mslot_cur = mslot;
+
+    // ---- K operands of this tile, then request the next tile's group K.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupV));
+    sa_u32x4v kop[2][4];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      sa_f32x16 s[2];  // [g]: S^T of keys 32c.., query group g
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kop[c][s] = lds_read_b128(kl + kro[s] + 4096 * c);
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    issue_k(kb_next, it_next);
+
+    // ---- S^T = K Q^T: S[g][c] element e is key 32c + 8(e/4) + 4hh + e%4, query 32g + col.
+    sa_f32x16 S[2][2];
+    __builtin_amdgcn_s_setprio(kMfmaPrio);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         sa_f32x16 t = {};
 #pragma unroll
-        for (int st = 0; st < 4; ++st) t = mfma32(as_bf16x8(kr[c][st]), qf[g][st], t);
-        s[g] = t;
+        for (int s = 0; s < 4; ++s) t = mfma32(as_bf16x8(kop[c][s]), qf[g][s], t);
+        S[g][c] = t;
       }
-      if (c == 1) load_k(a, kbase, kb_next * kBlock, col, hh, kr);
-
-      if (nvalid < kBlock) {  // keys past Lk in the last (partial) block
+    __builtin_amdgcn_s_setprio(0);
+    if (kBias) {  // S' = s * sm_scale + bias (natural-log units; log2(e) applied with -m)
+      // The bias copy of this tile was issued before its V copy: wait for it only.
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + kGroupK));
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = 32 * c + 8 * (i >> 2) + 4 * hh + (i & 3);
-          if (key >= nvalid) {
-            s[0][i] = -INFINITY;
-            s[1][i] = -INFINITY;
-          }
-        }
-      }
-      if (kMask && slot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const uint32_t half = (uint32_t)(mw_cur[g] >> (32 * c));
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = 8 * (i >> 2) + 4 * hh + (i & 3);
-            if (!((half >> key) & 1u)) s[g][i] = -INFINITY;
-          }
-        }
-      }
-      float bl[16];
-      if (kBias) {
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const int key = key0 + 32 * c + 8 * q4 + 4 * hh;
-          const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + (key - key0));
-          bl[4 * q4 + 0] = b4.x;
-          bl[4 * q4 + 1] = b4.y;
-          bl[4 * q4 + 2] = b4.z;
-          bl[4 * q4 + 3] = b4.w;
+          const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + 32 * c + 8 * q4 + 4 * hh);
+          const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            S[0][c][4 * q4 + j] = fmaf(S[0][c][4 * q4 + j], a.sm_scale, bq[j]);
+            S[1][c][4 * q4 + j] = fmaf(S[1][c][4 * q4 + j], a.sm_scale, bq[j]);
+          }
         }
-      }
-
-      uint32_t pk[2][8];
+    }
+    if (nvalid < kBlock) {  // keys past Lk, or an entry outside the grid
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        float alpha = 1.f;
-        if (softmax16<kBias>(s[g], bl, a.scale_log2, m[g], l[g], pk[g], alpha)) {
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
+        for (int e = 0; e < 16; ++e) {
+          if (32 * c + 8 * (e >> 2) + 4 * hh + (e & 3) >= nvalid) {
+            S[0][c][e] = -INFINITY;
+            S[1][c][e] = -INFINITY;
+          }
         }
-      }
-      // O^T += V^T P^T over this half's two 16-key steps.
+    }
+    if (kMask && mslot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int g = 0; g < 2; ++g)
 #pragma unroll
-        for (int dc = 0; dc < 2; ++dc) {
-          const sa_bf16x8 va = read_vt(vt, dc, c, u, col, hh);
+        for (int c = 0; c < 2; ++c) {
+          const uint32_t bits = (uint32_t)(mw_cur[g] >> (32 * c));
 #pragma unroll
-          for (int g = 0; g < 2; ++g) acc[dc][g] = mfma32(va, p_operand(pk[g], u), acc[dc][g]);
+          for (int e = 0; e < 16; ++e)
+            if (!((bits >> (8 * (e >> 2) + 4 * hh + (e & 3))) & 1u)) S[g][c][e] = -INFINITY;
         }
-      }
     }
 
-    // ---- V^T of the next tile into the (now free) LDS tile; prefetch the one after.
-    // LDS accesses of one wave execute in order and the compiler keeps the program order
-    // of these aliasing accesses, so no fence is needed (a fence would also wait for the
-    // global prefetches).
-    it = it_next;
-    kb_cur = kb_next;
-    store_vt(vt, lane, vr);
-    if (kBias) bl_lds[lane] = bv;
-    slot_cur = slot_next;
-    mw_cur[0] = mw_next[0];
-    mw_cur[1] = mw_next[1];
-    it_next = next_valid(it + 1);
-    kb_next = it_next < cnt ? list[it_next] : kb_cur;
-    load_v(a, vbase, kb_next * kBlock, lane, vr);
-    load_bias(kb_next * kBlock);
-    load_mask(it_next);
+    // ---- Row max (lazy raise), then P = exp2(S * scale - m) in bf16 and the row sums.
+    const float to_log2 = kBias ? kLog2e : a.scale_log2;
+    float cand[2];
+    bool raise = false;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      float mx = fmaxf(fmaxf(S[g][0][0], S[g][0][1]), S[g][0][2]);
+#pragma unroll
+      for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][0][e]), S[g][0][e + 1]);
+      mx = fmaxf(fmaxf(mx, S[g][0][15]), S[g][1][0]);
+#pragma unroll
+      for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][1][e]), S[g][1][e + 1]);
+      mx = fmaxf(mx, S[g][1][15]);
+      mx = xhalf_max(mx);
+      cand[g] = mx * to_log2;  // to_log2 > 0
+      raise |= cand[g] > m[g] + kRescaleLog2;
+    }
+    // Raise the running max only when this tile exceeds it by more than the threshold
+    // (always on the first tile, where m = -inf).
+    if (__ballot(raise) != 0) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const float m_new = fmaxf(m[g], cand[g]);
+        const float alpha = fast_exp2(m[g] - m_new);  // 0 when m = -inf
+        m[g] = m_new;
+        l[g] *= alpha;
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
+      }
+    }
+    uint32_t P[2][2][8];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const float mu = (m[g] == -INFINITY) ? 0.f : m[g];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = fast_exp2(fmaf(S[g][c][e], to_log2, -mu));
+          const float p1 = fast_exp2(fmaf(S[g][c][e + 1], to_log2, -mu));
+          P[g][c][e >> 1] = cvt_pk_bf16(p0, p1);
+          l[g] = dot2_bf16_ones(P[g][c][e >> 1], l[g]);
+        }
+    }
+
+    // ---- V^T operands of this tile, then request the next tile's V.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
+    sa_u32x4v vop[2][2][2];
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint2 lo = lds_read_tr16(vl + vro[dc][0] + 128 * (32 * c + 16 * u));
+          const uint2 hi = lds_read_tr16(vl + vro[dc][1] + 128 * (32 * c + 16 * u));
+          vop[dc][c][u] = sa_u32x4v{lo.x, lo.y, hi.x, hi.y};
+        }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    issue_v(kb_next);
+
+    // ---- O^T += V^T P^T over the tile's four 16-key steps.
+    __builtin_amdgcn_s_setprio(kMfmaPrio);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+            acc[dc][g] = mfma32(as_bf16x8(vop[dc][c][u]),
+                                as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
+                                                    P[g][c][4 * u + 3]}),
+                                acc[dc][g]);
+    __builtin_amdgcn_s_setprio(0);
+    it = it + 1;
+    kb = kb_next;
   }
+  // The copies requested after the last tile land in this wave's LDS: wait for them before
+  // the wave ends and its workgroup's LDS can be reassigned.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    const float l_tot = l[g] + __shfl_xor(l[g], 32);
+    const float l_tot = xhalf_sum(l[g]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int row = qb * kBlock + 32 * g + col;
     if (row < a.Lq) {
@@ -418,6 +460,7 @@ __global__ __launch_bounds__(256, SA_ATTN_MIN_WAVES) void bsa_fwd_kernel(FwdArgs
 }
 
 }  // namespace
+
 
 extern "C" int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int n_xcd, int32_t* order,
                                   int64_t* n_slots) {
@@ -490,6 +533,11 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
       if (s[i] % 8 != 0) return sa::fail(SA_ERR_UNSUPPORTED, "%s: strides must be multiples of 8 elements", fn);
     }
   }
+  // K/V tiles are copied through 32-bit buffer offsets relative to each head's first row.
+  for (const int64_t* st : {k_strides, v_strides}) {
+    if ((int64_t)(Lk - 1) * st[2] * 2 + 2 * kHeadDim > INT_MAX)
+      return sa::fail(SA_ERR_UNSUPPORTED, "%s: key rows of one head span more than 2 GiB", fn);
+  }
   const int64_t grid = n_slots / kWaves;
   SA_REQUIRE(grid < (1LL << 31), "%s: grid too large", fn);
 
@@ -507,6 +555,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
   a.bias_sh = key_bias ? bias_strides[1] : 0;
+  a.sm_scale = sm_scale;
   a.scale_log2 = sm_scale * kLog2e;
   a.list_bh_stride = lists_shared ? 0 : nqb;
   a.kv_slot = kv_slot;
