@@ -39,6 +39,7 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <type_traits>
 #include <vector>
 
 #include "sa_common.h"
@@ -242,12 +243,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   }
 
   sa_f32x16 acc[2][2];  // [dc][g]
-#pragma unroll
-  for (int dc = 0; dc < 2; ++dc)
-#pragma unroll
-    for (int g = 0; g < 2; ++g) acc[dc][g] = sa_f32x16{};
-  float m[2] = {-INFINITY, -INFINITY};
-  float l[2] = {0.f, 0.f};
+  float m[2];
+  float l[2];
 
   // An entry outside [0, nkb) copies block 0 and is masked out entirely.
   auto entry = [&](int it) -> int { return it < cnt ? list[it] : -1; };
@@ -276,165 +273,200 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     dma_tile(vhead, vbytes, kb0 * vrow, vrow, vgo, vl);
   };
 
-  int it = 0;
-  int kb = entry(0);
-  if (cnt > 0) {
-    issue_k(kb, 0);
-    issue_v(kb);
-  }
-  while (it < cnt) {
-    // Past the end of the list the copies re-load the current block, so every iteration
-    // has the same operations in flight.
-    const int it_next = it + 1 < cnt ? it + 1 : it;
-    const int kb_next = entry(it_next);
-    const int nvalid = block_ok(kb) ? min(kBlock, a.Lk - kb * kBlock) : 0;
-    const uint64_t mw_cur[2] = {mw[0], mw[1]};
-    const int mslot_cur = mslot;
-
-    // ---- K operands of this tile, then request the next tile's group K.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupV));
-    sa_u32x4v kop[2][4];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kop[c][s] = lds_read_b128(kl + kro[s] + 4096 * c);
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    issue_k(kb_next, it_next);
-
-    // ---- S^T = K Q^T: S[g][c] element e is key 32c + 8(e/4) + 4hh + e%4, query 32g + col.
-    sa_f32x16 S[2][2];
-    __builtin_amdgcn_s_setprio(kMfmaPrio);
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        sa_f32x16 t = {};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) t = mfma32(as_bf16x8(kop[c][s]), qf[g][s], t);
-        S[g][c] = t;
-      }
-    __builtin_amdgcn_s_setprio(0);
-    if (kBias) {  // S' = s * sm_scale + bias (natural-log units; log2(e) applied with -m)
-      // The bias copy of this tile was issued before its V copy: wait for it only.
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + kGroupK));
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + 32 * c + 8 * q4 + 4 * hh);
-          const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            S[0][c][4 * q4 + j] = fmaf(S[0][c][4 * q4 + j], a.sm_scale, bq[j]);
-            S[1][c][4 * q4 + j] = fmaf(S[1][c][4 * q4 + j], a.sm_scale, bq[j]);
-          }
-        }
-    }
-    if (nvalid < kBlock) {  // keys past Lk, or an entry outside the grid
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          if (32 * c + 8 * (e >> 2) + 4 * hh + (e & 3) >= nvalid) {
-            S[0][c][e] = -INFINITY;
-            S[1][c][e] = -INFINITY;
-          }
-        }
-    }
-    if (kMask && mslot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const uint32_t bits = (uint32_t)(mw_cur[g] >> (32 * c));
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (!((bits >> (8 * (e >> 2) + 4 * hh + (e & 3))) & 1u)) S[g][c][e] = -INFINITY;
-        }
-    }
-
-    // ---- Row max (lazy raise), then P = exp2(S * scale - m) in bf16 and the row sums.
-    const float to_log2 = kBias ? kLog2e : a.scale_log2;
-    float cand[2];
-    bool raise = false;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      float mx = fmaxf(fmaxf(S[g][0][0], S[g][0][1]), S[g][0][2]);
-#pragma unroll
-      for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][0][e]), S[g][0][e + 1]);
-      mx = fmaxf(fmaxf(mx, S[g][0][15]), S[g][1][0]);
-#pragma unroll
-      for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][1][e]), S[g][1][e + 1]);
-      mx = fmaxf(mx, S[g][1][15]);
-      mx = xhalf_max(mx);
-      cand[g] = mx * to_log2;  // to_log2 > 0
-      raise |= cand[g] > m[g] + kRescaleLog2;
-    }
-    // Raise the running max only when this tile exceeds it by more than the threshold
-    // (always on the first tile, where m = -inf).
-    if (__ballot(raise) != 0) {
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const float m_new = fmaxf(m[g], cand[g]);
-        const float alpha = fast_exp2(m[g] - m_new);  // 0 when m = -inf
-        m[g] = m_new;
-        l[g] *= alpha;
-#pragma unroll
-        for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
-      }
-    }
-    uint32_t P[2][2][8];
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const float mu = (m[g] == -INFINITY) ? 0.f : m[g];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int e = 0; e < 16; e += 2) {
-          const float p0 = fast_exp2(fmaf(S[g][c][e], to_log2, -mu));
-          const float p1 = fast_exp2(fmaf(S[g][c][e + 1], to_log2, -mu));
-          P[g][c][e >> 1] = cvt_pk_bf16(p0, p1);
-          l[g] = dot2_bf16_ones(P[g][c][e >> 1], l[g]);
-        }
-    }
-
-    // ---- V^T operands of this tile, then request the next tile's V.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
-    sa_u32x4v vop[2][2][2];
+  // One pass over the item's key blocks. Fast pass (kSafe = false): P = exp2(S) with no
+  // max subtraction. Softmax is invariant to a common factor, and bf16 P keeps fp32's
+  // exponent range, so this equals the max-subtracted result as long as the scores stay in
+  // range; the caller checks the row sums afterwards and redoes the item with the safe pass
+  // (running max, lazy rescale) otherwise.
+  auto run = [&](auto safe_tag) {
+    constexpr bool kSafe = decltype(safe_tag)::value;
 #pragma unroll
     for (int dc = 0; dc < 2; ++dc)
 #pragma unroll
+      for (int g = 0; g < 2; ++g) acc[dc][g] = sa_f32x16{};
+    m[0] = m[1] = -INFINITY;
+    l[0] = l[1] = 0.f;
+    int it = 0;
+    int kb = entry(0);
+    if (cnt > 0) {
+      issue_k(kb, 0);
+      issue_v(kb);
+    }
+    while (it < cnt) {
+      // Past the end of the list the copies re-load the current block, so every iteration
+      // has the same operations in flight.
+      const int it_next = it + 1 < cnt ? it + 1 : it;
+      const int kb_next = entry(it_next);
+      const int nvalid = block_ok(kb) ? min(kBlock, a.Lk - kb * kBlock) : 0;
+      const uint64_t mw_cur[2] = {mw[0], mw[1]};
+      const int mslot_cur = mslot;
+
+      // ---- K operands of this tile, then request the next tile's group K.
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupV));
+      sa_u32x4v kop[2][4];
+#pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint2 lo = lds_read_tr16(vl + vro[dc][0] + 128 * (32 * c + 16 * u));
-          const uint2 hi = lds_read_tr16(vl + vro[dc][1] + 128 * (32 * c + 16 * u));
-          vop[dc][c][u] = sa_u32x4v{lo.x, lo.y, hi.x, hi.y};
-        }
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    issue_v(kb_next);
+        for (int s = 0; s < 4; ++s) kop[c][s] = lds_read_b128(kl + kro[s] + 4096 * c);
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      issue_k(kb_next, it_next);
 
-    // ---- O^T += V^T P^T over the tile's four 16-key steps.
-    __builtin_amdgcn_s_setprio(kMfmaPrio);
+      // ---- S^T = K Q^T: S[g][c] element e is key 32c + 8(e/4) + 4hh + e%4, query 32g + col.
+      sa_f32x16 S[2][2];
+      __builtin_amdgcn_s_setprio(kMfmaPrio);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+        for (int g = 0; g < 2; ++g) {
+          sa_f32x16 t = {};
 #pragma unroll
-        for (int dc = 0; dc < 2; ++dc)
+          for (int s = 0; s < 4; ++s) t = mfma32(as_bf16x8(kop[c][s]), qf[g][s], t);
+          S[g][c] = t;
+        }
+      __builtin_amdgcn_s_setprio(0);
+      if (kBias) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
+        // The bias copy of this tile was issued before its V copy: wait for it only.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + kGroupK));
 #pragma unroll
-          for (int g = 0; g < 2; ++g)
-            acc[dc][g] = mfma32(as_bf16x8(vop[dc][c][u]),
-                                as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
-                                                    P[g][c][4 * u + 3]}),
-                                acc[dc][g]);
-    __builtin_amdgcn_s_setprio(0);
-    it = it + 1;
-    kb = kb_next;
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + 32 * c + 8 * q4 + 4 * hh);
+            const float bq[4] = {b4.x * kLog2e, b4.y * kLog2e, b4.z * kLog2e, b4.w * kLog2e};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              S[0][c][4 * q4 + j] = fmaf(S[0][c][4 * q4 + j], a.scale_log2, bq[j]);
+              S[1][c][4 * q4 + j] = fmaf(S[1][c][4 * q4 + j], a.scale_log2, bq[j]);
+            }
+          }
+      }
+      if (nvalid < kBlock) {  // keys past Lk, or an entry outside the grid
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            if (32 * c + 8 * (e >> 2) + 4 * hh + (e & 3) >= nvalid) {
+              S[0][c][e] = -INFINITY;
+              S[1][c][e] = -INFINITY;
+            }
+          }
+      }
+      if (kMask && mslot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const uint32_t bits = (uint32_t)(mw_cur[g] >> (32 * c));
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              if (!((bits >> (8 * (e >> 2) + 4 * hh + (e & 3))) & 1u)) S[g][c][e] = -INFINITY;
+          }
+      }
+
+      // ---- P = exp2(S * sc - m) in bf16 and the row sums (m = 0 in the fast pass).
+      const float sc = kBias ? 1.f : a.scale_log2;  // S is already scaled with a bias
+      float mu[2] = {0.f, 0.f};
+      if (kSafe) {
+        // Row max; the running max is raised only when this tile exceeds it by more than
+        // the threshold (always on the first tile, where m = -inf).
+        float cand[2];
+        bool raise = false;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          float mx = fmaxf(fmaxf(S[g][0][0], S[g][0][1]), S[g][0][2]);
+#pragma unroll
+          for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][0][e]), S[g][0][e + 1]);
+          mx = fmaxf(fmaxf(mx, S[g][0][15]), S[g][1][0]);
+#pragma unroll
+          for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][1][e]), S[g][1][e + 1]);
+          mx = fmaxf(mx, S[g][1][15]);
+          cand[g] = xhalf_max(mx) * sc;  // sc > 0
+          raise |= cand[g] > m[g] + kRescaleLog2;
+        }
+        if (__ballot(raise) != 0) {
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            const float m_new = fmaxf(m[g], cand[g]);
+            const float alpha = fast_exp2(m[g] - m_new);  // 0 when m = -inf
+            m[g] = m_new;
+            l[g] *= alpha;
+#pragma unroll
+            for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) mu[g] = (m[g] == -INFINITY) ? 0.f : m[g];
+      }
+      uint32_t P[2][2][8];
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) {
+            const float p0 = fast_exp2(kSafe ? fmaf(S[g][c][e], sc, -mu[g]) : S[g][c][e] * sc);
+            const float p1 = fast_exp2(kSafe ? fmaf(S[g][c][e + 1], sc, -mu[g]) : S[g][c][e + 1] * sc);
+            P[g][c][e >> 1] = cvt_pk_bf16(p0, p1);
+            l[g] = dot2_bf16_ones(P[g][c][e >> 1], l[g]);
+          }
+
+      // ---- V^T operands of this tile, then request the next tile's V.
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
+      sa_u32x4v vop[2][2][2];
+#pragma unroll
+      for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const uint2 lo = lds_read_tr16(vl + vro[dc][0] + 128 * (32 * c + 16 * u));
+            const uint2 hi = lds_read_tr16(vl + vro[dc][1] + 128 * (32 * c + 16 * u));
+            vop[dc][c][u] = sa_u32x4v{lo.x, lo.y, hi.x, hi.y};
+          }
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      issue_v(kb_next);
+
+      // ---- O^T += V^T P^T over the tile's four 16-key steps.
+      __builtin_amdgcn_s_setprio(kMfmaPrio);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+            for (int g = 0; g < 2; ++g)
+              acc[dc][g] = mfma32(as_bf16x8(vop[dc][c][u]),
+                                  as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
+                                                      P[g][c][4 * u + 3]}),
+                                  acc[dc][g]);
+      __builtin_amdgcn_s_setprio(0);
+      it = it + 1;
+      kb = kb_next;
+    }
+    // The copies requested after the last tile land in this wave's LDS: wait for them
+    // before the LDS is read again or the wave ends.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  };
+
+  run(std::false_type{});
+  // The fast pass is exact unless a row's sum left [2^-90, 2^90] (scores far from 0, where
+  // exp2 would lose range) or an accumulator overflowed; then redo the item safely.
+  if (cnt > 0) {
+    bool bad = false;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const float l_tot = xhalf_sum(l[g]);
+      bad |= !(l_tot >= 0x1p-90f && l_tot <= 0x1p90f);
+      float amax = 0.f;
+#pragma unroll
+      for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][g][e])), fabsf(acc[dc][g][e + 1]));
+      bad |= !(amax <= 3.0e38f);
+    }
+    if (__ballot(bad) != 0) run(std::true_type{});
   }
-  // The copies requested after the last tile land in this wave's LDS: wait for them before
-  // the wave ends and its workgroup's LDS can be reassigned.
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
 #pragma unroll

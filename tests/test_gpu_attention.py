@@ -119,6 +119,35 @@ def test_key_bias(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125, key_bias=bias.double()))
 
 
+def test_large_scores_redo_with_running_max(dev):
+    # Head 0 has scores of several hundred (exp2 overflows without the max subtraction),
+    # head 1 ordinary ones: the kernel must redo exactly the items whose sums left range.
+    case("large scores on one head")
+    B, H, L = 1, 2, 300
+    q, k, v = (_rand((B, H, L, 64), 130 + i) for i in range(3))
+    q[:, 0] *= 16
+    k[:, 0] *= 16
+    nb = math.ceil(L / 64)
+    g = torch.Generator().manual_seed(13)
+    mask = torch.rand(B, H, nb, nb, generator=g) < 0.6
+    mask[..., 0] = True
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125)
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_uniform_negative_bias_is_shift_invariant(dev):
+    # A bias of -300 on every key underflows exp2 without the max subtraction; softmax is
+    # shift invariant, so the result must equal the unbiased one.
+    case("uniform -300 key bias")
+    B, H, L = 1, 2, 200
+    q, k, v = (_rand((B, H, L, 64), 140 + i) for i in range(3))
+    mask = torch.ones(1, 1, 4, 4, dtype=torch.bool)
+    kv = kv_list_from_mask(mask.to(dev), B, H, 4, 4)
+    bias = torch.full((B, 1, L), -300.0)
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bias.to(dev))
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
 def test_mask_to_kv_list_matches_nonzero(dev):
     case("mask_to_kv_list")
     g = torch.Generator().manual_seed(8)
