@@ -27,9 +27,9 @@
 //
 // Softmax economy: the running max is only raised when a tile exceeds it by more than
 // kRescaleLog2 (then p <= 2^kRescaleLog2), so the accumulator rescale is rare; row sums
-// accumulate the bf16-rounded P pairs with v_dot2c_f32_bf16; maxima use v_max3_f32. The
-// MFMA blocks run at raised wave priority so that the two waves of a SIMD tend to overlap
-// one's MFMAs with the other's softmax.
+// accumulate the bf16-rounded P pairs with v_dot2c_f32_bf16; maxima use v_max3_f32. A
+// first pass skips the max entirely (P = exp2(S * scale), exact while the row sums stay in
+// range, which is checked); items whose sums leave range are redone with the running max.
 //
 // Scheduling: a host-built work order maps dispatch slots to items so that each XCD
 // (workgroups round-robin over 8 XCDs) processes a contiguous range of heads, longest
@@ -52,7 +52,6 @@ constexpr int kWaves = 4;        // independent waves per workgroup
 constexpr int kTileBytes = kBlock * kHeadDim * 2;  // one K or V tile: 64 rows x 128 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
-constexpr int kMfmaPrio = 3;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef short sa_i16x4v __attribute__((ext_vector_type(4)));
@@ -132,6 +131,16 @@ __device__ inline sa_u32x4v lds_read_b128(const lds_u8* p) {
 __device__ inline uint2 lds_read_tr16(const lds_u8* p) {
   const sa_i16x4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) sa_i16x4v*)(p));
   return __builtin_bit_cast(uint2, v);
+}
+typedef unsigned sa_u32x2v __attribute__((ext_vector_type(2)));
+// The same read issued as inline assembly: the compiler's wait analysis cannot tell these
+// reads from the copies still landing in the other LDS buffers and would otherwise wait for
+// all of them; the caller waits for the reads explicitly (lgkm_wait_vop).
+template <int kOff>
+__device__ inline sa_u32x2v lds_read_tr16_asm(uint32_t addr) {
+  sa_u32x2v r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
 }
 
 // Copy one 64-row tile into LDS: instruction i, lane l -> row 8i + l/8 (tile-relative),
@@ -313,7 +322,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
       // ---- S^T = K Q^T: S[g][c] element e is key 32c + 8(e/4) + 4hh + e%4, query 32g + col.
       sa_f32x16 S[2][2];
-      __builtin_amdgcn_s_setprio(kMfmaPrio);
+      
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -323,7 +332,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
           for (int s = 0; s < 4; ++s) t = mfma32(as_bf16x8(kop[c][s]), qf[g][s], t);
           S[g][c] = t;
         }
-      __builtin_amdgcn_s_setprio(0);
+      
       if (kBias) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
         // The bias copy of this tile was issued before its V copy: wait for it only.
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + kGroupK));
@@ -412,22 +421,35 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
       // ---- V^T operands of this tile, then request the next tile's V.
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
+      sa_u32x2v vr[2][2][2][2];  // [dc][t][c][u]
+#pragma unroll
+      for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const uint32_t base = (uint32_t)(uintptr_t)(vl + vro[dc][t]);
+          vr[dc][t][0][0] = lds_read_tr16_asm<0>(base);
+          vr[dc][t][0][1] = lds_read_tr16_asm<2048>(base);
+          vr[dc][t][1][0] = lds_read_tr16_asm<4096>(base);
+          vr[dc][t][1][1] = lds_read_tr16_asm<6144>(base);
+        }
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(vr[0][0][0][0]), "+v"(vr[0][0][0][1]), "+v"(vr[0][0][1][0]), "+v"(vr[0][0][1][1]),
+                     "+v"(vr[0][1][0][0]), "+v"(vr[0][1][0][1]), "+v"(vr[0][1][1][0]), "+v"(vr[0][1][1][1]),
+                     "+v"(vr[1][0][0][0]), "+v"(vr[1][0][0][1]), "+v"(vr[1][0][1][0]), "+v"(vr[1][0][1][1]),
+                     "+v"(vr[1][1][0][0]), "+v"(vr[1][1][0][1]), "+v"(vr[1][1][1][0]), "+v"(vr[1][1][1][1]));
       sa_u32x4v vop[2][2][2];
 #pragma unroll
       for (int dc = 0; dc < 2; ++dc)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const uint2 lo = lds_read_tr16(vl + vro[dc][0] + 128 * (32 * c + 16 * u));
-            const uint2 hi = lds_read_tr16(vl + vro[dc][1] + 128 * (32 * c + 16 * u));
-            vop[dc][c][u] = sa_u32x4v{lo.x, lo.y, hi.x, hi.y};
-          }
+          for (int u = 0; u < 2; ++u)
+            vop[dc][c][u] = sa_u32x4v{vr[dc][0][c][u].x, vr[dc][0][c][u].y, vr[dc][1][c][u].x, vr[dc][1][c][u].y};
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
       issue_v(kb_next);
 
       // ---- O^T += V^T P^T over the tile's four 16-key steps.
-      __builtin_amdgcn_s_setprio(kMfmaPrio);
+      
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -440,7 +462,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
                                   as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
                                                       P[g][c][4 * u + 3]}),
                                   acc[dc][g]);
-      __builtin_amdgcn_s_setprio(0);
+      
       it = it + 1;
       kb = kb_next;
     }
