@@ -166,33 +166,47 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   __syncthreads();
 
   const int nch = (a.nkb + 63) >> 6;
+  const int k = a.topk < a.nkb ? a.topk : a.nkb;
+  // The wave's 4 rows are selected together: their 32-step searches are independent chains
+  // of ballot -> popcount -> compare, interleaved to hide each other's latency.
+  uint32_t key[4][NCH];  // ordered keys of this lane's columns c = 64e + lane (0 = unused)
+  bool live[4];
+#pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int rr = wave * 4 + u;
-    const int r = r0 + rr;
-    if (r >= a.nqb) break;  // wave-uniform
-    const int64_t row = row_base + r;
-    // Ordered keys of this lane's columns c = 64e + lane (0 = below every real key's use).
-    uint32_t key[NCH];
+    live[u] = r0 + rr < a.nqb;  // wave-uniform
+    const int64_t row = row_base + r0 + rr;
 #pragma unroll
     for (int e = 0; e < NCH; ++e) {
       const int c = 64 * e + lane;
-      key[e] = (e < nch && c < a.nkb) ? order_bits(s_lds[rr][c]) : 0u;
-      if (a.scores_out && e < nch && c < a.nkb) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
+      const bool valid = live[u] && e < nch && c < a.nkb;
+      key[u][e] = valid ? order_bits(s_lds[rr][c]) : 0u;
+      if (a.scores_out && valid) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
     }
-    const int k = a.topk < a.nkb ? a.topk : a.nkb;
-    uint32_t thr = 0u;   // the k-th largest key (0 when k == 0: then nothing is selected)
-    int need = 0;        // keys equal to thr to keep, lowest columns first
-    if (k > 0) {
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = thr | (1u << bit);
+  }
+  uint32_t thr[4] = {0u, 0u, 0u, 0u};  // the k-th largest key (0 when k == 0: nothing selected)
+  if (k > 0) {
+    for (int bit = 31; bit >= 0; --bit) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t cand = thr[u] | (1u << bit);
         int count = 0;
 #pragma unroll
-        for (int e = 0; e < NCH; ++e) count += __popcll(__ballot(key[e] >= cand));
-        if (count >= k) thr = cand;
+        for (int e = 0; e < NCH; ++e) count += __popcll(__ballot(key[u][e] >= cand));
+        if (count >= k) thr[u] = cand;
       }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (!live[u]) break;  // wave-uniform; later rows are past nqb as well
+    const int r = r0 + wave * 4 + u;
+    const int64_t row = row_base + r;
+    int need = 0;  // keys equal to thr to keep, lowest columns first
+    if (k > 0) {
       int gt = 0;
 #pragma unroll
-      for (int e = 0; e < NCH; ++e) gt += __popcll(__ballot(key[e] > thr));
+      for (int e = 0; e < NCH; ++e) gt += __popcll(__ballot(key[u][e] > thr[u]));
       need = k - gt;
     }
     const bool text_row = r < a.n_text;
@@ -204,13 +218,13 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     for (int e = 0; e < NCH; ++e) {
       const int c = 64 * e + lane;
       const bool valid = e < nch && c < a.nkb;
-      const bool tie = valid && k > 0 && key[e] == thr;
+      const bool tie = valid && k > 0 && key[u][e] == thr[u];
       const uint64_t tb = __ballot(tie);
       const int tie_rank = ties + __builtin_amdgcn_mbcnt_hi((uint32_t)(tb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)tb, 0));
       ties += __popcll(tb);
       bool on = false;
       if (valid) {
-        const bool sel = k > 0 && (key[e] > thr || (tie && tie_rank < need));
+        const bool sel = k > 0 && (key[u][e] > thr[u] || (tie && tie_rank < need));
         on = sel || text_row || c < a.n_text;
         if (loc) on = on || loc[c] != 0;
         if (a.mask_out) a.mask_out[row * a.nkb + c] = on ? 1 : 0;
