@@ -35,6 +35,7 @@ constexpr int kD = 64;           // head dim handled here
 constexpr int kMaxC = 2 * kD + 2;  // channels of the per-head (k, |k|, v, |v|) metric
 constexpr int kTileS = 64;       // src rows per match workgroup
 constexpr int kTileD = 64;       // dst columns per staged tile
+constexpr int kTileLd = 68;      // channel-major LDS row: 64 rows + 4 pad (16-byte aligned)
 constexpr int kRankTile = 1024;  // keys staged per rank step
 
 __device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -157,9 +158,10 @@ __device__ inline bool better(float v, int i, float bv, int bi) { return v > bv 
 __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
   extern __shared__ float sm[];
   const int C = a.C;
-  const int stride = C + 1;  // odd stride: 64 rows read at one channel hit distinct banks
+  // Tiles are stored channel-major (As[c][row], Bs[c][col], kTileLd floats per channel) so
+  // that a thread reads its 4 rows and its 4 columns of one channel with one 16-byte read each.
   float* As = sm;
-  float* Bs = sm + kTileS * stride;
+  float* Bs = sm + C * kTileLd;
   const int g = blockIdx.y, split = blockIdx.z;
   const int s0 = blockIdx.x * kTileS;
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
   for (int e = tid; e < kTileS * C; e += 256) {
     const int r = e / C, c = e - r * C;
     const int s = s0 + r;
-    As[r * stride + c] = s < a.n_src ? mg[(int64_t)a.a_idx[s] * C + c] : 0.f;
+    As[c * kTileLd + r] = s < a.n_src ? mg[(int64_t)a.a_idx[s] * C + c] : 0.f;
   }
   float best[4];
   int bidx[4];
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
     for (int e = tid; e < kTileD * C; e += 256) {
       const int r = e / C, c = e - r * C;
       const int d = d0 + r;
-      Bs[r * stride + c] = d < d_hi ? mg[(int64_t)a.b_idx[d] * C + c] : 0.f;
+      Bs[c * kTileLd + r] = d < d_hi ? mg[(int64_t)a.b_idx[d] * C + c] : 0.f;
     }
     __syncthreads();
     float acc[4][4];
@@ -192,11 +194,10 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
     for (int c = 0; c < C; ++c) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[(4 * ty + i) * stride + c];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[(4 * tx + j) * stride + c];
+      const float4 a4 = *reinterpret_cast<const float4*>(As + c * kTileLd + 4 * ty);
+      const float4 b4 = *reinterpret_cast<const float4*>(Bs + c * kTileLd + 4 * tx);
+      const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+      const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -580,7 +581,7 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
     a.n_src = m.n_src; a.n_dst = m.n_dst; a.splits = splits;
     a.dst_per_split = (m.n_dst + splits - 1) / splits;
     a.part_max = part_max; a.part_idx = part_idx;
-    const size_t lds = (size_t)(kTileS + kTileD) * (C + 1) * sizeof(float);
+    const size_t lds = (size_t)2 * C * kTileLd * sizeof(float);
     if (lds > 65536) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(match_kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
