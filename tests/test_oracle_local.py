@@ -52,3 +52,15 @@ def test_cogvideox_density_and_invariants():
     text[:, :4] = True
     # Density of local U text with the centre-token rule (independently computed as 0.0680).
     assert abs((bm | text).float().mean().item() - 0.0680) < 5e-4
+
+
+def test_cogvideox_bitmap_matches_fixture():
+    # tests/golden/local_window_cogvideox2b.npy (packbits of the 278 x 278 bitmap) pins the
+    # config-3 local window of both the oracle and the library's host builder.
+    import os
+    import numpy as np
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "local_window_cogvideox2b.npy")
+    nb = COGVIDEOX_2B.nb
+    want = torch.from_numpy(np.unpackbits(np.load(path, allow_pickle=False))[: nb * nb].reshape(nb, nb))
+    assert torch.equal(native.local_window(COGVIDEOX_2B, 1, 8, 8), want)
+    assert torch.equal(local_window_bitmap(COGVIDEOX_2B, (1, 8, 8)), want)
