@@ -20,6 +20,7 @@ import math
 import torch
 
 from . import _lib
+from ._gather import gather_tokens as _gather
 from .utils.block_sparse_attn_kernel import _prep_qkv, work_order
 
 config = {
@@ -103,18 +104,6 @@ def get_sliding_tile_attention_mask(kernel_size, tile_size, img_size, text_lengt
         lay = StaLayout(kernel_size, tile_size, img_size, text_length, device)
         _LAYOUTS[key] = lay
     return lay
-
-
-def _gather(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
-    _lib.require_gpu(x)
-    x = _prep_qkv(x)
-    B, H, L, D = x.shape
-    out = torch.empty(B, H, idx.numel(), D, dtype=x.dtype, device=x.device)
-    with torch.cuda.device(x.device):
-        rc = _lib.load().sa_gather_tokens(x.data_ptr(), _lib.i64(*x.stride()[:3]), B, H, L, D, idx.data_ptr(),
-                                          idx.numel(), out.data_ptr(), _lib.i64(*out.stride()[:3]), _lib.stream_of(x))
-    _lib.check(rc, "sa_gather_tokens")
-    return out
 
 
 class SildingTileAttention:

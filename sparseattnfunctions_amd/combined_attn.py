@@ -13,17 +13,58 @@ combined block mask of the MI355X build on the GPU:
 then runs the block-sparse attention kernel on it. This replaces the reference's
 per-head routing between pattern attention and the SparseGen+ estimator
 (combined_attn.py:47-101, partern_attention.py:516-521), which is host-synchronising and
-1.5-5B specific. `use_rearranger=True` (the reference's 1.5-5B token permutation) is not
-supported with this rule: the local window is defined on the text-first (t, h, w) layout.
+1.5-5B specific. `rearranger` / `recover` are the reference's 1.5-5B token permutations
+(combined_attn.py:17-41), as GPU gathers; `use_rearranger=True` is not supported with the
+combined rule, whose local window is defined on the text-first (t, h, w) layout.
 """
 from __future__ import annotations
 
 import math
 
+import torch
+
+from ._gather import gather_tokens
 from .block_mask_attn import dense_kv_list
 from .block_masks import local_window_bitmap, meanpool_topk_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
 from .workloads import COGVIDEOX_2B, Geometry, topk_count
+
+
+# The reference's 1.5-5B permutation (combined_attn.py:17-41): 224 text tokens first, then
+# 11 x 48 x 85 video tokens in (t, h, w) order. Frames 0-8 are cut into 3 x 4 x 5 cubes and
+# frames 9-10 into 2 x 6 x 5 cubes (frame, row, column sizes); the output lists the cubes of
+# each chunk in (frame group, row group, column group) order with each cube's tokens in
+# (frame, row, column) order, chunk 1 then chunk 2, then the text tokens.
+_R_TEXT, _R_T, _R_H, _R_W = 224, 11, 48, 85
+_R_CHUNKS = ((0, 3, 3, 12, 4, 17, 5), (9, 1, 2, 8, 6, 17, 5))  # first frame, fgroups, f, rgroups, r, cgroups, c
+
+
+def rearranger_permutation() -> torch.Tensor:
+    """int32 [L]: output token j of `rearranger` is input token perm[j] (CPU tensor)."""
+    parts = []
+    for t0, nfg, nf, nrg, nr, ncg, nc in _R_CHUNKS:
+        t = torch.arange(nfg * nf).reshape(nfg, 1, 1, nf, 1, 1) + t0
+        h = torch.arange(nrg * nr).reshape(1, nrg, 1, 1, nr, 1)
+        w = torch.arange(ncg * nc).reshape(1, 1, ncg, 1, 1, nc)
+        # dims: (frame group, row group, column group, frame, row, column) of each cube token
+        tok = (t.reshape(nfg, 1, 1, nf, 1, 1) * _R_H + h) * _R_W + w
+        tok = tok.expand(nfg, nrg, ncg, nf, nr, nc)
+        parts.append(_R_TEXT + tok.reshape(-1))
+    parts.append(torch.arange(_R_TEXT))
+    return torch.cat(parts).to(torch.int32)
+
+
+_PERM_CACHE = {}
+
+
+def _perms(device):
+    key = str(device)
+    if key not in _PERM_CACHE:
+        perm = rearranger_permutation()
+        inv = torch.empty_like(perm)
+        inv[perm.long()] = torch.arange(perm.numel(), dtype=torch.int32)
+        _PERM_CACHE[key] = (perm.to(device), inv.to(device))
+    return _PERM_CACHE[key]
 
 
 class CombinedAttn:
@@ -51,6 +92,25 @@ class CombinedAttn:
         local = local_window_bitmap(self.geometry, self.window, q.device)
         return meanpool_topk_kv_list(q, k, topk_count(self.global_ratio, nb), self.n_text_blocks(),
                                      local_bitmap=local)
+
+    @staticmethod
+    def rearranger(q, k, v):
+        """The 1.5-5B token permutation of q, k, v (L = 224 + 11*48*85): video cubes first,
+        text last (combined_attn.py:17-31). Returns permuted copies."""
+        L = _R_TEXT + _R_T * _R_H * _R_W
+        if q.shape[2] != L or k.shape[2] != L or v.shape[2] != L:
+            raise ValueError(f"rearranger expects the 1.5-5B sequence length {L}, got {q.shape[2]}")
+        perm, _ = _perms(q.device)
+        return tuple(gather_tokens(x, perm) for x in (q, k, v))
+
+    @staticmethod
+    def recover(out):
+        """Inverse of `rearranger` for the attention output (combined_attn.py:32-40)."""
+        L = _R_TEXT + _R_T * _R_H * _R_W
+        if out.shape[2] != L:
+            raise ValueError(f"recover expects the 1.5-5B sequence length {L}, got {out.shape[2]}")
+        _, inv = _perms(out.device)
+        return gather_tokens(out, inv)
 
     def _scale(self, q):
         return self.sm_scale if self.sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
