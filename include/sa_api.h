@@ -147,6 +147,56 @@ int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const fl
                           int32_t* kv_cnt, uint8_t* mask_out, float* scores_out, void* stream);
 
 /*
+ * Sampled tokens of the adaptive estimator.
+ * Replaces random_sample_tokens + pad_to_multiple (utils/mask_related.py:2-37): for every
+ * 64-token block of q (and of k), the tokens at the num_keep largest of the block's 64
+ * uniform draws, in (draw descending, position ascending) order -- torch.topk(sorted=True)
+ * -- where positions past L stand for token L-1 (the reference's replicate padding).
+ *   rand_q, rand_k  fp32 contiguous [B*H][nb][64] draws, nb = ceil(L/64) (rand_k, k,
+ *             k_strides, tok_k, k_sampled NULL: sample q only).
+ *   tok_q/tok_k nullable int32 [B*H][nb*num_keep] token ids.
+ *   q_sampled, k_sampled  bf16 [B*H][ns_pad][64] (rows >= nb*num_keep are not written).
+ *   1 <= num_keep <= 64, ns_pad >= nb*num_keep, D = 64.
+ */
+int sa_sample_block_tokens(const float* rand_q, const uint16_t* q, const int64_t q_strides[3],
+                           const float* rand_k, const uint16_t* k, const int64_t k_strides[3],
+                           int B, int H, int L, int D, int num_keep, int32_t* tok_q, int32_t* tok_k,
+                           uint16_t* q_sampled, uint16_t* k_sampled, int ns_pad, void* stream);
+
+/*
+ * Sampled block scores of the adaptive estimator.
+ * Replaces the attention-and-pool part of calc_attn_block_sum_efficient
+ * (utils/mask_related.py:62-81): with ns = nb*num_keep sampled rows per head,
+ * a = softmax_j(sq_i . sk_j / 8) and pooled[bh][I][J] = sum of a over the num_keep x
+ * num_keep cell (I, J) (the conv2d with a ones kernel and stride num_keep). fp32 throughout
+ * (the reference rounds scores, softmax and sums to bf16).
+ *   q_sampled, k_sampled from sa_sample_block_tokens; num_keep 8 or 16; ns_pad = ns rounded
+ *             up to a multiple of 32.
+ *   pooled    fp32 [B*H][nb][nb].
+ */
+int sa_sampled_block_scores(const uint16_t* q_sampled, const uint16_t* k_sampled, int BH, int nb,
+                            int num_keep, int ns_pad, float* pooled, void* stream);
+
+/*
+ * Energy-threshold / adaptive top-k block selection -> kv lists.
+ * Replaces transfer_attn_to_mask (SparseGen_Plus.py:12-84). Per score row (n = nkb columns):
+ * ranks in (score descending, column ascending) order and sequential fp32 prefix sums cum[]
+ * in rank order, total = cum[n-1]; keeps the columns of rank < k with
+ *   mode 0 ("energy"): k = n if total < threshold*total, else the first j with
+ *             cum[j] >= threshold*total; then k = min(max(k, min_keep), max_keep)
+ *             (:57-73: the crossing column itself is not kept before clamping);
+ *   mode 1 ("topk"): k = init_k; if cum[init_k-1] < 0.6*total and init_k < n, k = min(3k, n);
+ *             then if cum[init_k-1] < 0.9*total and init_k < n, k = min(k/3*2, n) (:31-46);
+ * united with columns < n_text_blocks and every column of rows < n_text_blocks (:81-82).
+ *   scores    fp32 [BH][nqb][nkb], nkb <= 1024; kv_idx int32 [BH*nqb][max_cnt >= nkb],
+ *             kv_cnt int32 [BH*nqb]; mask_out nullable uint8 [BH][nqb][nkb].
+ *   min_keep/max_keep/init_k are the reference's integers (max(1, int(seq*ratio)), ...).
+ */
+int sa_energy_kv_list(const float* scores, int BH, int nqb, int nkb, int mode, float threshold,
+                      int min_keep, int max_keep, int init_k, int n_text_blocks, int32_t* kv_idx,
+                      int max_cnt, int32_t* kv_cnt, uint8_t* mask_out, void* stream);
+
+/*
  * (host) Static local 3-D window of the combined mask, one byte per (query block, key
  * block): 1 iff both blocks are video blocks and their centre tokens (index
  * block*qb + block/2, clamped to L-1) lie within +-dt latent frames, +-dh patch rows and

@@ -35,6 +35,8 @@ def lib():
         L.oracle_block_score.restype = ctypes.c_float
         L.oracle_block_topk.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P]
         L.oracle_block_topk.restype = None
+        L.oracle_energy_list.argtypes = [_P, _I, _I, _I, _I, ctypes.c_float, _I, _I, _I, _I, _P, _I, _P, _P]
+        L.oracle_energy_list.restype = None
         L.oracle_local_window.argtypes = [_I] * 9 + [_P]
         L.oracle_local_window.restype = None
         L.oracle_tome_partition.argtypes = [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
@@ -86,6 +88,20 @@ def block_topk(qp, kp, topk: int, n_text: int, local=None, scores_in=None, nqb=N
     lib().oracle_block_topk(_p(qp), _p(kp), _p(scores_in), BH, nqb, nkb, D, topk, n_text, _p(loc),
                             _p(kv_idx), nkb, _p(kv_cnt), _p(mask), _p(scores))
     return kv_idx, kv_cnt, mask, scores
+
+
+def energy_list(scores, mode: int, threshold: float = 0.95, min_keep: int = 1, max_keep: int = 1 << 30,
+                init_k: int = 1, n_text: int = 4):
+    """scores fp32 [BH, nqb, nkb] -> (kv_idx [rows, nkb], kv_cnt [rows], mask uint8 [rows, nkb])."""
+    BH, nqb, nkb = scores.shape
+    scores = scores.contiguous().float()
+    rows = BH * nqb
+    kv_idx = torch.full((rows, nkb), -1, dtype=torch.int32)
+    kv_cnt = torch.empty(rows, dtype=torch.int32)
+    mask = torch.empty(rows, nkb, dtype=torch.uint8)
+    lib().oracle_energy_list(_p(scores), BH, nqb, nkb, mode, threshold, min_keep, max_keep, init_k, n_text,
+                             _p(kv_idx), nkb, _p(kv_cnt), _p(mask))
+    return kv_idx, kv_cnt, mask
 
 
 def local_window(geom, dt: int, dh: int, dw: int) -> torch.Tensor:

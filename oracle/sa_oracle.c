@@ -13,6 +13,8 @@
  *   oracle_block_topk      block scores, per-row top-k (utils/block_sparse_attn_kernel.py:31-39,
  *                          SparseGen_Plus.py:28-50), text rows/columns forced dense
  *                          (SparseGen_Plus.py:81-82), union with a local window, compaction
+ *   oracle_energy_list     energy-threshold and adaptive top-k selection of
+ *                          transfer_attn_to_mask (SparseGen_Plus.py:12-84) over fp32 scores
  */
 #include <math.h>
 #include <stdint.h>
@@ -107,6 +109,73 @@ void oracle_block_topk(const float* qp, const float* kp, const float* scores_in,
       kv_cnt[row] = cnt < max_cnt ? cnt : max_cnt;
     }
   free(keys);
+  free(keep);
+}
+
+/*
+ * transfer_attn_to_mask (SparseGen_Plus.py:12-84) per row: sort (score desc, index asc),
+ * cum[j] = sequential fp32 sum of the first j+1 sorted scores, total = cum[n-1];
+ *   mode 0 "energy" (:52-78): k = first j with cum[j] >= thr*total (n if cum[n-1] < thr*total),
+ *          clamped to [min_keep, max_keep]; keep the first k sorted columns;
+ *   mode 1 "topk" (:28-50): k0 = init_k, e = cum[k0-1]; if e < 0.6*total and k0 < n:
+ *          k = min(3*k0, n); if e < 0.9*total and k0 < n: k = min(k/3*2, n);
+ * then text rows/columns (< n_text) forced on (:81-82); ascending kv lists and 0/1 mask.
+ */
+void oracle_energy_list(const float* scores, int BH, int nqb, int nkb, int mode, float thr, int min_keep,
+                        int max_keep, int init_k, int n_text, int32_t* kv_idx, int max_cnt, int32_t* kv_cnt,
+                        uint8_t* mask_out) {
+  oracle_key* keys = (oracle_key*)malloc(sizeof(oracle_key) * (size_t)nkb);
+  float* cum = (float*)malloc(sizeof(float) * (size_t)nkb);
+  uint8_t* keep = (uint8_t*)malloc((size_t)nkb);
+  const int n = nkb;
+  for (int64_t row = 0; row < (int64_t)BH * nqb; ++row) {
+    const float* s = scores + row * n;
+    for (int c = 0; c < n; ++c) {
+      keys[c].ord = order_bits(s[c]);
+      keys[c].idx = c;
+    }
+    qsort(keys, (size_t)n, sizeof(oracle_key), cmp_key);
+    float acc = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      acc += s[keys[j].idx];
+      cum[j] = acc;
+    }
+    const float total = cum[n - 1];
+    int k;
+    if (mode == 0) {
+      const float target = thr * total;
+      int first = n;
+      for (int j = 0; j < n; ++j)
+        if (cum[j] >= target) {
+          first = j;
+          break;
+        }
+      k = total < target ? n : first;
+      if (k < min_keep) k = min_keep;
+      if (k > max_keep) k = max_keep;
+    } else {
+      const int k0 = init_k;
+      const float e = cum[k0 - 1];
+      k = k0;
+      if (!(e >= 0.6f * total) && k0 < n) k = (3 * k < n) ? 3 * k : n;
+      if (!(e >= 0.9f * total) && k0 < n) k = (k / 3 * 2 < n) ? k / 3 * 2 : n;
+    }
+    memset(keep, 0, (size_t)n);
+    for (int j = 0; j < k && j < n; ++j) keep[keys[j].idx] = 1;
+    const int r = (int)(row % nqb);
+    int cnt = 0;
+    for (int c = 0; c < n; ++c) {
+      const int on = keep[c] || r < n_text || c < n_text;
+      if (mask_out) mask_out[row * n + c] = (uint8_t)on;
+      if (on) {
+        if (cnt < max_cnt) kv_idx[row * max_cnt + cnt] = c;
+        ++cnt;
+      }
+    }
+    kv_cnt[row] = cnt < max_cnt ? cnt : max_cnt;
+  }
+  free(keys);
+  free(cum);
   free(keep);
 }
 

@@ -17,7 +17,9 @@ _SUBMODULES = (
     "utils",
     "utils.block_sparse_attn_kernel",
     "utils.merge_unmerge",
+    "utils.mask_related",
     "block_mask_attn",
+    "SparseGen_Plus",
     "combined_attn",
     "MergeAttention",
     "SildingTileAttention",
