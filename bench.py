@@ -120,6 +120,29 @@ def other_configs(q, k, v, dev):
                  "attn_tflops": _tflops(f3, ms3_attn), "sparsity": round(proc.sparsity(), 4),
                  "effective_tflop_per_call": round(f3 / 1e12, 4)}
 
+    # SparseGen_Plus on the C2 inputs (a sparse step after warm-up, schedule step 10):
+    # sampled block scores (num_keep 8) -> energy kv lists -> block-sparse attention.
+    from sparseattnfunctions_amd import SparseGen_Plus as sgp
+    from sparseattnfunctions_amd.utils.mask_related import calc_attn_block_sum_efficient
+
+    sg = sgp.BlockSparseAttention(warmup_epoch=0, verbose=False)
+    sg.counter = 10 * sg.layernum
+    sg.forward(q, k, v)
+    kvs = sg.mask[0]
+    thr = float(sg.energy_threshold_list[10])
+    fs = 4 * D * kvs.computed_pairs(L, L)
+    ms_est = time_fn(lambda: calc_attn_block_sum_efficient(q, k, num_keep=8), iters=10)
+    pooled = calc_attn_block_sum_efficient(q, k, num_keep=8)
+    ms_sel = time_fn(lambda: sgp.transfer_attn_to_kv_list(pooled, "energy", max_retain_ratio=sg.max_retain_ratio_list[10],
+                                                          min_retain_ratio=sg.min_retain_ratio_list[10],
+                                                          energy_threshold=thr), iters=10)
+    ms_attn = time_fn(lambda: block_sparse_attention(q, k, v, kvs, 0.125, n_text_blocks=4), iters=10)
+    ms_sg = time_fn(lambda: sg.forward(q, k, v), iters=10)
+    out["sparsegen_plus"] = {"ms": round(ms_sg, 4), "tflops": _tflops(fs, ms_sg), "estimator_ms": round(ms_est, 4),
+                             "energy_lists_ms": round(ms_sel, 4), "attn_ms": round(ms_attn, 4),
+                             "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
+                             "effective_tflop_per_call": round(fs / 1e12, 4)}
+
     # C4: token merging (seed 3), r = 4000 -> 13776 tokens, biased dense attention, unmerge.
     q4, k4, v4 = (t.to(dev) for t in cogvideox_qkv(3))
     mp = MergeAttention()
