@@ -143,6 +143,20 @@ def other_configs(q, k, v, dev):
                              "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
                              "effective_tflop_per_call": round(fs / 1e12, 4)}
 
+    # Sliding-tile attention (default config) on the C2 inputs: the fused call (query and
+    # output permutations inside the kernel) against permute-copies + attention + copy back.
+    from sparseattnfunctions_amd._kv import KVList
+    from sparseattnfunctions_amd.SildingTileAttention import SildingTileAttention
+
+    sta = SildingTileAttention()
+    sta(q, k, v)
+    lay = sta.block_mask
+    f_sta = 4 * D * B * H * KVList(lay.kv_idx, lay.kv_cnt, 1, 1, lay.nb, lay.nb).computed_pairs(L, L)
+    ms_sta = time_fn(lambda: sta(q, k, v), iters=10)
+    ms_sta_copies = time_fn(lambda: sta.process_out_back(sta.attention(*sta.preprocess(q, k, v))), iters=10)
+    out["sta"] = {"ms": round(ms_sta, 4), "tflops": _tflops(f_sta, ms_sta), "copies_ms": round(ms_sta_copies, 4),
+                  "block_density": round(lay.density(), 4), "block_tflop_per_call": round(f_sta / 1e12, 4)}
+
     # C4: token merging (seed 3), r = 4000 -> 13776 tokens, biased dense attention, unmerge.
     q4, k4, v4 = (t.to(dev) for t in cogvideox_qkv(3))
     mp = MergeAttention()

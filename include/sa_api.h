@@ -102,6 +102,32 @@ int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], 
                                  void* stream);
 
 /*
+ * Block-sparse attention over a remapped token layout, with the layout transform done by
+ * the kernel's own loads and stores instead of copies. Replaces the permute-attend-unpermute
+ * sequences of the reference: the sliding-tile layout (SildingTileAttention.py:111-143), the
+ * 1.5-5B rearranger/recover (combined_attn.py:17-41) and the per-frame pad/truncate of
+ * preprocess_qkv/reverse_process_out (utils/mask_related.py:87-187) on the query side.
+ * As sa_block_sparse_fwd_tilemask (kv_slot and tile_masks both NULL: plain lists) with an
+ * optional key_bias as in sa_block_sparse_fwd (not together with tile masks), plus:
+ *   q_rows    nullable int32 [Lq]: logical query i reads q row q_rows[i]; an entry outside
+ *             [0, q_src_rows) reads zeros (padding). NULL: q row i (q_src_rows ignored).
+ *   o_rows    nullable int32 [Lq]: logical query i is written to out row o_rows[i]; an entry
+ *             outside [0, o_dst_rows) is not written. NULL: out row i.
+ * Lq is the logical query count (the kv lists index its 64-row blocks); k/v are in the
+ * logical key order. The caller must not map two queries to one out row.
+ */
+int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                               const int64_t k_strides[3], const uint16_t* v,
+                               const int64_t v_strides[3], uint16_t* out,
+                               const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                               const int32_t* kv_idx, const int32_t* kv_cnt, const int32_t* kv_slot,
+                               int max_cnt, int lists_shared, const uint64_t* tile_masks,
+                               const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                               const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                               int o_dst_rows, const int32_t* work_order, int64_t n_slots,
+                               void* stream);
+
+/*
  * (host) Dispatch order of the attention work items (one per list row) for a GPU whose
  * workgroups are dealt round-robin to n_xcd XCDs (8 on MI355X): each XCD gets a
  * contiguous range of (b, h) heads, so their K/V stay in that XCD's L2, and within it the

@@ -2,12 +2,13 @@
 
 The reference permutes the video tokens into 13x3x3 tiles (:111-131), runs
 `flex_attention` with a BlockMask built from `sta_mask_3d` (:18-106) and permutes the
-output back (:135-143). Here the tile-major permutation is a token-gather kernel, and the
+output back (:135-143). Here k and v are copied into the tile-major order by a
+token-gather kernel, while the queries are read and the outputs written through the same
+permutation by the attention kernel itself (row maps, `sa_block_sparse_fwd_mapped`). The
 mask is compiled once per configuration (on the host, `sa_sta_block_masks`) into 64x64
 block lists shared by every head, with a bitmask for each block a tile boundary cuts
-through; the block-sparse kernel applies those bitmasks element-wise
-(`sa_block_sparse_fwd_tilemask`), so the result is the same token-level mask as
-flex_attention's.
+through; the block-sparse kernel applies those bitmasks element-wise, so the result is the
+same token-level mask as flex_attention's.
 
 Difference by design: `preprocess` returns permuted copies instead of writing the
 permutation into the caller's q, k, v (the reference mutates its inputs in place, :128-130).
@@ -21,7 +22,8 @@ import torch
 
 from . import _lib
 from ._gather import gather_tokens as _gather
-from .utils.block_sparse_attn_kernel import _prep_qkv, work_order
+from ._kv import KVList
+from .utils.block_sparse_attn_kernel import _prep_qkv, block_sparse_attention, work_order
 
 config = {
     "kernel_size": (1, 9, 9),
@@ -149,8 +151,18 @@ class SildingTileAttention:
         return out
 
     def forward(self, q, k, v):
-        q, k, v = self.preprocess(q, k, v)
-        return self.process_out_back(self.attention(q, k, v))
+        """preprocess -> attention -> process_out_back, with the query permutation and the
+        output's inverse permutation done by the attention kernel's loads and stores (row
+        maps); only k and v are copied into the tile-major layout."""
+        lay = self._get_layout(q.device)
+        B, H, L, D = q.shape
+        if L != lay.L or k.shape != q.shape or v.shape != q.shape:
+            raise ValueError(f"expected q, k, v of {lay.L} tokens for this configuration, got {tuple(q.shape)}")
+        kt, vt = _gather(k, lay.perm), _gather(v, lay.perm)
+        kv = KVList(lay.kv_idx, lay.kv_cnt, 1, 1, lay.nb, lay.nb)
+        return block_sparse_attention(q, kt, vt, kv, 1.0 / math.sqrt(D), n_text_blocks=lay.text_blocks,
+                                      q_rows=lay.perm, o_rows=lay.perm,
+                                      tile_masks=(lay.kv_slot, lay.masks, True))
 
     def __call__(self, *args, **kwds):
         return self.forward(*args, **kwds)

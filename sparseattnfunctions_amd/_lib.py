@@ -42,6 +42,11 @@ _PROTOTYPES = {
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _F, _P,
          ctypes.c_int64, _P],
     ),
+    "sa_block_sparse_fwd_mapped": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P, _I64P, _F,
+         _P, _I, _P, _I, _P, ctypes.c_int64, _P],
+    ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
     "sa_sta_permutation": (_I, [_I, _I, _I, _I, _P, _P]),
     "sa_sta_block_masks": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),

@@ -80,6 +80,9 @@ struct FwdArgs {
   int list_bh_stride;          // list row = bh * list_bh_stride + qb (0: lists shared by heads)
   const int32_t* kv_slot;      // [rows][max_cnt] tile-mask slot of each entry, -1 = full tile
   const uint64_t* tile_masks;  // [slots][64] bit k of row r: query r may attend key k
+  const int32_t* q_rows;       // [Lq] q row of query i (outside [0, q_src_rows): zeros); null = i
+  const int32_t* o_rows;       // [Lq] out row of query i (outside [0, o_dst_rows): dropped); null = i
+  int q_src_rows, o_dst_rows;
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
@@ -241,14 +244,24 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   }
 
   // Q^T B operands: qf[g][s] = q[qb*64 + 32g + col][16s + 8hh .. +7] (rows clamped into Lq;
-  // clamped rows are never stored).
+  // clamped rows are never stored). With a row map, query i reads q row q_rows[i] (zeros
+  // when that is outside the tensor: padding rows of a remapped layout).
   sa_bf16x8 qf[2][4];
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    const int row = min(qb * kBlock + 32 * g + col, a.Lq - 1);
+    int row = min(qb * kBlock + 32 * g + col, a.Lq - 1);
+    bool zero = false;
+    if (a.q_rows) {
+      row = a.q_rows[row];
+      zero = (unsigned)row >= (unsigned)a.q_src_rows;
+      row = zero ? 0 : row;
+    }
     const uint16_t* p = qbase + (int64_t)row * a.q_sl + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[g][s] = as_bf16x8(*reinterpret_cast<const uint4*>(p + 16 * s));
+    for (int s = 0; s < 4; ++s) {
+      const uint4 w = *reinterpret_cast<const uint4*>(p + 16 * s);
+      qf[g][s] = as_bf16x8(zero ? make_uint4(0u, 0u, 0u, 0u) : w);
+    }
   }
 
   sa_f32x16 acc[2][2];  // [dc][g]
@@ -495,8 +508,13 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   for (int g = 0; g < 2; ++g) {
     const float l_tot = xhalf_sum(l[g]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const int row = qb * kBlock + 32 * g + col;
-    if (row < a.Lq) {
+    int row = qb * kBlock + 32 * g + col;
+    bool store = row < a.Lq;
+    if (store && a.o_rows) {  // remapped layout: query i goes to out row o_rows[i]
+      row = a.o_rows[row];
+      store = (unsigned)row < (unsigned)a.o_dst_rows;
+    }
+    if (store) {
       uint16_t* orow = obase + (int64_t)row * a.o_sl;
 #pragma unroll
       for (int dc = 0; dc < 2; ++dc) {
@@ -558,7 +576,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                int H, int Lq, int Lk, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
                bool lists_shared, const int32_t* kv_slot, const uint64_t* tile_masks, const float* key_bias,
                const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
-               void* stream, const char* fn) {
+               const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
+               const char* fn) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -568,6 +587,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   const int nkb = sa::cdiv(Lk, kBlock);
   SA_REQUIRE(max_cnt > 0, "%s: max_cnt must be > 0", fn);
   SA_REQUIRE(!key_bias || bias_strides, "%s: key_bias without bias_strides", fn);
+  SA_REQUIRE(!q_rows || q_src_rows > 0, "%s: q_rows given with q_src_rows=%d", fn, q_src_rows);
+  SA_REQUIRE(!o_rows || o_dst_rows > 0, "%s: o_rows given with o_dst_rows=%d", fn, o_dst_rows);
   const int64_t n_items = (int64_t)B * H * nqb;
   SA_REQUIRE(n_items < (1LL << 30), "%s: too many query blocks", fn);
   if (work_order) {
@@ -614,6 +635,10 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.list_bh_stride = lists_shared ? 0 : nqb;
   a.kv_slot = kv_slot;
   a.tile_masks = tile_masks;
+  a.q_rows = q_rows;
+  a.o_rows = o_rows;
+  a.q_src_rows = q_rows ? q_src_rows : Lq;
+  a.o_dst_rows = o_rows ? o_dst_rows : Lq;
 
   hipStream_t s = sa::as_stream(stream);
   const dim3 g((unsigned)grid), blk(64 * kWaves);
@@ -637,8 +662,8 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
                                    const float* key_bias, const int64_t bias_strides[2], float sm_scale,
                                    const int32_t* work_order, int64_t n_slots, void* stream) {
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
-                    max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, stream,
-                    "sa_block_sparse_fwd");
+                    max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
+                    0, nullptr, 0, stream, "sa_block_sparse_fwd");
 }
 
 extern "C" int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
@@ -651,5 +676,19 @@ extern "C" int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_s
   SA_REQUIRE(kv_slot && tile_masks, "sa_block_sparse_fwd_tilemask: null kv_slot/tile_masks");
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, lists_shared != 0, kv_slot, tile_masks, nullptr, nullptr, sm_scale, work_order, n_slots,
-                    stream, "sa_block_sparse_fwd_tilemask");
+                    nullptr, 0, nullptr, 0, stream, "sa_block_sparse_fwd_tilemask");
+}
+
+extern "C" int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                          const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                          uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                          int D, const int32_t* kv_idx, const int32_t* kv_cnt, const int32_t* kv_slot,
+                                          int max_cnt, int lists_shared, const uint64_t* tile_masks,
+                                          const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                          const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                                          int o_dst_rows, const int32_t* work_order, int64_t n_slots, void* stream) {
+  SA_REQUIRE(!kv_slot == !tile_masks, "sa_block_sparse_fwd_mapped: kv_slot and tile_masks go together");
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, lists_shared != 0, kv_slot, tile_masks, key_bias, bias_strides, sm_scale, work_order,
+                    n_slots, q_rows, q_src_rows, o_rows, o_dst_rows, stream, "sa_block_sparse_fwd_mapped");
 }

@@ -57,24 +57,49 @@ def work_order(B: int, H: int, nqb: int, n_text_blocks: int, device) -> torch.Te
     return order
 
 
+def _row_map(rows, device):
+    if rows is None:
+        return None
+    if rows.dim() != 1:
+        raise ValueError("row maps must be 1-D int32 tensors")
+    return rows.to(device=device, dtype=torch.int32).contiguous()
+
+
 def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None,
-                           n_text_blocks: int = 0):
+                           n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
     q [B,H,Lq,64], k/v [B,H,Lk,64] bf16 on the GPU; key_bias optional fp32 [B,H,Lk] (any
     strides with a contiguous key axis, stride 0 to broadcast). `n_text_blocks` only
     affects scheduling (those block rows are dispatched first).
+
+    Layout remapping inside the kernel (no copies): with `q_rows` (int32 [n]) the attention
+    runs over n logical query rows, row i reading q's row q_rows[i] (zeros outside q); with
+    `o_rows` (int32 [n]) logical row i is written to out row o_rows[i] (dropped outside
+    out). `tile_masks` = (kv_slot [rows, max_cnt] int32, masks uint64 [slots, 64],
+    lists_shared) adds token-level masks inside cut blocks.
     """
     _lib.require_gpu(q, k, v)
     q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
-    B, H, Lq, D = q.shape
+    B, H, Lsrc, D = q.shape
+    q_rows, o_rows = _row_map(q_rows, q.device), _row_map(o_rows, q.device)
+    Lq = q_rows.numel() if q_rows is not None else (o_rows.numel() if o_rows is not None else Lsrc)
+    if q_rows is None and o_rows is not None and o_rows.numel() != Lsrc:
+        raise ValueError("o_rows without q_rows must have one entry per q row")
+    if q_rows is not None and o_rows is not None and o_rows.numel() != Lq:
+        raise ValueError("q_rows and o_rows must have the same length")
     Lk = k.shape[2]
     if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
         raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
-    if kv.rows != B * H * math.ceil(Lq / BLOCK):
-        raise ValueError(f"kv list has {kv.rows} rows, expected {B * H * math.ceil(Lq / BLOCK)}")
+    lists_shared = tile_masks is not None and tile_masks[2]
+    want_rows = (1 if lists_shared else B * H) * math.ceil(Lq / BLOCK)
+    if kv.rows != want_rows:
+        raise ValueError(f"kv list has {kv.rows} rows, expected {want_rows}")
     if out is None:
-        out = torch.empty_like(q)
+        out = torch.empty_like(q) if o_rows is not None else torch.empty(B, H, Lq, D, dtype=q.dtype,
+                                                                          device=q.device)
+    elif out.shape[:2] != (B, H) or out.shape[3] != D or (o_rows is None and out.shape[2] != Lq):
+        raise ValueError(f"out has shape {tuple(out.shape)}")
     bias_ptr, bias_strides = None, None
     if key_bias is not None:
         if key_bias.dtype != torch.float32 or key_bias.shape[-1] != Lk or key_bias.stride(-1) != 1:
@@ -83,6 +108,18 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
         bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
     order = work_order(B, H, math.ceil(Lq / BLOCK), n_text_blocks, q.device)
     lib = _lib.load()
+    if q_rows is not None or o_rows is not None or tile_masks is not None:
+        kv_slot, masks = (tile_masks[0], tile_masks[1]) if tile_masks is not None else (None, None)
+        with torch.cuda.device(q.device):
+            rc = lib.sa_block_sparse_fwd_mapped(
+                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
+                B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), _lib.ptr(kv_slot), kv.max_cnt,
+                int(bool(lists_shared)), _lib.ptr(masks), bias_ptr, bias_strides, float(sm_scale),
+                _lib.ptr(q_rows), Lsrc, _lib.ptr(o_rows), out.shape[2], order.data_ptr(), order.numel(),
+                _lib.stream_of(q))
+        _lib.check(rc, "sa_block_sparse_fwd_mapped")
+        return out
     with torch.cuda.device(q.device):
         rc = lib.sa_block_sparse_fwd(
             q.data_ptr(), _lib.i64(*q.stride()[:3]),
