@@ -253,7 +253,13 @@ int sa_sta_block_masks(int text_len, int T, int Hp, int Wp, const int tile[3], c
                        int32_t* kv_idx, int32_t* kv_cnt, int32_t* kv_slot, uint64_t* masks,
                        int* n_slots);
 
-/* Token gather out[b,h,j] = x[b,h,idx[j]] for j < L_out (layout permutations). */
+/*
+ * Token gather out[b,h,j] = x[b,h,idx[j]] for j < L_out; an index outside [0, L_in) gives a
+ * zero row. Serves the layout transforms that are copies: the sliding-tile order of k and v
+ * (SildingTileAttention.py:111-131), the 1.5-5B rearranger/recover (combined_attn.py:17-41),
+ * replicate padding (utils/mask_related.py:2-13) and preprocess_qkv/reverse_process_out
+ * (utils/mask_related.py:87-187).
+ */
 int sa_gather_tokens(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L_in, int D,
                      const int32_t* idx, int L_out, uint16_t* out, const int64_t out_strides[3],
                      void* stream);

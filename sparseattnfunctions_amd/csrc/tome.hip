@@ -653,8 +653,8 @@ extern "C" int sa_tome_unmerge(const uint16_t* xm, const int64_t xm_strides[3], 
 // SildingTileAttention.py:111-143 and the 1.5-5B rearranger of combined_attn.py:17-41).
 namespace {
 __global__ __launch_bounds__(256) void gather_tokens_kernel(const uint16_t* x, int64_t x_sb, int64_t x_sh,
-                                                            int64_t x_sl, const int32_t* idx, int L_out, int H,
-                                                            int64_t rows, uint16_t* out, int64_t o_sb,
+                                                            int64_t x_sl, int L_in, const int32_t* idx, int L_out,
+                                                            int H, int64_t rows, uint16_t* out, int64_t o_sb,
                                                             int64_t o_sh, int64_t o_sl) {
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
   if (row >= rows) return;
@@ -662,7 +662,10 @@ __global__ __launch_bounds__(256) void gather_tokens_kernel(const uint16_t* x, i
   const int64_t bh = row / L_out;
   const int j = (int)(row - bh * L_out);
   const int64_t b = bh / H, h = bh - b * H;
-  const uint4 w = *reinterpret_cast<const uint4*>(x + b * x_sb + h * x_sh + (int64_t)idx[j] * x_sl + 8 * c8);
+  const int src = idx[j];
+  uint4 w = make_uint4(0u, 0u, 0u, 0u);  // an index outside [0, L_in) gives a zero row (padding)
+  if ((unsigned)src < (unsigned)L_in)
+    w = *reinterpret_cast<const uint4*>(x + b * x_sb + h * x_sh + (int64_t)src * x_sl + 8 * c8);
   *reinterpret_cast<uint4*>(out + b * o_sb + h * o_sh + (int64_t)j * o_sl + 8 * c8) = w;
 }
 }  // namespace
@@ -679,7 +682,7 @@ extern "C" int sa_gather_tokens(const uint16_t* x, const int64_t x_strides[3], i
     if (x_strides[i] % 8 || out_strides[i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "sa_gather_tokens: strides must be multiples of 8");
   const int64_t rows = (int64_t)B * H * L_out;
   hipLaunchKernelGGL(gather_tokens_kernel, dim3(grid256(rows * 8)), dim3(256), 0, sa::as_stream(stream), x,
-                     x_strides[0], x_strides[1], x_strides[2], idx, L_out, H, rows, out, out_strides[0],
+                     x_strides[0], x_strides[1], x_strides[2], L_in, idx, L_out, H, rows, out, out_strides[0],
                      out_strides[1], out_strides[2]);
   return sa::check_launch("sa_gather_tokens");
 }
