@@ -223,6 +223,58 @@ int sa_energy_kv_list(const float* scores, int BH, int nqb, int nkb, int mode, f
                       int max_cnt, int32_t* kv_cnt, uint8_t* mask_out, void* stream);
 
 /*
+ * Per-head token gather out[b,h,j] = x[b,h, idx[(b*H + h)*L_out + j]] (zero row outside
+ * [0, L_in)). Replaces the per-head query-frame gather gather_q_chunk of the pattern
+ * attention (partern_attention.py:379-385, torch.gather with per-head frame indices).
+ */
+int sa_gather_tokens_heads(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L_in,
+                           int D, const int32_t* idx, int L_out, uint16_t* out,
+                           const int64_t out_strides[3], void* stream);
+
+/*
+ * Frame maps of the pattern attention (get_weight_for_patch, partern_attention.py:336-356)
+ * from the sampled attention's segment masses map_mass [B,H,F*ns,>=F+1] (bf16; row = sampled
+ * video query, column 0 = mass on the text keys, 1 + f = mass on frame f's samples):
+ *   img2text[bh][f] = sum of column 0 over frame f's ns rows / ns      (fp32 [B*H][F])
+ *   img2img[bh][f1][f2] = sum of column 1 + f2 over frame f1's rows / ns (fp32 [B*H][F][F])
+ */
+int sa_pattern_maps(const uint16_t* map_mass, const int64_t map_strides[3], int B, int H, int F,
+                    int ns, float* img2text, float* img2img, void* stream);
+
+/*
+ * Per-head plan of the pattern attention (partern_attention.py:215-276, 393-430) from the
+ * first-frame masses ff_mass [B,H,S,>=F+1] (bf16; column 0 text, 1 + i frame i) and img2img:
+ *   stats   fp32 [B*H][F+1][3]: sum, min, max of each mass column over the S rows;
+ *   fac     fp32 [B*H][F+1][4]: the modify factor x -> constrained_mod_factor(x / mean(x))
+ *           as {1/mean, alpha, beta, mode} (mode 0 unchanged, 1 clamp, 2 clamp(alpha x + beta)),
+ *           bounds [lo_text, hi_text] for column 0 and [lo_frame, hi_frame] for the frames,
+ *           the "any head out of range" decision taken over all B*H heads per column;
+ *   frame_case int32 [B*H][F]: 1 if img2img[0][i] >= map_thr (first-frame masses are used
+ *           for key frame i), else 0 (queries of frame argmax_f img2img[f][i]);
+ *   inv_map0 fp32 [B*H][F]: 1 / img2img[0][i];
+ *   q_idx   int32 [B*H][F*S]: query token T + frame*S + r of selected row i*S + r.
+ */
+int sa_pattern_plan(const uint16_t* ff_mass, const int64_t ff_strides[3], const float* img2img,
+                    int B, int H, int F, int S, int T, float lo_text, float hi_text,
+                    float lo_frame, float hi_frame, float map_thr, float* stats, float* fac,
+                    int32_t* frame_case, float* inv_map0, int32_t* q_idx, void* stream);
+
+/*
+ * Final mix of the pattern attention (partern_attention.py:455-460): for video row f1*S + r,
+ *   out[T + f1*S + r] = sum_i img2img[f1][i] * s_i(r) * o_frames[i*S + r]
+ *                       + img2text[f1] * mft(r) * o_text[f1*S + r]
+ * with s_i(r) the frame-i modify factor (frame_case 0) or ff_mass[r][1+i] * inv_map0[i]
+ * (frame_case 1) and mft(r) the text modify factor, both from fac. Rows < T of out are not
+ * touched. o_frames/o_text [B,H,F*S,64], out [B,H,T+F*S,64] bf16; F <= 16.
+ */
+int sa_pattern_combine(const uint16_t* o_frames, const int64_t of_strides[3], const uint16_t* o_text,
+                       const int64_t ot_strides[3], const uint16_t* ff_mass,
+                       const int64_t ff_strides[3], const float* img2text, const float* img2img,
+                       const float* fac, const int32_t* frame_case, const float* inv_map0, int B,
+                       int H, int F, int S, int T, float lo_text, float hi_text, float lo_frame,
+                       float hi_frame, uint16_t* out, const int64_t out_strides[3], void* stream);
+
+/*
  * (host) Static local 3-D window of the combined mask, one byte per (query block, key
  * block): 1 iff both blocks are video blocks and their centre tokens (index
  * block*qb + block/2, clamped to L-1) lie within +-dt latent frames, +-dh patch rows and

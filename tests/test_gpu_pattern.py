@@ -1,0 +1,76 @@
+"""GPU parity of the frame-pattern attention (ParternAttentionColVersion_V2) against the fp64
+oracle at a reduced geometry (11 frames of 6 x 10 tokens, 16 text tokens, 20 samples) and
+a smoke run at the reference's 1.5-5B geometry.
+
+Tolerances: frame maps atol 3e-3 (sums of bf16-rounded masses); per-head choices (query
+frame case per key frame) exact where the oracle's decision margin exceeds 1e-2; outputs
+max-abs 3e-2 and mean-abs 3e-3 against the fp64 oracle (bf16 attention outputs are mixed
+with up to 11 weights each).
+"""
+import pytest
+import torch
+
+from conftest import case
+from oracle import pattern as opat
+from sparseattnfunctions_amd import partern_attention as pa
+
+pytestmark = pytest.mark.gpu
+
+G = pa.PatternGeometry(frames=11, height=6, width=10, text_length=16, sample_num=20)
+
+
+def _inputs(seed, B=1, H=4, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    shape = (B, H, G.L, 64)
+    # frames share a common component so the maps are not flat
+    base = torch.randn(B, H, G.S, 64, generator=g)
+    def mk():
+        x = torch.randn(shape, generator=g) * 0.7
+        x[:, :, G.text_length:] += base.repeat(1, 1, G.frames, 1)
+        return (x * scale).to(torch.bfloat16)
+    return mk(), mk(), mk()
+
+
+def test_maps_match_oracle(dev):
+    case("pattern maps")
+    q, k, _ = _inputs(1)
+    _, idx = pa.get_indexs(G)
+    p = idx[G.text_length: G.text_length + G.sample_num] - G.text_length
+    i2i, i2t = pa.ParternAttentionColVersion_V2(G).get_weight_for_patch(q.to(dev), k.to(dev), idx)
+    w_i2i, w_i2t = opat.weight_for_patch(q, k, p, G.frames, G.S, G.text_length)
+    assert torch.allclose(i2i.cpu().double(), w_i2i, atol=3e-3)
+    assert torch.allclose(i2t.cpu().double(), w_i2t, atol=3e-3)
+
+
+@pytest.mark.parametrize("seed", [2, 3])
+def test_forward_matches_oracle(dev, seed):
+    case(f"pattern forward seed={seed}")
+    q, k, v = _inputs(seed)
+    torch.manual_seed(seed)
+    _, idx = pa.get_indexs(G)
+    p = idx[G.text_length: G.text_length + G.sample_num] - G.text_length
+    proc = pa.ParternAttentionColVersion_V2(G)
+    out = proc(q.to(dev), k.to(dev), v.to(dev), index_k=idx).cpu()
+    want, parts = opat.pattern_v2(q, k, v, p, G.frames, G.S, G.text_length, return_parts=True)
+    # decisions: case per (head, key frame) where the oracle's map[0][i] is not within 1e-2 of 0.1
+    m0 = parts["i2i"][:, :, 0, :]
+    firm = (m0 - 0.1).abs() > 1e-2
+    got_case = proc.last_plan["frame_case"].cpu().bool()
+    assert torch.equal(got_case[firm], parts["cases"][firm])
+    err = (out.double() - want).abs()
+    assert torch.isfinite(out.float()).all()
+    assert err.max().item() <= 3e-2, err.max().item()
+    assert err.mean().item() <= 3e-3, err.mean().item()
+
+
+def test_reference_geometry_smoke(dev):
+    # 1.5-5B geometry, 2 heads: runs, finite, text rows equal dense attention of the text rows.
+    case("pattern forward 1.5-5B geometry")
+    g = pa.DEFAULT
+    gen = torch.Generator(device=dev).manual_seed(4)
+    q, k, v = (torch.randn(1, 2, g.L, 64, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
+    out = pa.ParternAttentionColVersion_V2()(q, k, v)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and torch.isfinite(out.float()).all()
+    ref = torch.softmax(q[0, :, :g.text_length].float() @ k[0].float().transpose(-1, -2) / 8, dim=-1) @ v[0].float()
+    assert (out[0, :, :g.text_length].float() - ref).abs().max().item() <= 2e-2
