@@ -1,0 +1,357 @@
+// Head routing of the 1.5-5B pattern attention (unified_judge, partern_attention.py:464-521)
+// for gfx950.
+//
+//   probs_kernel       one wave per (head, 32 sampled query rows): S^T = K Q^T with
+//                      v_mfma_f32_32x32x16_bf16 over all sampled keys (optional additive bias
+//                      on the first keys), row max and sum in a first pass, then the
+//                      probabilities of a key range written row-major (through LDS, 128-byte
+//                      rows) in a second pass;
+//   share_kernel       judge_sparsity (:470-479): per query row, the probability mass of its
+//                      K largest entries (K-th largest found by a 32-step search on the fp32
+//                      bit patterns), one workgroup per row;
+//   gram_kernel        judge_similarity (:480-514): for key frame f2, the Gram matrix
+//                      G[f1][f3] = sum_{s1,s2} P[f1 s1][f2 s2] * P[f3 s1][f2 s2] of the
+//                      frame-pair patterns (their inner products and norms);
+//   finish_kernel      per head: mean share > 0.9 (sparse), mean cosine similarity of the
+//                      patterns sharing a key frame > 0.9 (twice), and the routing decision.
+#include <cmath>
+
+#include "sa_common.h"
+
+namespace {
+
+constexpr int kD = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef unsigned jd_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline sa_f32x16 score_tile(const uint16_t* kp, const sa_bf16x8 (&qf)[4]) {
+  jd_u32x4 kop[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kop[s] = *reinterpret_cast<const jd_u32x4*>(kp + 16 * s);
+  sa_f32x16 t = {};
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(sa_bf16x8, kop[s]), qf[s], t, 0, 0, 0);
+  return t;
+}
+
+// ---------------------------------------------------------------------------------------
+struct ProbArgs {
+  const uint16_t* qs;  // [BH][rows_pad][64]
+  const uint16_t* ks;  // [BH][keys_pad][64]
+  int rows, rows_pad, keys, keys_pad;
+  float scale_log2;
+  int n_bias;
+  float bias_log2;     // added to keys < n_bias (log2 domain)
+  int c_lo, c_hi;      // key range written
+  float* P;            // P[bh*p_bh + r*p_row + (key - c_lo)]
+  int64_t p_bh, p_row;
+  int ng;              // rows_pad / 32
+  int64_t total;       // BH * ng
+};
+
+__global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
+  __shared__ float tile[4][32][33];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
+  if (wid >= a.total) return;  // no workgroup barriers below
+  const int64_t bh = wid / a.ng;
+  const int g = (int)(wid - bh * a.ng);
+  const int col = lane & 31, hh = lane >> 5;
+  sa_bf16x8 qf[4];
+  {
+    const uint16_t* qp = a.qs + (bh * a.rows_pad + 32 * g + col) * kD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(sa_bf16x8, *reinterpret_cast<const jd_u32x4*>(qp + 16 * s));
+  }
+  const uint16_t* kbase = a.ks + (bh * a.keys_pad + col) * kD + 8 * hh;
+  auto logit = [&](const sa_f32x16& t, int kt, int i) {
+    const int key = 32 * kt + 8 * (i >> 2) + 4 * hh + (i & 3);
+    if (key >= a.keys) return -INFINITY;
+    return t[i] * a.scale_log2 + (key < a.n_bias ? a.bias_log2 : 0.f);
+  };
+  float m = -INFINITY, l = 0.f;
+  for (int kt = 0; kt < a.keys_pad / 32; ++kt) {
+    const sa_f32x16 t = score_tile(kbase + (int64_t)kt * 32 * kD, qf);
+    float x[16], tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = logit(t, kt, i);
+      tmax = fmaxf(tmax, x[i]);
+    }
+    const float mn = fmaxf(m, tmax);
+    if (mn != -INFINITY) {
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sum += __builtin_amdgcn_exp2f(x[i] - mn);
+      l = l * __builtin_amdgcn_exp2f(m - mn) + sum;
+      m = mn;
+    }
+  }
+  {
+    const auto mo = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    const auto lo = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    const float m0 = __uint_as_float(mo[0]), m1 = __uint_as_float(mo[1]);
+    const float M = fmaxf(m0, m1);
+    l = __uint_as_float(lo[0]) * __builtin_amdgcn_exp2f(m0 - M) + __uint_as_float(lo[1]) * __builtin_amdgcn_exp2f(m1 - M);
+    m = M;
+  }
+  const float inv = 1.f / l;
+  const int row0 = 32 * g;
+  for (int kt = a.c_lo / 32; kt * 32 < a.c_hi; ++kt) {
+    const sa_f32x16 t = score_tile(kbase + (int64_t)kt * 32 * kD, qf);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      tile[wave][col][8 * (i >> 2) + 4 * hh + (i & 3)] = __builtin_amdgcn_exp2f(logit(t, kt, i) - m) * inv;
+    __builtin_amdgcn_wave_barrier();
+    // lanes 2r, 2r+1 write keys 0..15 / 16..31 of row r
+    const int r = lane >> 1, half = lane & 1;
+    if (row0 + r < a.rows) {
+      float* dst = a.P + bh * a.p_bh + (int64_t)(row0 + r) * a.p_row;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = 32 * kt + 16 * half + j;
+        if (key >= a.c_lo && key < a.c_hi) dst[key - a.c_lo] = tile[wave][r][16 * half + j];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// share_kernel: one workgroup per (bh, row) over n probabilities (n <= 16384, in LDS).
+struct ShareArgs {
+  const float* P;
+  int64_t p_bh, p_row;
+  int rows, n, K;
+  float* share;  // [BH][rows]
+  int64_t total;
+};
+
+__global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
+  __shared__ uint32_t v[16384];
+  __shared__ uint32_t red_u[256];
+  __shared__ float red_f[256];
+  const int64_t w = blockIdx.x;
+  if (w >= a.total) return;
+  const int t = threadIdx.x;
+  const int64_t bh = w / a.rows;
+  const int r = (int)(w - bh * a.rows);
+  const float* src = a.P + bh * a.p_bh + (int64_t)r * a.p_row;
+  for (int i = t; i < a.n; i += 256) v[i] = __float_as_uint(src[i]);  // p >= 0: bits order as values
+  __syncthreads();
+  // K-th largest bit pattern: largest thr with #{v >= thr} >= K.
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    uint32_t c = 0;
+    for (int i = t; i < a.n; i += 256) c += v[i] >= cand;
+    red_u[t] = c;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+      if (t < s) red_u[t] += red_u[t + s];
+      __syncthreads();
+    }
+    if (red_u[0] >= (uint32_t)a.K) thr = cand;
+    __syncthreads();
+  }
+  // Mass above thr, plus thr for the ties needed to make K.
+  float s = 0.f;
+  uint32_t gt = 0;
+  for (int i = t; i < a.n; i += 256) {
+    if (v[i] > thr) {
+      s += __uint_as_float(v[i]);
+      ++gt;
+    }
+  }
+  red_f[t] = s;
+  red_u[t] = gt;
+  __syncthreads();
+  for (int k = 128; k > 0; k >>= 1) {
+    if (t < k) {
+      red_f[t] += red_f[t + k];
+      red_u[t] += red_u[t + k];
+    }
+    __syncthreads();
+  }
+  if (t == 0) a.share[bh * a.rows + r] = red_f[0] + (float)((int)a.K - (int)red_u[0]) * __uint_as_float(thr);
+}
+
+// ---------------------------------------------------------------------------------------
+// gram_kernel: one workgroup per (bh, key frame f2). P rows f1*ns + s1 (video sample rows),
+// columns f2*ns + s2 (video sample columns).
+struct GramArgs {
+  const float* P;
+  int64_t p_bh, p_row;
+  int ns;
+  float* G;  // [BH][F][F*(F+1)/2]
+  int64_t total;
+};
+
+template <int F>
+__global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
+  constexpr int NP = F * (F + 1) / 2;
+  __shared__ float rows[F][512];
+  __shared__ float red[256];
+  const int64_t w = blockIdx.x;
+  if (w >= a.total) return;
+  const int t = threadIdx.x;
+  const int64_t bh = w / F;
+  const int f2 = (int)(w - bh * F);
+  float acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) acc[p] = 0.f;
+  const float* base = a.P + bh * a.p_bh + (int64_t)f2 * a.ns;
+  for (int s1 = 0; s1 < a.ns; ++s1) {
+    __syncthreads();
+    for (int e = t; e < F * a.ns; e += 256) {
+      const int f1 = e / a.ns, s2 = e - f1 * a.ns;
+      rows[f1][s2] = base[(int64_t)(f1 * a.ns + s1) * a.p_row + s2];
+    }
+    __syncthreads();
+    for (int s2 = t; s2 < a.ns; s2 += 256) {
+      float x[F];
+#pragma unroll
+      for (int f1 = 0; f1 < F; ++f1) x[f1] = rows[f1][s2];
+      int p = 0;
+#pragma unroll
+      for (int f1 = 0; f1 < F; ++f1)
+#pragma unroll
+        for (int f3 = f1; f3 < F; ++f3) {
+          acc[p] = fmaf(x[f1], x[f3], acc[p]);
+          ++p;
+        }
+    }
+  }
+  float* out = a.G + (bh * F + f2) * NP;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    __syncthreads();
+    red[t] = acc[p];
+    __syncthreads();
+    for (int k = 128; k > 0; k >>= 1) {
+      if (t < k) red[t] += red[t + k];
+      __syncthreads();
+    }
+    if (t == 0) out[p] = red[0];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+struct FinishArgs {
+  const float* share;  // [BH][rows]
+  const float* G1;     // [BH][F][NP]
+  const float* G2;
+  int BH, rows, F;
+  float sparse_thr, sim_thr;
+  float* share_mean;  // [BH]
+  float* col1;        // [BH]
+  float* col2;        // [BH]
+  int32_t* use;       // [BH]
+};
+
+__device__ inline float col_sim(const float* G, int F) {
+  const int NP = F * (F + 1) / 2;
+  float tot = 0.f;
+  for (int f2 = 0; f2 < F; ++f2) {
+    const float* g = G + f2 * NP;
+    auto at = [&](int i, int j) {  // i <= j: pair index of (i, j) in row-major upper triangle
+      if (i > j) { const int tmp = i; i = j; j = tmp; }
+      return g[i * F - i * (i - 1) / 2 + (j - i)];
+    };
+    float s = 0.f;
+    for (int f1 = 0; f1 < F; ++f1)
+      for (int f3 = 0; f3 < F; ++f3) s += at(f1, f3) / sqrtf(at(f1, f1) * at(f3, f3));
+    tot += s / (float)(F * F);
+  }
+  return tot / (float)F;
+}
+
+__global__ __launch_bounds__(64) void finish_kernel(FinishArgs a) {
+  const int bh = blockIdx.x * 64 + threadIdx.x;
+  if (bh >= a.BH) return;
+  float s = 0.f;
+  if (a.share) {
+    for (int r = 0; r < a.rows; ++r) s += a.share[(int64_t)bh * a.rows + r];
+    s /= (float)a.rows;
+  }
+  const int NP = a.F * (a.F + 1) / 2;
+  const float c1 = a.G1 ? col_sim(a.G1 + (int64_t)bh * a.F * NP, a.F) : 0.f;
+  const float c2 = a.G2 ? col_sim(a.G2 + (int64_t)bh * a.F * NP, a.F) : 0.f;
+  a.share_mean[bh] = s;
+  a.col1[bh] = c1;
+  a.col2[bh] = c2;
+  a.use[bh] = (!(s > a.sparse_thr) && c1 > a.sim_thr && c2 > a.sim_thr) ? 1 : 0;
+}
+
+}  // namespace
+
+extern "C" int sa_sampled_probs(const uint16_t* q_rows, const uint16_t* k_rows, int BH, int rows, int rows_pad,
+                                int keys, int keys_pad, float sm_scale, int n_bias, float bias, int c_lo, int c_hi,
+                                float* P, int64_t p_bh_stride, int64_t p_row_stride, void* stream) {
+  const char* fn = "sa_sampled_probs";
+  SA_REQUIRE(q_rows && k_rows && P, "%s: null pointer", fn);
+  SA_REQUIRE(BH > 0 && rows > 0 && keys > 0, "%s: bad shape", fn);
+  SA_REQUIRE(rows_pad % 32 == 0 && rows_pad >= rows && keys_pad % 32 == 0 && keys_pad >= keys,
+             "%s: rows_pad/keys_pad must be multiples of 32 covering rows/keys", fn);
+  SA_REQUIRE(0 <= c_lo && c_lo < c_hi && c_hi <= keys, "%s: bad key range [%d, %d)", fn, c_lo, c_hi);
+  SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f, "%s: bad sm_scale", fn);
+  SA_REQUIRE(p_row_stride >= c_hi - c_lo, "%s: p_row_stride too small", fn);
+  ProbArgs a;
+  a.qs = q_rows; a.ks = k_rows; a.rows = rows; a.rows_pad = rows_pad; a.keys = keys; a.keys_pad = keys_pad;
+  a.scale_log2 = sm_scale * kLog2e; a.n_bias = n_bias; a.bias_log2 = bias * kLog2e;
+  a.c_lo = c_lo; a.c_hi = c_hi; a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride;
+  a.ng = rows_pad / 32; a.total = (int64_t)BH * a.ng;
+  hipLaunchKernelGGL(probs_kernel, dim3((unsigned)((a.total + 3) / 4)), dim3(256), 0, sa::as_stream(stream), a);
+  return sa::check_launch(fn);
+}
+
+extern "C" int sa_topk_share(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int rows, int n,
+                             int K, float* share, void* stream) {
+  const char* fn = "sa_topk_share";
+  SA_REQUIRE(P && share, "%s: null pointer", fn);
+  SA_REQUIRE(BH > 0 && rows > 0 && n > 0 && K >= 1 && K <= n, "%s: bad shape (1 <= K <= n)", fn);
+  if (n > 16384) return sa::fail(SA_ERR_UNSUPPORTED, "%s: n=%d > 16384", fn, n);
+  ShareArgs a;
+  a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride; a.rows = rows; a.n = n; a.K = K; a.share = share;
+  a.total = (int64_t)BH * rows;
+  hipLaunchKernelGGL(share_kernel, dim3((unsigned)a.total), dim3(256), 0, sa::as_stream(stream), a);
+  return sa::check_launch(fn);
+}
+
+extern "C" int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int F, int ns,
+                               float* G, void* stream) {
+  const char* fn = "sa_pattern_gram";
+  SA_REQUIRE(P && G, "%s: null pointer", fn);
+  SA_REQUIRE(BH > 0 && ns > 0 && ns <= 512, "%s: bad shape (ns <= 512)", fn);
+  SA_REQUIRE(F >= 1 && F <= 12, "%s: frames %d outside [1, 12]", fn, F);
+  GramArgs a;
+  a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride; a.ns = ns; a.G = G; a.total = (int64_t)BH * F;
+  const dim3 g((unsigned)a.total), blk(256);
+  hipStream_t s = sa::as_stream(stream);
+  switch (F) {
+#define SA_GRAM_CASE(n)\
+  case n:              \
+    hipLaunchKernelGGL(gram_kernel<n>, g, blk, 0, s, a);\
+    break;
+    SA_GRAM_CASE(1) SA_GRAM_CASE(2) SA_GRAM_CASE(3) SA_GRAM_CASE(4) SA_GRAM_CASE(5) SA_GRAM_CASE(6)
+    SA_GRAM_CASE(7) SA_GRAM_CASE(8) SA_GRAM_CASE(9) SA_GRAM_CASE(10) SA_GRAM_CASE(11) SA_GRAM_CASE(12)
+#undef SA_GRAM_CASE
+  }
+  return sa::check_launch(fn);
+}
+
+extern "C" int sa_pattern_judge_finish(const float* share, const float* G1, const float* G2, int BH, int rows, int F,
+                                       float sparse_thr, float sim_thr, float* share_mean, float* col1, float* col2,
+                                       int32_t* use, void* stream) {
+  const char* fn = "sa_pattern_judge_finish";
+  SA_REQUIRE(share_mean && col1 && col2 && use, "%s: null output", fn);
+  SA_REQUIRE(BH > 0 && rows > 0 && F >= 1 && F <= 12, "%s: bad shape", fn);
+  FinishArgs a;
+  a.share = share; a.G1 = G1; a.G2 = G2; a.BH = BH; a.rows = rows; a.F = F;
+  a.sparse_thr = sparse_thr; a.sim_thr = sim_thr; a.share_mean = share_mean; a.col1 = col1; a.col2 = col2; a.use = use;
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((BH + 63) / 64)), dim3(64), 0, sa::as_stream(stream), a);
+  return sa::check_launch(fn);
+}

@@ -207,3 +207,131 @@ class ParternAttentionColVersion_V2:
 
     def __call__(self, *args, **kwds):
         return self.forward(*args, **kwds)
+
+
+# ---- head routing (partern_attention.py:464-521) ---------------------------------------------
+
+SPARSE_KEEP, SPARSE_THR, SIM_THR = 0.2, 0.9, 0.9
+_HEAD_CHUNK_BYTES = 1 << 30  # probability workspace per chunk of heads
+
+
+def _pad32(n: int) -> int:
+    return -(-n // 32) * 32
+
+
+def _compact(x, idx, n_pad):
+    """Rows idx of x (bf16 [B,H,L,64]) as a contiguous [B*H, n_pad, 64] buffer, zero padded."""
+    full = torch.full((n_pad,), -1, dtype=torch.int32)
+    full[: idx.numel()] = idx.to(torch.int32)
+    B, H = x.shape[:2]
+    return gather_tokens(x, full.to(x.device)).reshape(B * H, n_pad, 64)
+
+
+def _probs(qs, ks, rows, keys, n_bias, bias, c_lo, c_hi, P):
+    BH = qs.shape[0]
+    with torch.cuda.device(qs.device):
+        _lib.check(_lib.load().sa_sampled_probs(
+            qs.data_ptr(), ks.data_ptr(), BH, rows, qs.shape[1], keys, ks.shape[1], scale_factor, n_bias, bias,
+            c_lo, c_hi, P.data_ptr(), P.stride(0), P.stride(1), _lib.stream_of(qs)), "sa_sampled_probs")
+
+
+def _chunks(BH, bytes_per_head):
+    step = max(1, _HEAD_CHUNK_BYTES // max(1, bytes_per_head))
+    return [(h0, min(BH, h0 + step)) for h0 in range(0, BH, step)]
+
+
+def _sparsity_rows(q, k, g: PatternGeometry, idx_q):
+    """Per sampled first-frame query: mass of its top 20 % keys among every third token."""
+    B, H = q.shape[:2]
+    ns = idx_q.numel()
+    keys = torch.arange(0, g.L, 3)
+    n = keys.numel()
+    qs, ks = _compact(q, idx_q + g.text_length, _pad32(ns)), _compact(k, keys, _pad32(n))
+    K = int(n * SPARSE_KEEP)
+    share = torch.empty(B * H, ns, dtype=torch.float32, device=q.device)
+    for h0, h1 in _chunks(B * H, ns * n * 4):
+        P = torch.empty(h1 - h0, ns, n, dtype=torch.float32, device=q.device)
+        _probs(qs[h0:h1], ks[h0:h1], ns, n, 0, 0.0, 0, n, P)
+        with torch.cuda.device(q.device):
+            _lib.check(_lib.load().sa_topk_share(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, ns, n, K,
+                                                 share[h0:h1].data_ptr(), _lib.stream_of(q)), "sa_topk_share")
+    return share
+
+
+def _similarity_gram(q, k, g: PatternGeometry, index_k):
+    """Gram matrices [B*H, F, F(F+1)/2] of the sampled frame-pair attention patterns."""
+    B, H = q.shape[:2]
+    T, F, ns = g.text_length, g.frames, g.sample_num
+    nv = F * ns
+    qs = _compact(q, index_k[T:], _pad32(nv))
+    ks = _compact(k, index_k, _pad32(T + nv))
+    G = torch.empty(B * H, F, F * (F + 1) // 2, dtype=torch.float32, device=q.device)
+    for h0, h1 in _chunks(B * H, nv * nv * 4):
+        P = torch.empty(h1 - h0, nv, nv, dtype=torch.float32, device=q.device)
+        _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, math.log(ns / g.S), T, T + nv, P)
+        with torch.cuda.device(q.device):
+            _lib.check(_lib.load().sa_pattern_gram(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, F, ns,
+                                                   G[h0:h1].data_ptr(), _lib.stream_of(q)), "sa_pattern_gram")
+    return G
+
+
+def _finish(share, G1, G2, BH, rows, F, device):
+    f32 = dict(dtype=torch.float32, device=device)
+    sm, c1, c2 = torch.empty(BH, **f32), torch.empty(BH, **f32), torch.empty(BH, **f32)
+    use = torch.empty(BH, dtype=torch.int32, device=device)
+    with torch.cuda.device(device):
+        _lib.check(_lib.load().sa_pattern_judge_finish(
+            _lib.ptr(share), _lib.ptr(G1), _lib.ptr(G2), BH, rows, F, SPARSE_THR, SIM_THR, sm.data_ptr(),
+            c1.data_ptr(), c2.data_ptr(), use.data_ptr(), torch.cuda.current_stream(device).cuda_stream),
+            "sa_pattern_judge_finish")
+    return sm, c1, c2, use
+
+
+def judge_sparsity(q, k, geometry: PatternGeometry = DEFAULT, idx_q=None, return_share=False):
+    """True for heads whose sampled first-frame queries put > 90 % of their mass on the top
+    20 % of (every third) key (:470-479). idx_q: first-frame positions (default: a randperm)."""
+    g = geometry
+    q, k = _prep_qkv(q), _prep_qkv(k)
+    _lib.require_gpu(q, k)
+    if idx_q is None:
+        idx_q = torch.randperm(g.S)[: g.sample_num]
+    B, H = q.shape[:2]
+    share = _sparsity_rows(q, k, g, idx_q)
+    sm, _, _, _ = _finish(share, None, None, B * H, idx_q.numel(), g.frames, q.device)
+    sparse = (sm > SPARSE_THR).view(B, H)
+    return (sparse, sm.view(B, H)) if return_share else sparse
+
+
+def judge_similarity(q, k, geometry: PatternGeometry = DEFAULT, index_k=None, return_sim=False):
+    """True for heads whose sampled frame-pair attention patterns sharing a key frame have a
+    mean cosine similarity > 0.9 (:480-514)."""
+    g = geometry
+    q, k = _prep_qkv(q), _prep_qkv(k)
+    _lib.require_gpu(q, k)
+    if index_k is None:
+        _, index_k = get_indexs(g)
+    B, H = q.shape[:2]
+    G = _similarity_gram(q, k, g, index_k)
+    _, c1, _, _ = _finish(None, G, None, B * H, 1, g.frames, q.device)
+    sim = (c1 > SIM_THR).view(B, H)
+    return (sim, c1.view(B, H)) if return_sim else sim
+
+
+def unified_judge(q, k, geometry: PatternGeometry = DEFAULT, draws=None):
+    """Heads routed to the pattern attention: not sparse and self-similar twice (:516-521).
+    draws = (idx_q, index_k1, index_k2) overrides the three randperm draws."""
+    g = geometry
+    q, k = _prep_qkv(q), _prep_qkv(k)
+    _lib.require_gpu(q, k)
+    if draws is None:
+        idx_q = torch.randperm(g.S)[: g.sample_num]
+        _, ik1 = get_indexs(g)
+        _, ik2 = get_indexs(g)
+    else:
+        idx_q, ik1, ik2 = draws
+    B, H = q.shape[:2]
+    share = _sparsity_rows(q, k, g, idx_q)
+    G1 = _similarity_gram(q, k, g, ik1)
+    G2 = _similarity_gram(q, k, g, ik2)
+    sm, c1, c2, use = _finish(share, G1, G2, B * H, idx_q.numel(), g.frames, q.device)
+    return use.view(B, H).bool()

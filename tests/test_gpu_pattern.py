@@ -74,3 +74,39 @@ def test_reference_geometry_smoke(dev):
     assert out.shape == q.shape and torch.isfinite(out.float()).all()
     ref = torch.softmax(q[0, :, :g.text_length].float() @ k[0].float().transpose(-1, -2) / 8, dim=-1) @ v[0].float()
     assert (out[0, :, :g.text_length].float() - ref).abs().max().item() <= 2e-2
+
+
+def _judge_inputs():
+    # heads 0-1: every frame identical (self-similar patterns); heads 2-3: independent frames;
+    # head 3 with large scores (peaked, sparse attention).
+    g = torch.Generator().manual_seed(11)
+    B, H = 1, 4
+    q = torch.randn(B, H, G.L, 64, generator=g)
+    k = torch.randn(B, H, G.L, 64, generator=g)
+    T, S = G.text_length, G.S
+    for x in (q, k):
+        x[:, :2, T:] = x[:, :2, T:T + S].repeat(1, 1, G.frames, 1)
+    q[:, 3] *= 4
+    k[:, 3] *= 4
+    return q.to(torch.bfloat16), k.to(torch.bfloat16)
+
+
+def test_judges_match_oracle(dev):
+    case("unified_judge parts")
+    q, k = _judge_inputs()
+    qd, kd = q.to(dev), k.to(dev)
+    idx_q = torch.randperm(G.S, generator=torch.Generator().manual_seed(12))[: G.sample_num]
+    _, ik1 = pa.get_indexs(G)
+    _, ik2 = pa.get_indexs(G)
+    sp, share = pa.judge_sparsity(qd, kd, G, idx_q=idx_q, return_share=True)
+    w_sp, w_share = opat.judge_sparsity(q, k, idx_q, G.S, G.text_length)
+    assert torch.allclose(share.cpu().double(), w_share, rtol=1e-4, atol=1e-5)
+    sim, col = pa.judge_similarity(qd, kd, G, index_k=ik1, return_sim=True)
+    p1 = ik1[G.text_length: G.text_length + G.sample_num] - G.text_length
+    w_sim, w_col = opat.judge_similarity(q, k, p1, G.frames, G.S, G.text_length)
+    assert torch.allclose(col.cpu().double(), w_col, rtol=1e-4, atol=1e-5)
+    assert (w_col[0, :2] > 0.999).all() and (w_col[0, 2:] < 0.9).all()  # the inputs separate the heads
+    use = pa.unified_judge(qd, kd, G, draws=(idx_q, ik1, ik2))
+    p2 = ik2[G.text_length: G.text_length + G.sample_num] - G.text_length
+    want = opat.unified_judge(q, k, idx_q, p1, p2, G.frames, G.S, G.text_length)
+    assert torch.equal(use.cpu(), want)
