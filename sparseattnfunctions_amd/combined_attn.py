@@ -10,12 +10,18 @@ combined block mask of the MI355X build on the GPU:
                  U global top-k of the mean-pooled block scores (k = int(0.10 * nb))
                  U text block rows and columns,
 
-then runs the block-sparse attention kernel on it. This replaces the reference's
-per-head routing between pattern attention and the SparseGen+ estimator
-(combined_attn.py:47-101, partern_attention.py:516-521), which is host-synchronising and
-1.5-5B specific. `rearranger` / `recover` are the reference's 1.5-5B token permutations
-(combined_attn.py:17-41), as GPU gathers; `use_rearranger=True` is not supported with the
-combined rule, whose local window is defined on the text-first (t, h, w) layout.
+then runs the block-sparse attention kernel on it.
+
+`CombinedAttn(head_routing=True)` is the reference's own 1.5-5B body instead
+(combined_attn.py:42-101): after the warm-up steps, `unified_judge` (partern_attention.py:
+516-521) routes each head either to the frame-pattern attention (`ParternAttentionColVersion_V2`,
+at most 48 heads per call as the reference does) or to SparseGen_Plus's block-sparse
+attention, optionally through the 1.5-5B token permutation (`use_rearranger=True`); the
+routing needs one host synchronisation per call (the count of pattern heads), as in the
+reference. Selected heads are copied with torch's index_select/index_copy_.
+`rearranger` / `recover` are the reference's 1.5-5B token permutations (combined_attn.py:
+17-41), as GPU gathers; without head routing `use_rearranger=True` is not supported, since
+the combined rule's local window is defined on the text-first (t, h, w) layout.
 """
 from __future__ import annotations
 
@@ -69,7 +75,8 @@ def _perms(device):
 
 class CombinedAttn:
     def __init__(self, warmup_epoch: int = 5, geometry: Geometry = COGVIDEOX_2B, global_ratio: float = 0.10,
-                 window=(1, 8, 8), layer_num: int = 42, timestep: int = 50, sm_scale: float = None):
+                 window=(1, 8, 8), layer_num: int = 42, timestep: int = 50, sm_scale: float = None,
+                 head_routing: bool = False, pattern_geometry=None, verbose: bool = False):
         self.layer_num = layer_num
         self.timestep = timestep
         self.counter = 0
@@ -80,6 +87,19 @@ class CombinedAttn:
         self.window = tuple(window)
         self.sm_scale = sm_scale
         self.last_kv = None
+        # head_routing: the reference's 1.5-5B body (combined_attn.py:42-101): unified_judge
+        # routes each head to the frame-pattern attention or to SparseGen_Plus's block-sparse
+        # attention (dense during its warm-up).
+        self.head_routing = head_routing
+        self.verbose = verbose
+        self.last_routing = None
+        if head_routing:
+            from .partern_attention import DEFAULT, ParternAttentionColVersion_V2
+            from .SparseGen_Plus import BlockSparseAttention
+            self.pat_attn = ParternAttentionColVersion_V2(pattern_geometry or DEFAULT)
+            self.block_sparse_attention = BlockSparseAttention(block_size=64, layernum=layer_num, timestep=timestep,
+                                                               num_samples=4, warmup_epoch=warmup_epoch,
+                                                               verbose=verbose)
 
     def n_text_blocks(self) -> int:
         return math.ceil(self.geometry.text_len / self.geometry.block)
@@ -115,7 +135,49 @@ class CombinedAttn:
     def _scale(self, q):
         return self.sm_scale if self.sm_scale is not None else 1.0 / math.sqrt(q.shape[-1])
 
+    def _pattern_heads(self, qs, ks, vs):
+        # The reference runs the pattern attention on at most 48 selected heads at a time
+        # (combined_attn.py:56-79); its modify-factor decision is taken per such call.
+        outs = [self.pat_attn(qs[:, h:h + 48], ks[:, h:h + 48], vs[:, h:h + 48]) for h in range(0, qs.shape[1], 48)]
+        return torch.cat(outs, dim=1)
+
+    def _routed(self, q, k, v, use_rearranger):
+        from .partern_attention import unified_judge
+        if self.ct // self.layer_num < self.warmup_epoch:
+            self.ct += 1
+            return self.block_sparse_attention(q, k, v)
+        self.ct += 1
+        use = unified_judge(q, k, self.pat_attn.geometry)
+        self.last_routing = use
+        n_sel = int(use.sum().item())
+        if n_sel == 0:
+            return self.block_sparse_attention(q, k, v)
+        B, H, L, D = q.shape
+        flat = [x.reshape(B * H, L, D) for x in (q, k, v)]
+        sel = use.reshape(-1).nonzero().squeeze(1)
+        rest = (~use).reshape(-1).nonzero().squeeze(1)
+        self.counter += n_sel
+        out = torch.zeros(B * H, L, D, dtype=q.dtype, device=q.device)
+        pat = self._pattern_heads(*(x.index_select(0, sel).unsqueeze(0) for x in flat))
+        out.index_copy_(0, sel, pat[0])
+        if rest.numel() == 0:
+            self.counter += n_sel
+            self.block_sparse_attention.counter += 1
+        else:
+            qr, kr, vr = (x.index_select(0, rest).unsqueeze(0) for x in flat)
+            if use_rearranger:
+                qr, kr, vr = self.rearranger(qr, kr, vr)
+            o = self.block_sparse_attention(qr, kr, vr)
+            if use_rearranger:
+                o = self.recover(o)
+            out.index_copy_(0, rest, o[0])
+        if self.verbose:
+            print("counter:", self.counter, "now increment:", n_sel)
+        return out.view(B, H, L, D)
+
     def __call__(self, q, k, v, use_rearranger: bool = False):
+        if self.head_routing:
+            return self._routed(q, k, v, use_rearranger)
         if use_rearranger:
             raise NotImplementedError(
                 "use_rearranger (the 1.5-5B token permutation, combined_attn.py:17-41) is not supported "

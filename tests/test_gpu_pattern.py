@@ -110,3 +110,31 @@ def test_judges_match_oracle(dev):
     p2 = ik2[G.text_length: G.text_length + G.sample_num] - G.text_length
     want = opat.unified_judge(q, k, idx_q, p1, p2, G.frames, G.S, G.text_length)
     assert torch.equal(use.cpu(), want)
+
+
+def test_combined_attn_head_routing(dev):
+    # Heads routed by unified_judge: pattern heads equal the pattern attention on those heads,
+    # the others equal SparseGen_Plus's block-sparse attention on the remaining heads.
+    case("CombinedAttn head routing")
+    from sparseattnfunctions_amd.combined_attn import CombinedAttn
+    from sparseattnfunctions_amd.SparseGen_Plus import BlockSparseAttention
+    q, k = _judge_inputs()
+    v = _inputs(21, H=4)[2]
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    proc = CombinedAttn(warmup_epoch=0, head_routing=True, pattern_geometry=G, layer_num=2, timestep=3)
+    state = torch.get_rng_state()
+    out = proc(qd, kd, vd)
+    use = proc.last_routing.cpu()
+    assert use.any() and (~use).any()
+    # replay the same draws: judge (3 randperms), then the pattern call's get_indexs
+    torch.set_rng_state(state)
+    want_use = pa.unified_judge(qd, kd, G)
+    assert torch.equal(want_use.cpu(), use)
+    sel = use.reshape(-1).nonzero().squeeze(1)
+    rest = (~use).reshape(-1).nonzero().squeeze(1)
+    pat = pa.ParternAttentionColVersion_V2(G)(*(x.reshape(4, G.L, 64)[sel.to(dev)].unsqueeze(0) for x in (qd, kd, vd)))
+    bsa = BlockSparseAttention(layernum=2, timestep=3, num_samples=4, warmup_epoch=0, verbose=False)
+    other = bsa(*(x.reshape(4, G.L, 64)[rest.to(dev)].unsqueeze(0) for x in (qd, kd, vd)))
+    got = out.reshape(4, G.L, 64)
+    assert torch.equal(got[sel.to(dev)], pat[0])
+    assert torch.equal(got[rest.to(dev)], other[0])
