@@ -143,6 +143,24 @@ def other_configs(q, k, v, dev):
                              "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
                              "effective_tflop_per_call": round(fs / 1e12, 4)}
 
+    # 1.5-5B geometry (B=2, H=48, L=45104): unified_judge and the frame-pattern attention on
+    # every head (synthetic inputs drawn on the GPU).
+    from sparseattnfunctions_amd import partern_attention as pa
+
+    g = pa.DEFAULT
+    gen = torch.Generator(device=dev).manual_seed(5)
+    q6, k6, v6 = (torch.randn(2, 48, g.L, 64, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
+    pat = pa.ParternAttentionColVersion_V2()
+    _, idx6 = pa.get_indexs(g)
+    ms_pat = time_fn(lambda: pat(q6, k6, v6, index_k=idx6), iters=3, warmup=1)
+    draws = (torch.randperm(g.S)[: g.sample_num], pa.get_indexs(g)[1], pa.get_indexs(g)[1])
+    ms_judge = time_fn(lambda: pa.unified_judge(q6, k6, g, draws=draws), iters=3, warmup=1)
+    T, S, F = g.text_length, g.S, g.frames
+    f_pat = 2 * 48 * 4 * 64 * (T * g.L + S * g.L + F * S * T + F * g.sample_num * (T + F * g.sample_num) + F * S * S)
+    out["pattern_1_5b"] = {"pattern_ms": round(ms_pat, 3), "pattern_tflops": _tflops(f_pat, ms_pat),
+                           "unified_judge_ms": round(ms_judge, 3), "heads": 96, "L": g.L}
+    del q6, k6, v6
+
     # Sliding-tile attention (default config) on the C2 inputs: the fused call (query and
     # output permutations inside the kernel) against permute-copies + attention + copy back.
     from sparseattnfunctions_amd._kv import KVList

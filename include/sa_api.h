@@ -275,6 +275,46 @@ int sa_pattern_combine(const uint16_t* o_frames, const int64_t of_strides[3], co
                        float hi_frame, uint16_t* out, const int64_t out_strides[3], void* stream);
 
 /*
+ * Softmax probabilities of sampled queries over sampled keys, for the head-routing judges
+ * (judge_sparsity / judge_similarity, partern_attention.py:470-514):
+ *   P[bh][r][c - c_lo] = softmax_c(q_rows[bh][r] . k_rows[bh][c] * sm_scale + (c < n_bias ? bias : 0))
+ * over all `keys` keys, written for c in [c_lo, c_hi) and r < rows.
+ *   q_rows [BH][rows_pad][64], k_rows [BH][keys_pad][64] bf16 contiguous (pads: multiples of
+ *   32; padded rows are not read as keys); P fp32 with strides p_bh_stride, p_row_stride.
+ */
+int sa_sampled_probs(const uint16_t* q_rows, const uint16_t* k_rows, int BH, int rows, int rows_pad,
+                     int keys, int keys_pad, float sm_scale, int n_bias, float bias, int c_lo,
+                     int c_hi, float* P, int64_t p_bh_stride, int64_t p_row_stride, void* stream);
+
+/*
+ * Per row of P (n >= 0 entries, n <= 16384): the sum of its K largest entries, 1 <= K <= n
+ * (judge_sparsity's sorted-prefix share, partern_attention.py:476-478). share fp32 [BH][rows].
+ */
+int sa_topk_share(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int rows,
+                  int n, int K, float* share, void* stream);
+
+/*
+ * Gram matrices of the sampled frame-pair attention patterns (judge_similarity,
+ * partern_attention.py:497-510): with P the [F*ns x F*ns] video part of the sampled
+ * probabilities, G[bh][f2][chunk][pair(f1,f3)] = sum over s1 in the chunk (20 positions)
+ * and all s2 of P[f1*ns + s1][f2*ns + s2] * P[f3*ns + s1][f2*ns + s2], f1 <= f3 (pairs in
+ * row-major upper-triangle order). F <= 12, ns <= 512.
+ */
+int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int F,
+                    int ns, float* G, void* stream);
+
+/*
+ * Routing decision of unified_judge (partern_attention.py:516-521) per head:
+ * share_mean = mean of share over rows (NULL: 0), col = mean over key frames f2 of the mean
+ * over (f1, f3) of the cosine G[f1][f3] / sqrt(G[f1][f1] G[f3][f3]) from the Gram partials
+ * (G1/G2 NULL: 0), use = share_mean <= sparse_thr && col1 > sim_thr && col2 > sim_thr.
+ */
+int sa_pattern_judge_finish(const float* share, const float* G1, const float* G2, int BH,
+                            int rows, int F, int ns, float sparse_thr, float sim_thr,
+                            float* share_mean, float* col1, float* col2, int32_t* use,
+                            void* stream);
+
+/*
  * (host) Static local 3-D window of the combined mask, one byte per (query block, key
  * block): 1 iff both blocks are video blocks and their centre tokens (index
  * block*qb + block/2, clamped to L-1) lie within +-dt latent frames, +-dh patch rows and

@@ -11,7 +11,8 @@
 //                      bit patterns), one workgroup per row;
 //   gram_kernel        judge_similarity (:480-514): for key frame f2, the Gram matrix
 //                      G[f1][f3] = sum_{s1,s2} P[f1 s1][f2 s2] * P[f3 s1][f2 s2] of the
-//                      frame-pair patterns (their inner products and norms);
+//                      frame-pair patterns (their inner products and norms), as partial sums
+//                      over chunks of s1;
 //   finish_kernel      per head: mean share > 0.9 (sparse), mean cosine similarity of the
 //                      patterns sharing a key frame > 0.9 (twice), and the routing decision.
 #include <cmath>
@@ -48,6 +49,7 @@ struct ProbArgs {
   float* P;            // P[bh*p_bh + r*p_row + (key - c_lo)]
   int64_t p_bh, p_row;
   int ng;              // rows_pad / 32
+  int vec_ok;          // 16-byte stores possible (P, strides and c_lo multiples of 4 floats)
   int64_t total;       // BH * ng
 };
 
@@ -70,16 +72,28 @@ __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
   auto logit = [&](const sa_f32x16& t, int kt, int i) {
     const int key = 32 * kt + 8 * (i >> 2) + 4 * hh + (i & 3);
     if (key >= a.keys) return -INFINITY;
-    return t[i] * a.scale_log2 + (key < a.n_bias ? a.bias_log2 : 0.f);
+    return fmaf(t[i], a.scale_log2, key < a.n_bias ? a.bias_log2 : 0.f);
   };
   float m = -INFINITY, l = 0.f;
   for (int kt = 0; kt < a.keys_pad / 32; ++kt) {
     const sa_f32x16 t = score_tile(kbase + (int64_t)kt * 32 * kD, qf);
     float x[16], tmax = -INFINITY;
+    // Whole tiles inside the key range and on one side of the bias boundary need no
+    // per-element tests.
+    const bool uniform = 32 * kt + 32 <= a.keys && (32 * kt + 32 <= a.n_bias || 32 * kt >= a.n_bias);
+    if (uniform) {
+      const float tb = 32 * kt < a.n_bias ? a.bias_log2 : 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = logit(t, kt, i);
-      tmax = fmaxf(tmax, x[i]);
+      for (int i = 0; i < 16; ++i) {
+        x[i] = fmaf(t[i], a.scale_log2, tb);
+        tmax = fmaxf(tmax, x[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        x[i] = logit(t, kt, i);
+        tmax = fmaxf(tmax, x[i]);
+      }
     }
     const float mn = fmaxf(m, tmax);
     if (mn != -INFINITY) {
@@ -110,10 +124,19 @@ __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
     const int r = lane >> 1, half = lane & 1;
     if (row0 + r < a.rows) {
       float* dst = a.P + bh * a.p_bh + (int64_t)(row0 + r) * a.p_row;
+      const int key0 = 32 * kt + 16 * half;
+      if (a.vec_ok && key0 >= a.c_lo && key0 + 16 <= a.c_hi) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = 32 * kt + 16 * half + j;
-        if (key >= a.c_lo && key < a.c_hi) dst[key - a.c_lo] = tile[wave][r][16 * half + j];
+        for (int j = 0; j < 16; j += 4)
+          *reinterpret_cast<float4*>(dst + key0 - a.c_lo + j) =
+              make_float4(tile[wave][r][16 * half + j], tile[wave][r][16 * half + j + 1],
+                          tile[wave][r][16 * half + j + 2], tile[wave][r][16 * half + j + 3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = key0 + j;
+          if (key >= a.c_lo && key < a.c_hi) dst[key - a.c_lo] = tile[wave][r][16 * half + j];
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -121,7 +144,7 @@ __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// share_kernel: one workgroup per (bh, row) over n probabilities (n <= 16384, in LDS).
+// share_kernel: one workgroup per (bh, row) over n probabilities (n <= 16384).
 struct ShareArgs {
   const float* P;
   int64_t p_bh, p_row;
@@ -130,91 +153,109 @@ struct ShareArgs {
   int64_t total;
 };
 
+__device__ inline uint32_t wave_sum_u(uint32_t x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+__device__ inline float wave_sum_f(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// Thread t holds entries t, t + 256, ... (at most 64 of them) in registers.
 __global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
-  __shared__ uint32_t v[16384];
-  __shared__ uint32_t red_u[256];
-  __shared__ float red_f[256];
+  constexpr int kPer = 64;
+  __shared__ uint32_t part_u[2][4];
+  __shared__ float part_f[4];
   const int64_t w = blockIdx.x;
   if (w >= a.total) return;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, wave = t >> 6;
   const int64_t bh = w / a.rows;
   const int r = (int)(w - bh * a.rows);
   const float* src = a.P + bh * a.p_bh + (int64_t)r * a.p_row;
-  for (int i = t; i < a.n; i += 256) v[i] = __float_as_uint(src[i]);  // p >= 0: bits order as values
-  __syncthreads();
-  // K-th largest bit pattern: largest thr with #{v >= thr} >= K.
+  uint32_t v[kPer];  // p >= 0: the bit patterns order as the values; 0 past n
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = t + 256 * j;
+    v[j] = i < a.n ? __float_as_uint(src[i]) : 0u;
+  }
+  // K-th largest bit pattern: largest thr with #{v >= thr} >= K (double-buffered partials,
+  // one barrier per step).
   uint32_t thr = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = thr | (1u << bit);
     uint32_t c = 0;
-    for (int i = t; i < a.n; i += 256) c += v[i] >= cand;
-    red_u[t] = c;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) c += v[j] >= cand;
+    c = wave_sum_u(c);
+    if ((t & 63) == 0) part_u[bit & 1][wave] = c;
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-      if (t < s) red_u[t] += red_u[t + s];
-      __syncthreads();
-    }
-    if (red_u[0] >= (uint32_t)a.K) thr = cand;
-    __syncthreads();
+    const uint32_t tot = part_u[bit & 1][0] + part_u[bit & 1][1] + part_u[bit & 1][2] + part_u[bit & 1][3];
+    if (tot >= (uint32_t)a.K) thr = cand;
   }
   // Mass above thr, plus thr for the ties needed to make K.
-  float s = 0.f;
+  float sum = 0.f;
   uint32_t gt = 0;
-  for (int i = t; i < a.n; i += 256) {
-    if (v[i] > thr) {
-      s += __uint_as_float(v[i]);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (v[j] > thr) {
+      sum += __uint_as_float(v[j]);
       ++gt;
     }
   }
-  red_f[t] = s;
-  red_u[t] = gt;
+  sum = wave_sum_f(sum);
+  gt = wave_sum_u(gt);
   __syncthreads();
-  for (int k = 128; k > 0; k >>= 1) {
-    if (t < k) {
-      red_f[t] += red_f[t + k];
-      red_u[t] += red_u[t + k];
-    }
-    __syncthreads();
+  if ((t & 63) == 0) {
+    part_f[wave] = sum;
+    part_u[0][wave] = gt;
   }
-  if (t == 0) a.share[bh * a.rows + r] = red_f[0] + (float)((int)a.K - (int)red_u[0]) * __uint_as_float(thr);
+  __syncthreads();
+  if (t == 0) {
+    const float s4 = ((part_f[0] + part_f[1]) + part_f[2]) + part_f[3];
+    const uint32_t g4 = part_u[0][0] + part_u[0][1] + part_u[0][2] + part_u[0][3];
+    a.share[bh * a.rows + r] = s4 + (float)((int)a.K - (int)g4) * __uint_as_float(thr);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
-// gram_kernel: one workgroup per (bh, key frame f2). P rows f1*ns + s1 (video sample rows),
-// columns f2*ns + s2 (video sample columns).
+// gram_kernel: one workgroup per (bh, key frame f2, chunk of kGramChunk sample positions s1).
+// Thread t takes columns s2 = t, t + 256, ... of frame f2 and accumulates, over its s1 chunk,
+// the products of the F values P[f1*ns + s1][f2*ns + s2] (f1 = 0..F-1) of each column.
+// Partial sums go to G_part[bh][f2][chunk][pair]; the finish kernel adds the chunks in order.
+constexpr int kGramChunk = 20;
+
 struct GramArgs {
   const float* P;
   int64_t p_bh, p_row;
-  int ns;
-  float* G;  // [BH][F][F*(F+1)/2]
+  int ns, n_chunks;
+  float* G;  // [BH][F][n_chunks][F*(F+1)/2]
   int64_t total;
 };
 
 template <int F>
 __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
   constexpr int NP = F * (F + 1) / 2;
-  __shared__ float rows[F][512];
-  __shared__ float red[256];
+  __shared__ float part[4][NP];
   const int64_t w = blockIdx.x;
   if (w >= a.total) return;
-  const int t = threadIdx.x;
-  const int64_t bh = w / F;
-  const int f2 = (int)(w - bh * F);
+  const int t = threadIdx.x, wave = t >> 6;
+  const int64_t bhf = w / a.n_chunks;
+  const int chunk = (int)(w - bhf * a.n_chunks);
+  const int64_t bh = bhf / F;
+  const int f2 = (int)(bhf - bh * F);
+  const int s1_lo = chunk * kGramChunk, s1_hi = min(a.ns, s1_lo + kGramChunk);
   float acc[NP];
 #pragma unroll
   for (int p = 0; p < NP; ++p) acc[p] = 0.f;
   const float* base = a.P + bh * a.p_bh + (int64_t)f2 * a.ns;
-  for (int s1 = 0; s1 < a.ns; ++s1) {
-    __syncthreads();
-    for (int e = t; e < F * a.ns; e += 256) {
-      const int f1 = e / a.ns, s2 = e - f1 * a.ns;
-      rows[f1][s2] = base[(int64_t)(f1 * a.ns + s1) * a.p_row + s2];
-    }
-    __syncthreads();
-    for (int s2 = t; s2 < a.ns; s2 += 256) {
+  for (int s2 = t; s2 < a.ns; s2 += 256) {
+    for (int s1 = s1_lo; s1 < s1_hi; ++s1) {
       float x[F];
 #pragma unroll
-      for (int f1 = 0; f1 < F; ++f1) x[f1] = rows[f1][s2];
+      for (int f1 = 0; f1 < F; ++f1) x[f1] = base[(int64_t)(f1 * a.ns + s1) * a.p_row + s2];
       int p = 0;
 #pragma unroll
       for (int f1 = 0; f1 < F; ++f1)
@@ -225,26 +266,22 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
         }
     }
   }
-  float* out = a.G + (bh * F + f2) * NP;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    __syncthreads();
-    red[t] = acc[p];
-    __syncthreads();
-    for (int k = 128; k > 0; k >>= 1) {
-      if (t < k) red[t] += red[t + k];
-      __syncthreads();
-    }
-    if (t == 0) out[p] = red[0];
+    const float r = wave_sum_f(acc[p]);
+    if ((t & 63) == 0) part[wave][p] = r;
   }
+  __syncthreads();
+  float* out = a.G + (bhf * a.n_chunks + chunk) * NP;
+  for (int p = t; p < NP; p += 256) out[p] = ((part[0][p] + part[1][p]) + part[2][p]) + part[3][p];
 }
 
 // ---------------------------------------------------------------------------------------
 struct FinishArgs {
-  const float* share;  // [BH][rows]
-  const float* G1;     // [BH][F][NP]
+  const float* share;  // [BH][rows] or null
+  const float* G1;     // [BH][F][n_chunks][NP] partials or null
   const float* G2;
-  int BH, rows, F;
+  int BH, rows, F, n_chunks;
   float sparse_thr, sim_thr;
   float* share_mean;  // [BH]
   float* col1;        // [BH]
@@ -252,38 +289,57 @@ struct FinishArgs {
   int32_t* use;       // [BH]
 };
 
-__device__ inline float col_sim(const float* G, int F) {
+// Mean cosine similarity of the patterns sharing a key frame, from one head's Gram partials:
+// col = mean over f2 of mean over (f1, f3) of G[f2][f1][f3] / sqrt(G[f2][f1][f1] G[f2][f3][f3]).
+__device__ float col_sim(const float* Gp, int F, int n_chunks, float* gs /* LDS [F * NP] */) {
+  const int lane = threadIdx.x;
   const int NP = F * (F + 1) / 2;
-  float tot = 0.f;
-  for (int f2 = 0; f2 < F; ++f2) {
-    const float* g = G + f2 * NP;
-    auto at = [&](int i, int j) {  // i <= j: pair index of (i, j) in row-major upper triangle
-      if (i > j) { const int tmp = i; i = j; j = tmp; }
-      return g[i * F - i * (i - 1) / 2 + (j - i)];
-    };
+  for (int e = lane; e < F * NP; e += 64) {
+    const int f2 = e / NP, p = e - f2 * NP;
     float s = 0.f;
-    for (int f1 = 0; f1 < F; ++f1)
-      for (int f3 = 0; f3 < F; ++f3) s += at(f1, f3) / sqrtf(at(f1, f1) * at(f3, f3));
-    tot += s / (float)(F * F);
+    for (int c = 0; c < n_chunks; ++c) s += Gp[((int64_t)f2 * n_chunks + c) * NP + p];
+    gs[e] = s;
   }
-  return tot / (float)F;
+  __syncthreads();
+  auto at = [&](const float* g, int i, int j) {
+    if (i > j) {
+      const int tmp = i;
+      i = j;
+      j = tmp;
+    }
+    return g[i * F - i * (i - 1) / 2 + (j - i)];
+  };
+  float part = 0.f;
+  for (int u = lane; u < F * F * F; u += 64) {
+    const int f2 = u / (F * F), f1 = (u / F) % F, f3 = u % F;
+    const float* g = gs + f2 * NP;
+    part += at(g, f1, f3) / sqrtf(at(g, f1, f1) * at(g, f3, f3));
+  }
+  const float tot = wave_sum_f(part);
+  __syncthreads();
+  return tot / (float)(F * F * F);
 }
 
 __global__ __launch_bounds__(64) void finish_kernel(FinishArgs a) {
-  const int bh = blockIdx.x * 64 + threadIdx.x;
+  __shared__ float gs[16 * 136];
+  const int bh = blockIdx.x;
   if (bh >= a.BH) return;
+  const int lane = threadIdx.x;
   float s = 0.f;
   if (a.share) {
-    for (int r = 0; r < a.rows; ++r) s += a.share[(int64_t)bh * a.rows + r];
-    s /= (float)a.rows;
+    for (int r = lane; r < a.rows; r += 64) s += a.share[(int64_t)bh * a.rows + r];
+    s = wave_sum_f(s) / (float)a.rows;
   }
   const int NP = a.F * (a.F + 1) / 2;
-  const float c1 = a.G1 ? col_sim(a.G1 + (int64_t)bh * a.F * NP, a.F) : 0.f;
-  const float c2 = a.G2 ? col_sim(a.G2 + (int64_t)bh * a.F * NP, a.F) : 0.f;
-  a.share_mean[bh] = s;
-  a.col1[bh] = c1;
-  a.col2[bh] = c2;
-  a.use[bh] = (!(s > a.sparse_thr) && c1 > a.sim_thr && c2 > a.sim_thr) ? 1 : 0;
+  const int64_t gstride = (int64_t)a.F * a.n_chunks * NP;
+  const float c1 = a.G1 ? col_sim(a.G1 + bh * gstride, a.F, a.n_chunks, gs) : 0.f;
+  const float c2 = a.G2 ? col_sim(a.G2 + bh * gstride, a.F, a.n_chunks, gs) : 0.f;
+  if (lane == 0) {
+    a.share_mean[bh] = s;
+    a.col1[bh] = c1;
+    a.col2[bh] = c2;
+    a.use[bh] = (!(s > a.sparse_thr) && c1 > a.sim_thr && c2 > a.sim_thr) ? 1 : 0;
+  }
 }
 
 }  // namespace
@@ -304,6 +360,8 @@ extern "C" int sa_sampled_probs(const uint16_t* q_rows, const uint16_t* k_rows, 
   a.scale_log2 = sm_scale * kLog2e; a.n_bias = n_bias; a.bias_log2 = bias * kLog2e;
   a.c_lo = c_lo; a.c_hi = c_hi; a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride;
   a.ng = rows_pad / 32; a.total = (int64_t)BH * a.ng;
+  a.vec_ok = (reinterpret_cast<uintptr_t>(P) % 16 == 0 && p_row_stride % 4 == 0 && p_bh_stride % 4 == 0 &&
+              c_lo % 4 == 0) ? 1 : 0;
   hipLaunchKernelGGL(probs_kernel, dim3((unsigned)((a.total + 3) / 4)), dim3(256), 0, sa::as_stream(stream), a);
   return sa::check_launch(fn);
 }
@@ -328,7 +386,9 @@ extern "C" int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_ro
   SA_REQUIRE(BH > 0 && ns > 0 && ns <= 512, "%s: bad shape (ns <= 512)", fn);
   SA_REQUIRE(F >= 1 && F <= 12, "%s: frames %d outside [1, 12]", fn, F);
   GramArgs a;
-  a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride; a.ns = ns; a.G = G; a.total = (int64_t)BH * F;
+  a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride; a.ns = ns; a.G = G;
+  a.n_chunks = (ns + kGramChunk - 1) / kGramChunk;
+  a.total = (int64_t)BH * F * a.n_chunks;
   const dim3 g((unsigned)a.total), blk(256);
   hipStream_t s = sa::as_stream(stream);
   switch (F) {
@@ -344,14 +404,15 @@ extern "C" int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_ro
 }
 
 extern "C" int sa_pattern_judge_finish(const float* share, const float* G1, const float* G2, int BH, int rows, int F,
-                                       float sparse_thr, float sim_thr, float* share_mean, float* col1, float* col2,
+                                       int ns, float sparse_thr, float sim_thr, float* share_mean, float* col1, float* col2,
                                        int32_t* use, void* stream) {
   const char* fn = "sa_pattern_judge_finish";
   SA_REQUIRE(share_mean && col1 && col2 && use, "%s: null output", fn);
-  SA_REQUIRE(BH > 0 && rows > 0 && F >= 1 && F <= 12, "%s: bad shape", fn);
+  SA_REQUIRE(BH > 0 && rows > 0 && F >= 1 && F <= 12 && ns > 0, "%s: bad shape", fn);
   FinishArgs a;
   a.share = share; a.G1 = G1; a.G2 = G2; a.BH = BH; a.rows = rows; a.F = F;
+  a.n_chunks = (ns + kGramChunk - 1) / kGramChunk;
   a.sparse_thr = sparse_thr; a.sim_thr = sim_thr; a.share_mean = share_mean; a.col1 = col1; a.col2 = col2; a.use = use;
-  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((BH + 63) / 64)), dim3(64), 0, sa::as_stream(stream), a);
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)BH), dim3(64), 0, sa::as_stream(stream), a);
   return sa::check_launch(fn);
 }

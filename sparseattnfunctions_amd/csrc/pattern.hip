@@ -9,10 +9,11 @@
 //         fstats_kernel    per head and factor: sum, min and max of the first-frame masses
 //                          (text mass for modify_factor_text, frame-i mass for frame i);
 //         select_kernel    constrained_mod_factor (:215-276) as a per-element affine map +
-//                          clamp, with the cross-head "any head out of range" decision; the
-//                          query frame of every key frame (argmax over img2img_map columns,
-//                          or the first frame where img2img_map[0][i] >= 0.1, :414-423) and the
-//                          per-head query-row gather table;
+//                          clamp, with the cross-head "any head out of range" decision, and
+//                          the case of every key frame (first-frame masses where
+//                          img2img_map[0][i] >= 0.1, :414-423);
+//         qidx_kernel      the per-head query-row gather table (query frame = argmax over the
+//                          img2img_map column, or the first frame);
 //   combine_kernel         out = sum_i img2img[f1][i] * scale_i(r) * O_i[r]
 //                                + img2text[f1] * mft(r) * O_text[f1*S + r]   (:455-460).
 #include "sa_common.h"
@@ -171,21 +172,33 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     const float* mp = a.img2img + (int64_t)bh * a.F * a.F;
     const float m0 = mp[i];  // img2img[0][i]
     const bool first = !(m0 < a.map_thr);
-    int sel = 0;
+    a.frame_case[t2] = first ? 1 : 0;
+    a.inv_map0[t2] = 1.f / m0;
+  }
+}
+
+// The query row gathered for selected row i*S + r of head bh: T + sel(bh, i)*S + r, with
+// sel = 0 when the first-frame masses are used for key frame i, else the argmax of column i.
+__global__ __launch_bounds__(256) void qidx_kernel(SelectArgs a) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)a.F * a.S;
+  if (e >= (int64_t)a.BH * per) return;
+  const int64_t bh = e / per;
+  const int j = (int)(e - bh * per);
+  const int i = j / a.S, r = j - i * a.S;
+  const float* mp = a.img2img + bh * a.F * a.F;
+  int sel = 0;
+  if (mp[i] < a.map_thr) {
     float best = mp[i];
-    for (int f1 = 1; f1 < a.F; ++f1) {  // argmax over the column, first maximum wins
+    for (int f1 = 1; f1 < a.F; ++f1) {
       const float x = mp[f1 * a.F + i];
       if (x > best) {
         best = x;
         sel = f1;
       }
     }
-    if (first) sel = 0;
-    a.frame_case[t2] = first ? 1 : 0;
-    a.inv_map0[t2] = 1.f / m0;
-    int32_t* qi = a.q_idx + (int64_t)bh * a.F * a.S + (int64_t)i * a.S;
-    for (int r = 0; r < a.S; ++r) qi[r] = a.T + sel * a.S + r;
   }
+  a.q_idx[e] = a.T + sel * a.S + r;
 }
 
 __device__ inline float apply_fac(const float* f, float x, float lo, float hi) {
@@ -362,6 +375,8 @@ extern "C" int sa_pattern_plan(const uint16_t* ff_mass, const int64_t ff_strides
   se.fac = fac; se.frame_case = frame_case; se.inv_map0 = inv_map0; se.q_idx = q_idx;
   const int n = BH * (1 + F) + BH * F;
   hipLaunchKernelGGL(select_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, se);
+  const int64_t nq = (int64_t)BH * F * S;
+  hipLaunchKernelGGL(qidx_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s, se);
   return sa::check_launch(fn);
 }
 

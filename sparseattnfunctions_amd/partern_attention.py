@@ -212,7 +212,8 @@ class ParternAttentionColVersion_V2:
 # ---- head routing (partern_attention.py:464-521) ---------------------------------------------
 
 SPARSE_KEEP, SPARSE_THR, SIM_THR = 0.2, 0.9, 0.9
-_HEAD_CHUNK_BYTES = 1 << 30  # probability workspace per chunk of heads
+_HEAD_CHUNK_BYTES = 4 << 30  # probability workspace per chunk of heads
+_GRAM_CHUNK = 20             # sample positions per Gram partial (kGramChunk in judge.hip)
 
 
 def _pad32(n: int) -> int:
@@ -265,7 +266,7 @@ def _similarity_gram(q, k, g: PatternGeometry, index_k):
     nv = F * ns
     qs = _compact(q, index_k[T:], _pad32(nv))
     ks = _compact(k, index_k, _pad32(T + nv))
-    G = torch.empty(B * H, F, F * (F + 1) // 2, dtype=torch.float32, device=q.device)
+    G = torch.empty(B * H, F, -(-ns // _GRAM_CHUNK), F * (F + 1) // 2, dtype=torch.float32, device=q.device)
     for h0, h1 in _chunks(B * H, nv * nv * 4):
         P = torch.empty(h1 - h0, nv, nv, dtype=torch.float32, device=q.device)
         _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, math.log(ns / g.S), T, T + nv, P)
@@ -275,13 +276,13 @@ def _similarity_gram(q, k, g: PatternGeometry, index_k):
     return G
 
 
-def _finish(share, G1, G2, BH, rows, F, device):
+def _finish(share, G1, G2, BH, rows, F, ns, device):
     f32 = dict(dtype=torch.float32, device=device)
     sm, c1, c2 = torch.empty(BH, **f32), torch.empty(BH, **f32), torch.empty(BH, **f32)
     use = torch.empty(BH, dtype=torch.int32, device=device)
     with torch.cuda.device(device):
         _lib.check(_lib.load().sa_pattern_judge_finish(
-            _lib.ptr(share), _lib.ptr(G1), _lib.ptr(G2), BH, rows, F, SPARSE_THR, SIM_THR, sm.data_ptr(),
+            _lib.ptr(share), _lib.ptr(G1), _lib.ptr(G2), BH, rows, F, ns, SPARSE_THR, SIM_THR, sm.data_ptr(),
             c1.data_ptr(), c2.data_ptr(), use.data_ptr(), torch.cuda.current_stream(device).cuda_stream),
             "sa_pattern_judge_finish")
     return sm, c1, c2, use
@@ -297,7 +298,7 @@ def judge_sparsity(q, k, geometry: PatternGeometry = DEFAULT, idx_q=None, return
         idx_q = torch.randperm(g.S)[: g.sample_num]
     B, H = q.shape[:2]
     share = _sparsity_rows(q, k, g, idx_q)
-    sm, _, _, _ = _finish(share, None, None, B * H, idx_q.numel(), g.frames, q.device)
+    sm, _, _, _ = _finish(share, None, None, B * H, idx_q.numel(), g.frames, g.sample_num, q.device)
     sparse = (sm > SPARSE_THR).view(B, H)
     return (sparse, sm.view(B, H)) if return_share else sparse
 
@@ -312,7 +313,7 @@ def judge_similarity(q, k, geometry: PatternGeometry = DEFAULT, index_k=None, re
         _, index_k = get_indexs(g)
     B, H = q.shape[:2]
     G = _similarity_gram(q, k, g, index_k)
-    _, c1, _, _ = _finish(None, G, None, B * H, 1, g.frames, q.device)
+    _, c1, _, _ = _finish(None, G, None, B * H, 1, g.frames, g.sample_num, q.device)
     sim = (c1 > SIM_THR).view(B, H)
     return (sim, c1.view(B, H)) if return_sim else sim
 
@@ -333,5 +334,5 @@ def unified_judge(q, k, geometry: PatternGeometry = DEFAULT, draws=None):
     share = _sparsity_rows(q, k, g, idx_q)
     G1 = _similarity_gram(q, k, g, ik1)
     G2 = _similarity_gram(q, k, g, ik2)
-    sm, c1, c2, use = _finish(share, G1, G2, B * H, idx_q.numel(), g.frames, q.device)
+    sm, c1, c2, use = _finish(share, G1, G2, B * H, idx_q.numel(), g.frames, g.sample_num, q.device)
     return use.view(B, H).bool()
