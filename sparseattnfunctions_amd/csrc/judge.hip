@@ -25,6 +25,7 @@ constexpr int kD = 64;
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef unsigned jd_u32x4 __attribute__((ext_vector_type(4)));
+typedef float jd_f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline sa_f32x16 score_tile(const uint16_t* kp, const sa_bf16x8 (&qf)[4]) {
   jd_u32x4 kop[4];
@@ -54,7 +55,7 @@ struct ProbArgs {
 };
 
 __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
-  __shared__ float tile[4][32][33];
+  __shared__ float tile[4][32][36];  // [wave][query row][key], rows 16-byte aligned
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
@@ -69,32 +70,28 @@ __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
     for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(sa_bf16x8, *reinterpret_cast<const jd_u32x4*>(qp + 16 * s));
   }
   const uint16_t* kbase = a.ks + (bh * a.keys_pad + col) * kD + 8 * hh;
-  auto logit = [&](const sa_f32x16& t, int kt, int i) {
-    const int key = 32 * kt + 8 * (i >> 2) + 4 * hh + (i & 3);
-    if (key >= a.keys) return -INFINITY;
-    return fmaf(t[i], a.scale_log2, key < a.n_bias ? a.bias_log2 : 0.f);
+  // Logits (log2 domain) of key tile kt; -inf past the keys. Whole tiles inside the key
+  // range and on one side of the bias boundary need no per-element tests.
+  auto logits = [&](const sa_f32x16& t, int kt, float (&x)[16]) {
+    if (32 * kt + 32 <= a.keys && (32 * kt + 32 <= a.n_bias || 32 * kt >= a.n_bias)) {
+      const float tb = 32 * kt < a.n_bias ? a.bias_log2 : 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = fmaf(t[i], a.scale_log2, tb);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = 32 * kt + 8 * (i >> 2) + 4 * hh + (i & 3);
+        x[i] = key >= a.keys ? -INFINITY : fmaf(t[i], a.scale_log2, key < a.n_bias ? a.bias_log2 : 0.f);
+      }
+    }
   };
   float m = -INFINITY, l = 0.f;
   for (int kt = 0; kt < a.keys_pad / 32; ++kt) {
     const sa_f32x16 t = score_tile(kbase + (int64_t)kt * 32 * kD, qf);
     float x[16], tmax = -INFINITY;
-    // Whole tiles inside the key range and on one side of the bias boundary need no
-    // per-element tests.
-    const bool uniform = 32 * kt + 32 <= a.keys && (32 * kt + 32 <= a.n_bias || 32 * kt >= a.n_bias);
-    if (uniform) {
-      const float tb = 32 * kt < a.n_bias ? a.bias_log2 : 0.f;
+    logits(t, kt, x);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        x[i] = fmaf(t[i], a.scale_log2, tb);
-        tmax = fmaxf(tmax, x[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        x[i] = logit(t, kt, i);
-        tmax = fmaxf(tmax, x[i]);
-      }
-    }
+    for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, x[i]);
     const float mn = fmaxf(m, tmax);
     if (mn != -INFINITY) {
       float sum = 0.f;
@@ -114,29 +111,32 @@ __global__ __launch_bounds__(256) void probs_kernel(ProbArgs a) {
   }
   const float inv = 1.f / l;
   const int row0 = 32 * g;
+  const int c4 = lane & 7;  // lane writes keys 4*c4 .. 4*c4+3 of rows lane/8 + 8j
   for (int kt = a.c_lo / 32; kt * 32 < a.c_hi; ++kt) {
     const sa_f32x16 t = score_tile(kbase + (int64_t)kt * 32 * kD, qf);
+    float x[16];
+    logits(t, kt, x);
 #pragma unroll
     for (int i = 0; i < 16; ++i)
-      tile[wave][col][8 * (i >> 2) + 4 * hh + (i & 3)] = __builtin_amdgcn_exp2f(logit(t, kt, i) - m) * inv;
+      tile[wave][col][8 * (i >> 2) + 4 * hh + (i & 3)] = __builtin_amdgcn_exp2f(x[i] - m) * inv;
     __builtin_amdgcn_wave_barrier();
-    // lanes 2r, 2r+1 write keys 0..15 / 16..31 of row r
-    const int r = lane >> 1, half = lane & 1;
-    if (row0 + r < a.rows) {
+    // 8 lanes per row: each store instruction writes 128 contiguous bytes of 8 rows.
+    const int key0 = 32 * kt + 4 * c4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 8 * j + (lane >> 3);
+      if (row0 + r >= a.rows) continue;
       float* dst = a.P + bh * a.p_bh + (int64_t)(row0 + r) * a.p_row;
-      const int key0 = 32 * kt + 16 * half;
-      if (a.vec_ok && key0 >= a.c_lo && key0 + 16 <= a.c_hi) {
-#pragma unroll
-        for (int j = 0; j < 16; j += 4)
-          *reinterpret_cast<float4*>(dst + key0 - a.c_lo + j) =
-              make_float4(tile[wave][r][16 * half + j], tile[wave][r][16 * half + j + 1],
-                          tile[wave][r][16 * half + j + 2], tile[wave][r][16 * half + j + 3]);
+      const float4 v = *reinterpret_cast<const float4*>(&tile[wave][r][4 * c4]);
+      const int o = key0 - a.c_lo;  // column of key0 in P
+      if (a.vec_ok && key0 >= a.c_lo && key0 + 4 <= a.c_hi) {
+        // streamed: P is far larger than the caches, K stays resident
+        __builtin_nontemporal_store(jd_f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<jd_f32x4*>(dst + o));
       } else {
+        const float e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = key0 + j;
-          if (key >= a.c_lo && key < a.c_hi) dst[key - a.c_lo] = tile[wave][r][16 * half + j];
-        }
+        for (int u = 0; u < 4; ++u)
+          if (key0 + u >= a.c_lo && key0 + u < a.c_hi) dst[o + u] = e[u];
       }
     }
     __builtin_amdgcn_wave_barrier();

@@ -250,8 +250,9 @@ def _sparsity_rows(q, k, g: PatternGeometry, idx_q):
     qs, ks = _compact(q, idx_q + g.text_length, _pad32(ns)), _compact(k, keys, _pad32(n))
     K = int(n * SPARSE_KEEP)
     share = torch.empty(B * H, ns, dtype=torch.float32, device=q.device)
-    for h0, h1 in _chunks(B * H, ns * n * 4):
-        P = torch.empty(h1 - h0, ns, n, dtype=torch.float32, device=q.device)
+    # rows padded to whole 128-byte lines
+    for h0, h1 in _chunks(B * H, ns * _pad32(n) * 4):
+        P = torch.empty(h1 - h0, ns, _pad32(n), dtype=torch.float32, device=q.device)
         _probs(qs[h0:h1], ks[h0:h1], ns, n, 0, 0.0, 0, n, P)
         with torch.cuda.device(q.device):
             _lib.check(_lib.load().sa_topk_share(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, ns, n, K,
@@ -267,8 +268,8 @@ def _similarity_gram(q, k, g: PatternGeometry, index_k):
     qs = _compact(q, index_k[T:], _pad32(nv))
     ks = _compact(k, index_k, _pad32(T + nv))
     G = torch.empty(B * H, F, -(-ns // _GRAM_CHUNK), F * (F + 1) // 2, dtype=torch.float32, device=q.device)
-    for h0, h1 in _chunks(B * H, nv * nv * 4):
-        P = torch.empty(h1 - h0, nv, nv, dtype=torch.float32, device=q.device)
+    for h0, h1 in _chunks(B * H, nv * _pad32(nv) * 4):
+        P = torch.empty(h1 - h0, nv, _pad32(nv), dtype=torch.float32, device=q.device)
         _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, math.log(ns / g.S), T, T + nv, P)
         with torch.cuda.device(q.device):
             _lib.check(_lib.load().sa_pattern_gram(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, F, ns,
