@@ -8,21 +8,29 @@ Restates, in float64 with the random sample positions passed in, the reference's
 for a geometry of `frames` frames of height x width tokens after `text` text tokens, with
 `ns` sampled positions per frame.
 
-Pinned by tests/test_oracle_pattern.py against: closed forms (uniform attention: every map
-entry 1/F and every modify factor 1; identical frames), the reference's own op chain for
-constrained_mod_factor on hand-made factors (no adjustment / per-head affine rescale /
-flat heads), a brute-force per-frame loop for the frame mixing, and invariants (map rows sum
-to 1 with the text share; the similarity of a pattern with itself is 1).
+Pinned by tests/test_oracle_pattern.py against: the bf16 values of the text-key bias;
+closed forms for uniform attention (every map entry ns/z, every modify factor 1); closed
+forms for a directed construction in which every quantity of the forward and of both judges
+reduces to scalars (frame f's queries boost the keys of frame f+1 and carry a per-frame slope
+on a position channel; v is one direction per frame): the orientation of the maps, the
+query frame chosen per key frame, both frame cases, the per-row modify factors, the final
+mix, the rank-1 cosine of the similarity judge and the every-third-key share of the
+sparsity judge; the reference's op chain for constrained_mod_factor on hand-made factors;
+and invariants (map rows sum to 1 with the text share; identical frames give similarity 1).
 """
 from __future__ import annotations
-
-import math
 
 import torch
 
 
 def _softmax(x):
     return torch.softmax(x, dim=-1)
+
+
+def composition(ns, S):
+    """The bias of the sampled text keys: log(ns / S) computed in fp32 and rounded to the
+    inputs' dtype, bf16 (partern_attention.py:34-35, 343 and 497: composition.to(q.dtype))."""
+    return float(torch.log(torch.tensor(ns / S, dtype=torch.float32)).to(torch.bfloat16))
 
 
 def index_k(p, frames, S, text):
@@ -37,7 +45,7 @@ def weight_for_patch(q, k, p, frames, S, text):
     idx = index_k(p, frames, S, text)
     qs, ks = q.double()[:, :, idx], k.double()[:, :, idx]
     out = qs @ ks.transpose(-1, -2) / 8
-    out[..., :text] += math.log(ns / S)
+    out[..., :text] += composition(ns, S)
     out = _softmax(out)
     B, H = q.shape[:2]
     i2t = out[:, :, text:, :text].reshape(B, H, frames, ns * text).sum(-1, keepdim=True) / ns
@@ -119,7 +127,7 @@ def judge_similarity(q, k, p, frames, S, text, thr=0.9):
     idx = index_k(p, frames, S, text)
     qs, ks = q.double()[:, :, idx], k.double()[:, :, idx]
     out = qs @ ks.transpose(-1, -2) / 8
-    out[..., :text] += math.log(ns / S)
+    out[..., :text] += composition(ns, S)
     out = _softmax(out)
     B, H = q.shape[:2]
     F = frames

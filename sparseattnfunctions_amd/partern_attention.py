@@ -93,6 +93,13 @@ def _sample_indicator(g: PatternGeometry, device):
     return _cached(("sind", g, str(device)), make)
 
 
+def composition(geometry: PatternGeometry = DEFAULT) -> float:
+    """Bias of the sampled text keys: log(sample_num / S) in fp32, rounded to bf16 as the
+    reference adds it (partern_attention.py:34-35, 343, 497: composition.to(q.dtype))."""
+    g = geometry
+    return float(torch.log(torch.tensor(g.sample_num / g.S, dtype=torch.float32)).to(torch.bfloat16))
+
+
 def get_indexs(geometry: PatternGeometry = DEFAULT):
     """(all_idxs, index_k): `sample_num` random positions of the first frame repeated in every
     frame (torch.randperm on the CPU generator), and the same with the text tokens first."""
@@ -128,7 +135,7 @@ class ParternAttentionColVersion_V2:
         qs, ks = gather_tokens(q, idx), gather_tokens(k, idx)
         nk = idx.numel()
         bias = _cached(("bias", g, str(q.device)), lambda: torch.where(
-            torch.arange(nk, device=q.device) < g.text_length, math.log(g.sample_num / g.S), 0.0).float())
+            torch.arange(nk, device=q.device) < g.text_length, composition(g), 0.0).float())
         return block_sparse_attention(qs[:, :, g.text_length:], ks, _bcast(_sample_indicator(g, q.device), B, H),
                                       _dense(B, H, g.frames * g.sample_num, nk, q.device), scale_factor,
                                       key_bias=_bcast(bias, B, H))
@@ -270,7 +277,7 @@ def _similarity_gram(q, k, g: PatternGeometry, index_k):
     G = torch.empty(B * H, F, -(-ns // _GRAM_CHUNK), F * (F + 1) // 2, dtype=torch.float32, device=q.device)
     for h0, h1 in _chunks(B * H, nv * _pad32(nv) * 4):
         P = torch.empty(h1 - h0, nv, _pad32(nv), dtype=torch.float32, device=q.device)
-        _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, math.log(ns / g.S), T, T + nv, P)
+        _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, composition(g), T, T + nv, P)
         with torch.cuda.device(q.device):
             _lib.check(_lib.load().sa_pattern_gram(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, F, ns,
                                                    G[h0:h1].data_ptr(), _lib.stream_of(q)), "sa_pattern_gram")

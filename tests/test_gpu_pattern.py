@@ -63,6 +63,48 @@ def test_forward_matches_oracle(dev, seed):
     assert err.mean().item() <= 3e-3, err.mean().item()
 
 
+def _directed(a=2.5):
+    # Frame f's queries boost the keys of frame f+1 and carry a per-frame slope g_f on a
+    # position channel (first-frame rows also a per-row text component); v is one direction
+    # per frame. Every value is exact in bf16. Key frame 1 uses the first-frame masses
+    # (img2img_map[0][1] >= 0.1); every other key frame takes the queries of frame i - 1.
+    F, S, T = G.frames, G.S, G.text_length
+    g = [((f * 5) % 7 - 3) / 8 for f in range(F)]
+    q = torch.zeros(1, 1, G.L, 64)
+    k = torch.zeros_like(q)
+    v = torch.zeros_like(q)
+    k[0, 0, :T, 30] = 1
+    v[0, 0, :T, 40] = 1
+    for f in range(F):
+        rows = slice(T + f * S, T + (f + 1) * S)
+        t = torch.arange(S) / 32
+        q[0, 0, rows, (f + 1) % F] = 8 * a
+        q[0, 0, rows, 20] = 8 * g[f]
+        if f == 0:
+            q[0, 0, rows, 30] = (torch.arange(S) % 5 - 2).float()
+        k[0, 0, rows, f] = 1
+        k[0, 0, rows, 20] = t
+        v[0, 0, rows, 41 + f] = 1 + t
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def test_directed_forward_matches_oracle(dev):
+    case("pattern forward directed construction")
+    q, k, v = _directed()
+    _, idx = pa.get_indexs(G)
+    p = idx[G.text_length: G.text_length + G.sample_num] - G.text_length
+    proc = pa.ParternAttentionColVersion_V2(G)
+    out = proc(q.to(dev), k.to(dev), v.to(dev), index_k=idx).cpu()
+    want, parts = opat.pattern_v2(q, k, v, p, G.frames, G.S, G.text_length, return_parts=True)
+    want_case = torch.zeros(G.frames, dtype=torch.bool)
+    want_case[1] = True
+    assert torch.equal(parts["cases"][0, 0], want_case)
+    assert torch.equal(proc.last_plan["frame_case"].cpu().bool()[0, 0], want_case)
+    err = (out.double() - want).abs()
+    assert err.max().item() <= 3e-2, err.max().item()
+    assert err.mean().item() <= 3e-3, err.mean().item()
+
+
 def test_reference_geometry_smoke(dev):
     # 1.5-5B geometry, 2 heads: runs, finite, text rows equal dense attention of the text rows.
     case("pattern forward 1.5-5B geometry")
