@@ -143,6 +143,23 @@ def other_configs(q, k, v, dev):
                              "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
                              "effective_tflop_per_call": round(fs / 1e12, 4)}
 
+    # Pooled-attention map (attn_with_pooling, block_size 64) on the C2 inputs: dense attention
+    # that also returns the normalised 2-D max-pooled probabilities, against the same kernel
+    # over every block without the map.
+    from sparseattnfunctions_amd.block_mask_attn import dense_kv_list
+    from sparseattnfunctions_amd.utils.attn_pooling_kernel import attn_with_pooling
+
+    nb = math.ceil(L / 64)
+    f_dense = 4 * D * B * H * L * L
+    ms_pool = time_fn(lambda: attn_with_pooling(q, k, v, False, 0.125, 64), iters=5)
+    ms_pool_causal = time_fn(lambda: attn_with_pooling(q, k, v, True, 0.125, 64), iters=5)
+    kv_all = dense_kv_list(B, H, nb, nb, q.device)
+    ms_dense = time_fn(lambda: block_sparse_attention(q, k, v, kv_all, 0.125), iters=5)
+    out["attn_pooling"] = {"ms": round(ms_pool, 4), "tflops": _tflops(f_dense, ms_pool),
+                           "dense_attention_ms": round(ms_dense, 4), "causal_ms": round(ms_pool_causal, 4),
+                           "block_size": 64}
+    del kv_all
+
     # 1.5-5B geometry (B=2, H=48, L=45104): unified_judge and the frame-pattern attention on
     # every head (synthetic inputs drawn on the GPU).
     from sparseattnfunctions_amd import partern_attention as pa

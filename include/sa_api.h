@@ -128,6 +128,27 @@ int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_strides[3], co
                                void* stream);
 
 /*
+ * Dense or causal attention that also returns the 2-D max-pooled attention map, a block-score
+ * source (attn_with_pooling = _attention_pooling.forward, utils/attn_pooling_kernel.py:18-289):
+ *   out[b,h,r] = softmax_c(q[b,h,r] . k[b,h/(H/H_kv),c] * sm_scale) v[...]     bf16 [B,H,L,64]
+ *                (causal: keys c <= r only)
+ *   Po[b,h,i,j] = max over queries r of block i and keys c of block j of the softmax P[r][c],
+ *                 then each row of Po divided by its sum                          fp32 [B,H,nd,nd]
+ * with blocks of block_size in {32, 64, 128} tokens, nd = ceil(L / block_size) <= 8192, and
+ * Po[i][j] = 0 for j > i when causal. k and v have H_kv heads (H_kv divides H). Po has
+ * element strides po_strides (b, h, i) and unit stride over j. workspace: at least
+ * sa_attn_pooling_workspace() bytes, 256-byte aligned (kv lists, per-row maxima of every
+ * G-key column and log-sum-exps: about 4*B*H*L*L/G bytes, G = 32 for block_size 32, else 64).
+ */
+int sa_attn_pooling_workspace(int B, int H, int L, int block_size, int64_t* bytes);
+int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                        const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                        uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L,
+                        int D, int causal, float sm_scale, int block_size, float* po,
+                        const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+/*
  * (host) Dispatch order of the attention work items (one per list row) for a GPU whose
  * workgroups are dealt round-robin to n_xcd XCDs (8 on MI355X): each XCD gets a
  * contiguous range of (b, h) heads, so their K/V stay in that XCD's L2, and within it the

@@ -18,11 +18,13 @@ _SUBMODULES = (
     "utils.block_sparse_attn_kernel",
     "utils.merge_unmerge",
     "utils.mask_related",
+    "utils.attn_pooling_kernel",
     "block_mask_attn",
     "SparseGen_Plus",
     "combined_attn",
     "MergeAttention",
     "SildingTileAttention",
+    "partern_attention",
 )
 
 

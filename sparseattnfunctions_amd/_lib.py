@@ -48,6 +48,12 @@ _PROTOTYPES = {
          _P, _I, _P, _I, _P, ctypes.c_int64, _P],
     ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
+    "sa_attn_pooling_workspace": (_I, [_I, _I, _I, _I, _I64P]),
+    "sa_attn_pooling_fwd": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,
+         ctypes.c_int64, _P],
+    ),
     "sa_gather_tokens_heads": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _I64P, _P]),
     "sa_pattern_maps": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _P]),
     "sa_sampled_probs": (_I, [_P, _P, _I, _I, _I, _I, _I, _F, _I, _F, _I, _I, _P, ctypes.c_int64, ctypes.c_int64,

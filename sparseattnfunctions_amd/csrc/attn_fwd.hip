@@ -83,6 +83,15 @@ struct FwdArgs {
   const int32_t* q_rows;       // [Lq] q row of query i (outside [0, q_src_rows): zeros); null = i
   const int32_t* o_rows;       // [Lq] out row of query i (outside [0, o_dst_rows): dropped); null = i
   int q_src_rows, o_dst_rows;
+  int kv_rep;                  // query heads per key/value head (key head of query head h: h / kv_rep)
+  // Pooling mode (kPool > 0): per query row, the maximum scaled logit (log2 domain) of every
+  // kPool-key column is stored to pool_r[((bh * nqb + row / 64) * pool_ncol + column) * 64 +
+  // row % 64] (one query block's maxima are contiguous), and the row's log2-sum-exp2 to
+  // pool_lse[bh * pool_lpad + row]; pool_ncol = nkb * 64 / kPool, pool_lpad = nqb * 64.
+  float* pool_r;
+  int pool_ncol;
+  int pool_lpad;
+  float* pool_lse;
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
@@ -163,8 +172,9 @@ __device__ inline void dma_tile(const void* base, uint32_t bytes, uint32_t tile_
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kWaitLgkm0 = 0xC07F;
 
-template <bool kBias, bool kMask>
+template <bool kBias, bool kMask, int kPool>
 __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
+  static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
   // Separate LDS objects for K, V and bias so that the compiler's own wait analysis can
   // tell a copy into one from a read of another.
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes];
@@ -200,8 +210,9 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       kMask ? (const __attribute__((address_space(4))) int32_t*)(a.kv_slot + list_row * a.max_cnt) : nullptr;
 
   const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh;
-  const uint16_t* khead = a.k + b * a.k_sb + h * a.k_sh;
-  const uint16_t* vhead = a.v + b * a.v_sb + h * a.v_sh;
+  const int hk = a.kv_rep > 1 ? h / a.kv_rep : h;
+  const uint16_t* khead = a.k + b * a.k_sb + hk * a.k_sh;
+  const uint16_t* vhead = a.v + b * a.v_sb + hk * a.v_sh;
   uint16_t* obase = a.o + b * a.o_sb + h * a.o_sh;
   const float* bhead = kBias ? a.bias + b * a.bias_sb + h * a.bias_sh : nullptr;
   const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
@@ -387,6 +398,28 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
       // ---- P = exp2(S * sc - m) in bf16 and the row sums (m = 0 in the fast pass).
       const float sc = kBias ? 1.f : a.scale_log2;  // S is already scaled with a bias
+      if constexpr (kPool != 0) {
+        // Row maxima of the scaled logits per kPool-key column. Lane l stores row
+        // qb * 64 + l (query group hh, column col): one 256-byte store per column.
+        if (block_ok(kb)) {
+          constexpr int kCols = kBlock / kPool;  // columns per tile: 2 (32-key) or 1 (64-key)
+          float* rp = a.pool_r + (((int64_t)bh * a.nqb + qb) * a.pool_ncol + kb * kCols) * kBlock + lane;
+#pragma unroll
+          for (int cc = 0; cc < kCols; ++cc) {
+            float mx[2];
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+              float x = -INFINITY;
+#pragma unroll
+              for (int c = (kCols == 2 ? cc : 0); c < (kCols == 2 ? cc + 1 : 2); ++c)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) x = fmaxf(x, S[g][c][e]);
+              mx[g] = xhalf_max(x) * sc;  // sc > 0: max(S) * sc = max(S * sc)
+            }
+            rp[cc * kBlock] = hh ? mx[1] : mx[0];
+          }
+        }
+      }
       float mu[2] = {0.f, 0.f};
       if (kSafe) {
         // Row max; the running max is raised only when this tile exceeds it by more than
@@ -508,6 +541,12 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   for (int g = 0; g < 2; ++g) {
     const float l_tot = xhalf_sum(l[g]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if constexpr (kPool != 0) {
+      // log2-sum-exp2 of the row: P = exp2(S * sc - m) / l_tot (m = -inf: the fast pass, 0).
+      if (g == hh)
+        a.pool_lse[(int64_t)bh * a.pool_lpad + qb * kBlock + lane] =
+            (m[g] == -INFINITY ? 0.f : m[g]) + log2f(l_tot);
+    }
     int row = qb * kBlock + 32 * g + col;
     bool store = row < a.Lq;
     if (store && a.o_rows) {  // remapped layout: query i goes to out row o_rows[i]
@@ -577,7 +616,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                bool lists_shared, const int32_t* kv_slot, const uint64_t* tile_masks, const float* key_bias,
                const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
-               const char* fn) {
+               const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
+               float* pool_lse = nullptr) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -639,16 +679,28 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.o_rows = o_rows;
   a.q_src_rows = q_rows ? q_src_rows : Lq;
   a.o_dst_rows = o_rows ? o_dst_rows : Lq;
+  a.kv_rep = kv_rep;
+  a.pool_r = pool_r;
+  a.pool_ncol = pool_cols ? nkb * (kBlock / pool_cols) : 0;
+  a.pool_lpad = nqb * kBlock;
+  a.pool_lse = pool_lse;
+  SA_REQUIRE(pool_cols == 0 || (pool_r && pool_lse && !q_rows && !o_rows),
+             "%s: pooling needs its buffers and no row maps", fn);
 
   hipStream_t s = sa::as_stream(stream);
   const dim3 g((unsigned)grid), blk(64 * kWaves);
   if (kv_slot) {
     if (key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
-    hipLaunchKernelGGL((bsa_fwd_kernel<false, true>), g, blk, 0, s, a);
+    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 32>), g, blk, 0, s, a);
+    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 64>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 0>), g, blk, 0, s, a);
   } else if (key_bias) {
-    hipLaunchKernelGGL((bsa_fwd_kernel<true, false>), g, blk, 0, s, a);
+    if (pool_cols) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0>), g, blk, 0, s, a);
   } else {
-    hipLaunchKernelGGL((bsa_fwd_kernel<false, false>), g, blk, 0, s, a);
+    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 32>), g, blk, 0, s, a);
+    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 64>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0>), g, blk, 0, s, a);
   }
   return sa::check_launch(fn);
 }
@@ -691,4 +743,212 @@ extern "C" int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_str
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, lists_shared != 0, kv_slot, tile_masks, key_bias, bias_strides, sm_scale, work_order,
                     n_slots, q_rows, q_src_rows, o_rows, o_dst_rows, stream, "sa_block_sparse_fwd_mapped");
+}
+
+// ---------------------------------------------------------------------------------------
+// Pooled attention map (attn_with_pooling, utils/attn_pooling_kernel.py:18-289): the
+// attention kernel in pooling mode stores each row's maximum scaled logit per 32- or 64-key
+// column and its log2-sum-exp2; pool_reduce_kernel turns them into
+//   Po[i][j] = max over rows r of query block i, keys of key block j of exp2(R[c][r] - lse[r])
+// (the largest softmax probability of the block), each row of Po divided by its sum.
+namespace {
+
+constexpr int kPoolMaxNd = 8192;  // key blocks per row (dynamic LDS of the reduce: 32 KB)
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct PoolLayout {
+  int nqb, nkb, G, ncol_alloc, lpad;
+  size_t idx, cnt, slot, mask, r, lse, total;  // byte offsets into the workspace
+};
+
+PoolLayout pool_layout(int B, int H, int L, int block_size) {
+  PoolLayout p;
+  p.nqb = p.nkb = sa::cdiv(L, kBlock);
+  p.G = block_size == 32 ? 32 : 64;
+  p.ncol_alloc = p.nkb * (kBlock / p.G);
+  p.lpad = p.nqb * kBlock;
+  size_t o = 0;
+  p.idx = o;  o += align256((size_t)p.nqb * p.nkb * 4);
+  p.cnt = o;  o += align256((size_t)p.nqb * 4);
+  p.slot = o; o += align256((size_t)p.nqb * p.nkb * 4);
+  p.mask = o; o += align256(kBlock * 8);
+  p.r = o;    o += align256((size_t)B * H * p.ncol_alloc * p.lpad * 4);
+  p.lse = o;  o += align256((size_t)B * H * p.lpad * 4);
+  p.total = o;
+  return p;
+}
+
+// Dense (all key blocks) or causal (blocks <= the query block, the diagonal tile masked
+// to keys <= query) kv lists, shared by every head; mask slot 0 = lower triangle.
+struct PoolListArgs {
+  int32_t* idx;
+  int32_t* cnt;
+  int32_t* slot;
+  uint64_t* mask;
+  int nqb, nkb, causal;
+};
+
+__global__ __launch_bounds__(256) void pool_lists_kernel(PoolListArgs a) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < (int64_t)a.nqb * a.nkb) {
+    const int qb = (int)(t / a.nkb), j = (int)(t - (int64_t)qb * a.nkb);
+    a.idx[t] = j;
+    a.slot[t] = (a.causal && j == qb) ? 0 : -1;
+  }
+  if (t < a.nqb) a.cnt[t] = a.causal ? min((int)t + 1, a.nkb) : a.nkb;
+  if (t < kBlock) a.mask[t] = t == kBlock - 1 ? ~0ull : ((2ull << t) - 1ull);  // row t: keys 0..t
+}
+
+struct PoolReduceArgs {
+  const float* r;  // [B*H][nqb][ncol_alloc][64]
+  int nqb, ncol_alloc;
+  int lpad;
+  const float* lse;
+  int L, bs, G, nd, ncol, causal, H;
+  float* po;
+  int64_t po_sb, po_sh, po_si;
+  int64_t total;  // B * H * nd
+};
+
+// One workgroup per (bh, query block i); wave w takes key blocks j in [8w + 32t, 8w + 32t + 8);
+// lane l the rows r0 + l and r0 + 64 + l of the block. Every load is issued at a clamped,
+// in-bounds row and column, and entries outside the block or the causal lists are discarded
+// by selects, so the eight loads of a step are in flight together. Dynamic LDS: nd floats.
+__global__ __launch_bounds__(256) void pool_reduce_kernel(PoolReduceArgs a) {
+  constexpr int kU = 8;
+  extern __shared__ float row[];
+  __shared__ float part[256];
+  const int64_t w = blockIdx.x;
+  if (w >= a.total) return;  // uniform over the workgroup
+  const int64_t bh = w / a.nd;
+  const int i = (int)(w - bh * a.nd);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r0 = i * a.bs, r1 = min(r0 + a.bs, a.L);
+  const int ra = r0 + lane, rbw = r0 + 64 + lane;
+  const int ra_c = min(ra, r1 - 1), rb_c = min(rbw, r1 - 1);  // rows read (always < L)
+  const float* lb = a.lse + bh * a.lpad;
+  const float lse_a = lb[ra_c];
+  const float lse_b = lb[rb_c];
+  // column 0 of rows ra_c / rb_c; column c is c * 64 floats further
+  const float* pa = a.r + ((bh * a.nqb + ra_c / kBlock) * a.ncol_alloc) * kBlock + ra_c % kBlock;
+  const float* pb = a.r + ((bh * a.nqb + rb_c / kBlock) * a.ncol_alloc) * kBlock + rb_c % kBlock;
+  const int cpb = a.bs / a.G;                           // columns per key block: 1 or 2
+  const int jend = a.causal ? min(i + 1, a.nd) : a.nd;  // blocks past jend are 0
+  const bool two_rows = a.bs > kBlock;                  // block_size 128: two rows per lane
+  for (int j0 = kU * wave; j0 < a.nd; j0 += 4 * kU) {
+    // Phase 1: every load of the step (no branches between them).
+    int cr[kU][2];
+    bool ok[kU][2];
+    float va[kU][2], vb[kU][2];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const int j = j0 + u, c = j * cpb + v;
+        ok[u][v] = v < cpb && j < jend && c < a.ncol;
+        cr[u][v] = ok[u][v] ? c : 0;
+        va[u][v] = pa[cr[u][v] * kBlock];
+      }
+    if (two_rows) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) vb[u][v] = pb[cr[u][v] * kBlock];
+    }
+    // Phase 2: probabilities, with entries outside the block or the causal lists discarded
+    // (causal: column c was computed for row r only where its 64-key tile is in r's list).
+    float x[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      float m = 0.f;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const int ctile = cr[u][v] * a.G / kBlock;
+        const float ea = __builtin_amdgcn_exp2f(va[u][v] - lse_a);
+        m = fmaxf(m, (ok[u][v] && ra < r1 && !(a.causal && ctile > ra / kBlock)) ? ea : 0.f);
+        if (two_rows) {
+          const float eb = __builtin_amdgcn_exp2f(vb[u][v] - lse_b);
+          m = fmaxf(m, (ok[u][v] && rbw < r1 && !(a.causal && ctile > rbw / kBlock)) ? eb : 0.f);
+        }
+      }
+      x[u] = m;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) x[u] = fmaxf(x[u], __shfl_xor(x[u], o));
+      if (lane == u && j0 + u < a.nd) row[j0 + u] = x[u];
+    }
+  }
+  __syncthreads();
+  float s = 0.f;
+  for (int j = t; j < a.nd; j += 256) s += row[j];
+  part[t] = s;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (t < st) part[t] += part[t + st];
+    __syncthreads();
+  }
+  const float tot = part[0];
+  const int b = (int)(bh / a.H), h = (int)(bh - (int64_t)b * a.H);
+  float* dst = a.po + b * a.po_sb + h * a.po_sh + (int64_t)i * a.po_si;
+  for (int j = t; j < a.nd; j += 256) dst[j] = row[j] / tot;
+}
+
+}  // namespace
+
+extern "C" int sa_attn_pooling_workspace(int B, int H, int L, int block_size, int64_t* bytes) {
+  const char* fn = "sa_attn_pooling_workspace";
+  SA_REQUIRE(bytes, "%s: null bytes", fn);
+  SA_REQUIRE(B > 0 && H > 0 && L > 0, "%s: bad shape B=%d H=%d L=%d", fn, B, H, L);
+  SA_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128, "%s: block_size %d not in {32, 64, 128}",
+             fn, block_size);
+  *bytes = (int64_t)pool_layout(B, H, L, block_size).total;
+  return sa::ok();
+}
+
+extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                   const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                   uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L, int D,
+                                   int causal, float sm_scale, int block_size, float* po,
+                                   const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  const char* fn = "sa_attn_pooling_fwd";
+  SA_REQUIRE(po && po_strides && workspace, "%s: null pointer", fn);
+  SA_REQUIRE(B > 0 && H > 0 && L > 0, "%s: bad shape B=%d H=%d L=%d", fn, B, H, L);
+  SA_REQUIRE(H_kv > 0 && H % H_kv == 0, "%s: H_kv=%d must divide H=%d", fn, H_kv, H);
+  SA_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128, "%s: block_size %d not in {32, 64, 128}",
+             fn, block_size);
+  const PoolLayout p = pool_layout(B, H, L, block_size);
+  const int nd = sa::cdiv(L, block_size);
+  if (nd > kPoolMaxNd) return sa::fail(SA_ERR_UNSUPPORTED, "%s: %d blocks per row > %d", fn, nd, kPoolMaxNd);
+  SA_REQUIRE(workspace_bytes >= (int64_t)p.total, "%s: workspace of %lld bytes < %lld", fn,
+             (long long)workspace_bytes, (long long)p.total);
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s: workspace not 256-byte aligned", fn);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  PoolListArgs la;
+  la.idx = reinterpret_cast<int32_t*>(ws + p.idx);
+  la.cnt = reinterpret_cast<int32_t*>(ws + p.cnt);
+  la.slot = reinterpret_cast<int32_t*>(ws + p.slot);
+  la.mask = reinterpret_cast<uint64_t*>(ws + p.mask);
+  la.nqb = p.nqb; la.nkb = p.nkb; la.causal = causal ? 1 : 0;
+  hipStream_t s = sa::as_stream(stream);
+  const int64_t n_list = std::max<int64_t>((int64_t)p.nqb * p.nkb, kBlock);
+  hipLaunchKernelGGL(pool_lists_kernel, dim3((unsigned)((n_list + 255) / 256)), dim3(256), 0, s, la);
+  if (int rc = sa::check_launch(fn)) return rc;
+  float* r = reinterpret_cast<float*>(ws + p.r);
+  float* lse = reinterpret_cast<float*>(ws + p.lse);
+  if (int rc = launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, L, D, la.idx, la.cnt,
+                          p.nkb, true, causal ? la.slot : nullptr, causal ? la.mask : nullptr, nullptr, nullptr,
+                          sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, lse))
+    return rc;
+  PoolReduceArgs ra;
+  ra.r = r; ra.nqb = p.nqb; ra.ncol_alloc = p.ncol_alloc; ra.lpad = p.lpad; ra.lse = lse;
+  ra.L = L; ra.bs = block_size; ra.G = p.G; ra.nd = nd; ra.ncol = sa::cdiv(L, p.G); ra.causal = la.causal;
+  ra.H = H; ra.po = po; ra.po_sb = po_strides[0]; ra.po_sh = po_strides[1]; ra.po_si = po_strides[2];
+  ra.total = (int64_t)B * H * nd;
+  SA_REQUIRE(ra.total < (1LL << 31), "%s: grid too large", fn);
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)ra.total), dim3(256), (unsigned)(nd * sizeof(float)), s, ra);
+  return sa::check_launch(fn);
 }

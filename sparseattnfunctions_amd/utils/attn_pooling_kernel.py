@@ -1,0 +1,63 @@
+"""`attn_with_pooling` of special_attentions/utils/attn_pooling_kernel.py (:230-289), on MI355X.
+
+Dense (or causal) attention that also returns the 2-D max-pooled attention map
+Po [B, H, nd, nd] (nd = ceil(L / block_size), block_size in {32, 64, 128}): Po[i][j] is the
+largest softmax probability of query block i against key block j, each row then divided by
+its sum. It is a block-score map for the mask builders, e.g.
+`SparseGen_Plus.transfer_attn_to_kv_list(Po, ...)` for block_size 64.
+
+One call runs the block-sparse attention kernel over every key block (causal: the blocks up
+to the diagonal, the diagonal tile masked to keys <= query) in its pooling mode. Each query
+row stores its largest scaled logit per 32- or 64-key column and its log-sum-exp to a
+workspace. A reduce kernel then forms Po = max over the block's rows of exp2(R - lse) and
+normalises it. The probability matrix itself is never written.
+
+Differences from the reference: q, k and v must be bf16 (the reference also accepts fp16 and
+fp32, and casts bf16 up to fp32). head_dim must be 64. The rows of a last, partial query
+block that lie past L take no part in its maximum; the reference reads them without bounds
+checks.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from .. import _lib
+from .block_sparse_attn_kernel import _prep_qkv
+
+
+class _attention_pooling(torch.autograd.Function):
+    """forward(ctx, q, k, v, causal, sm_scale, block_size) -> (o, Po), as the reference
+    (:230-287); like the reference it has no backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, sm_scale, block_size):
+        assert block_size in {32, 64, 128}
+        q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
+        _lib.require_gpu(q, k, v)
+        B, H, L, D = q.shape
+        Hk = k.shape[1]
+        assert k.shape[-1] == D and v.shape[-1] == D
+        assert k.shape[1] == v.shape[1]
+        if k.shape[0] != B or v.shape[0] != B or k.shape[2] != L or v.shape[2] != L:
+            raise ValueError(f"k, v must be [B, H_kv, {L}, {D}], got {tuple(k.shape)}, {tuple(v.shape)}")
+        nd = math.ceil(L / block_size)
+        o = torch.empty_like(q)
+        po = torch.empty(B, H, nd, nd, dtype=torch.float32, device=q.device)
+        lib = _lib.load()
+        ws_bytes = ctypes.c_int64(0)
+        _lib.check(lib.sa_attn_pooling_workspace(B, H, L, block_size, ctypes.byref(ws_bytes)),
+                   "sa_attn_pooling_workspace")
+        ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+        with torch.cuda.device(q.device):
+            _lib.check(lib.sa_attn_pooling_fwd(
+                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                v.data_ptr(), _lib.i64(*v.stride()[:3]), o.data_ptr(), _lib.i64(*o.stride()[:3]),
+                B, H, Hk, L, D, 1 if causal else 0, float(sm_scale), block_size, po.data_ptr(),
+                _lib.i64(*po.stride()[:3]), ws.data_ptr(), ws.numel(), _lib.stream_of(q)), "sa_attn_pooling_fwd")
+        return o, po
+
+
+attn_with_pooling = _attention_pooling.apply

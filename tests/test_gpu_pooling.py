@@ -1,0 +1,80 @@
+"""GPU parity of attn_with_pooling (utils/attn_pooling_kernel.py) against the fp64 oracle.
+
+Tolerances: out max-abs <= 2e-2 and mean-abs <= 2e-3 (the attention bar); Po relative 5e-3
+(+1e-7 absolute): its entries are exp2 of fp32 logits minus the row's log-sum-exp, whose
+row sum accumulates bf16-rounded probabilities.
+At the C2 shape, size-independent properties: out is bit-identical to the block-sparse kernel
+over every block (the pooling mode only adds stores), Po rows sum to one, causal Po is zero
+above the diagonal.
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import case
+from oracle.pooling import pooled_attention
+from sparseattnfunctions_amd.utils.attn_pooling_kernel import attn_with_pooling
+
+pytestmark = pytest.mark.gpu
+
+
+def _qkv(seed, B, H, Hk, L, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, H, L, 64, generator=g) * scale).to(torch.bfloat16)
+    k = (torch.randn(B, Hk, L, 64, generator=g) * scale).to(torch.bfloat16)
+    v = torch.randn(B, Hk, L, 64, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("Hk", [4, 2])
+def test_pooled_attention_matches_oracle(dev, bs, causal, Hk):
+    case(f"attn_with_pooling bs={bs} causal={causal} Hk={Hk}")
+    q, k, v = _qkv(bs + 7 * Hk + causal, 1, 4, Hk, 1000, scale=1.5)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, 0.125, bs)
+    want_o, want_po = pooled_attention(q, k, v, causal, 0.125, bs)
+    err = (o.cpu().double() - want_o).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3, (err.max().item(), err.mean().item())
+    assert po.shape == want_po.shape and po.dtype == torch.float32
+    assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7), (po.cpu().double() - want_po).abs().max()
+    if causal:
+        nd = po.shape[-1]
+        assert torch.equal(po.cpu()[..., torch.ones(nd, nd, dtype=torch.bool).triu(1)],
+                           torch.zeros_like(po.cpu()[..., torch.ones(nd, nd, dtype=torch.bool).triu(1)]))
+
+
+def test_pooled_attention_large_scores(dev):
+    # scores of several hundred: the kernel's safe pass; Po must not depend on it
+    case("attn_with_pooling large scores")
+    q, k, v = _qkv(21, 1, 2, 2, 640, scale=6.0)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), False, 0.125, 64)
+    want_o, want_po = pooled_attention(q, k, v, False, 0.125, 64)
+    assert (o.cpu().double() - want_o).abs().max().item() <= 2e-2
+    assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_pooled_attention_c2_shape_properties(dev, causal):
+    case(f"attn_with_pooling C2 shape causal={causal}")
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention
+    from sparseattnfunctions_amd.block_mask_attn import dense_kv_list
+    B, H, L = 2, 30, 17776
+    gen = torch.Generator(device=dev).manual_seed(5)
+    q, k, v = (torch.randn(B, H, L, 64, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
+    o, po = attn_with_pooling(q, k, v, causal, 0.125, 64)
+    torch.cuda.synchronize()
+    nd = math.ceil(L / 64)
+    assert po.shape == (B, H, nd, nd)
+    assert torch.isfinite(po).all() and (po >= 0).all()
+    assert torch.allclose(po.sum(-1), torch.ones(B, H, nd, device=dev), atol=1e-5)
+    if causal:
+        assert (po[..., torch.ones(nd, nd, dtype=torch.bool, device=dev).triu(1)] == 0).all()
+        # a few rows against torch's causal SDPA in fp32
+        ref = torch.nn.functional.scaled_dot_product_attention(q[:1, :2].float(), k[:1, :2].float(),
+                                                               v[:1, :2].float(), is_causal=True)
+        assert (o[:1, :2].float() - ref).abs().max().item() <= 2e-2
+    else:
+        dense = block_sparse_attention(q, k, v, dense_kv_list(B, H, nd, nd, q.device), 0.125)
+        assert torch.equal(o, dense)
