@@ -317,12 +317,24 @@ int sa_topk_share(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int
 /*
  * Gram matrices of the sampled frame-pair attention patterns (judge_similarity,
  * partern_attention.py:497-510): with P the [F*ns x F*ns] video part of the sampled
- * probabilities, G[bh][f2][chunk][pair(f1,f3)] = sum over s1 in the chunk (20 positions)
+ * probabilities, G[bh][f2][chunk][pair(f1,f3)] = sum over s1 in the chunk (8 positions)
  * and all s2 of P[f1*ns + s1][f2*ns + s2] * P[f3*ns + s1][f2*ns + s2], f1 <= f3 (pairs in
  * row-major upper-triangle order). F <= 12, ns <= 512.
  */
 int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int F,
                     int ns, float* G, void* stream);
+
+/*
+ * The Gram partials of sa_pattern_gram computed straight from the sampled rows, without
+ * writing the probabilities (judge_similarity, partern_attention.py:480-514): q_rows
+ * [BH][rows_pad][64] holds the F*ns sampled video queries (row f*ns + s), k_rows
+ * [BH][keys_pad][64] the T text keys then the F*ns sampled keys (bf16 contiguous, pads:
+ * multiples of 32); the probabilities are softmax over all T + F*ns keys of
+ * q . k * sm_scale (+ bias on the T text keys). G as sa_pattern_gram; F <= 12.
+ */
+int sa_pattern_sim_gram(const uint16_t* q_rows, const uint16_t* k_rows, int BH, int F, int ns,
+                        int T, int rows_pad, int keys_pad, float sm_scale, float bias, float* G,
+                        void* stream);
 
 /*
  * Routing decision of unified_judge (partern_attention.py:516-521) per head:

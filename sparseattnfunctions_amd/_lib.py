@@ -60,6 +60,7 @@ _PROTOTYPES = {
                               _P]),
     "sa_topk_share": (_I, [_P, ctypes.c_int64, ctypes.c_int64, _I, _I, _I, _I, _P, _P]),
     "sa_pattern_gram": (_I, [_P, ctypes.c_int64, ctypes.c_int64, _I, _I, _I, _P, _P]),
+    "sa_pattern_sim_gram": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _F, _F, _P, _P]),
     "sa_pattern_judge_finish": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _F, _P, _P, _P, _P, _P]),
     "sa_pattern_plan": (_I, [_P, _I64P, _P, _I, _I, _I, _I, _I, _F, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P]),
     "sa_pattern_combine": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,

@@ -27,15 +27,23 @@ constexpr float kLog2e = 1.4426950408889634f;
 typedef unsigned jd_u32x4 __attribute__((ext_vector_type(4)));
 typedef float jd_f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ inline sa_f32x16 score_tile(const uint16_t* kp, const sa_bf16x8 (&qf)[4]) {
-  jd_u32x4 kop[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) kop[s] = *reinterpret_cast<const jd_u32x4*>(kp + 16 * s);
+__device__ inline sa_f32x16 score_tile_k(const jd_u32x4 (&kop)[4], const sa_bf16x8 (&qf)[4]) {
   sa_f32x16 t = {};
 #pragma unroll
   for (int s = 0; s < 4; ++s)
     t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(sa_bf16x8, kop[s]), qf[s], t, 0, 0, 0);
   return t;
+}
+
+__device__ inline void load_k(const uint16_t* kp, jd_u32x4 (&kop)[4]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kop[s] = *reinterpret_cast<const jd_u32x4*>(kp + 16 * s);
+}
+
+__device__ inline sa_f32x16 score_tile(const uint16_t* kp, const sa_bf16x8 (&qf)[4]) {
+  jd_u32x4 kop[4];
+  load_k(kp, kop);
+  return score_tile_k(kop, qf);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -225,7 +233,7 @@ __global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
 // Thread t takes columns s2 = t, t + 256, ... of frame f2 and accumulates, over its s1 chunk,
 // the products of the F values P[f1*ns + s1][f2*ns + s2] (f1 = 0..F-1) of each column.
 // Partial sums go to G_part[bh][f2][chunk][pair]; the finish kernel adds the chunks in order.
-constexpr int kGramChunk = 20;
+constexpr int kGramChunk = 8;
 
 struct GramArgs {
   const float* P;
@@ -277,6 +285,179 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// simgram_kernel: judge_similarity with the probabilities kept on chip. One wave per (bh,
+// chunk of kGramChunk = 8 sample positions s1). Its four 32-column query groups hold, for
+// two positions each, the F frames' rows f1*ns + s1 (column 16*(s1 & 1) + f1; columns with
+// f1 >= F and positions past ns are zero queries whose results are never used).
+//   pass 1: row max and sum over every key, bias on the T text keys (as probs_kernel);
+//   pass 2, per key frame f2: the probabilities of the frame's ns keys, 32 at a time, go
+//           through LDS ([group][key][column]); lane (key k, half sl) then adds, for each
+//           group, the products P[f1][k] P[f3][k] of its position's F rows into F(F+1)/2
+//           per-lane sums. After the frame the 64 lanes' sums are added through LDS, in lane
+//           order, into G[bh][f2][chunk][pair].
+struct SimGramArgs {
+  const uint16_t* qs;  // [BH][rows_pad][64], row f*ns + s
+  const uint16_t* ks;  // [BH][keys_pad][64], T text keys then F*ns sampled keys
+  int ns, T, keys, keys_pad, rows_pad;
+  float scale_log2, bias_log2;
+  float* G;  // [BH][F][n_chunks][NP]
+  int n_chunks;
+  int64_t total;  // BH * n_chunks
+};
+
+constexpr int kSgGroups = kGramChunk / 2;  // query groups per wave
+constexpr int kSgStride = 36;              // LDS row stride of the P tiles (conflict-free b128 reads)
+
+template <int F>
+__global__ __launch_bounds__(256, 2) void simgram_kernel(SimGramArgs a) {
+  static_assert(F >= 1 && F <= 12, "frames");
+  constexpr int NP = F * (F + 1) / 2;
+  constexpr int kRed = 64 * NP;
+  constexpr int kTile = kSgGroups * 32 * kSgStride;
+  constexpr int kLds = kRed > kTile ? kRed : kTile;
+  constexpr int kRead = (F + 3) / 4;  // 16-byte reads per row of F values
+  __shared__ __attribute__((aligned(16))) float lds[4][kLds];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
+  if (wid >= a.total) return;  // no workgroup barriers below
+  const int64_t bh = wid / a.n_chunks;
+  const int chunk = (int)(wid - bh * a.n_chunks);
+  const int col = lane & 31, hh = lane >> 5;
+  float* L = lds[wave];
+
+  sa_bf16x8 qf[kSgGroups][4];
+#pragma unroll
+  for (int g = 0; g < kSgGroups; ++g) {
+    const int s1 = chunk * kGramChunk + 2 * g + (col >> 4), f1 = col & 15;
+    const bool ok = f1 < F && s1 < a.ns;
+    const uint16_t* qp = a.qs + (bh * a.rows_pad + (ok ? f1 * a.ns + s1 : 0)) * kD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const jd_u32x4 w = ok ? *reinterpret_cast<const jd_u32x4*>(qp + 16 * s) : jd_u32x4{0u, 0u, 0u, 0u};
+      qf[g][s] = __builtin_bit_cast(sa_bf16x8, w);
+    }
+  }
+
+  // ---- pass 1: row statistics over every key
+  float m[kSgGroups], l[kSgGroups];
+#pragma unroll
+  for (int g = 0; g < kSgGroups; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+  }
+  const uint16_t* kbase = a.ks + (bh * a.keys_pad + col) * kD + 8 * hh;
+  for (int kt = 0; kt < a.keys_pad / 32; ++kt) {
+    jd_u32x4 kop[4];
+    load_k(kbase + (int64_t)kt * 32 * kD, kop);
+    const bool uniform = 32 * kt + 32 <= a.keys && (32 * kt + 32 <= a.T || 32 * kt >= a.T);
+    const float tb = 32 * kt < a.T ? a.bias_log2 : 0.f;
+#pragma unroll
+    for (int g = 0; g < kSgGroups; ++g) {
+      const sa_f32x16 t = score_tile_k(kop, qf[g]);
+      float x[16], tmax = -INFINITY;
+      if (uniform) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = fmaf(t[i], a.scale_log2, tb);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = 32 * kt + 8 * (i >> 2) + 4 * hh + (i & 3);
+          x[i] = key >= a.keys ? -INFINITY : fmaf(t[i], a.scale_log2, key < a.T ? a.bias_log2 : 0.f);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, x[i]);
+      const float mn = fmaxf(m[g], tmax);
+      if (mn != -INFINITY) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum += __builtin_amdgcn_exp2f(x[i] - mn);
+        l[g] = l[g] * __builtin_amdgcn_exp2f(m[g] - mn) + sum;
+        m[g] = mn;
+      }
+    }
+  }
+  float inv[kSgGroups];
+#pragma unroll
+  for (int g = 0; g < kSgGroups; ++g) {
+    const auto mo = __builtin_amdgcn_permlane32_swap(__float_as_uint(m[g]), __float_as_uint(m[g]), false, false);
+    const auto lo = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[g]), __float_as_uint(l[g]), false, false);
+    const float m0 = __uint_as_float(mo[0]), m1 = __uint_as_float(mo[1]);
+    const float M = fmaxf(m0, m1);
+    const float lt = __uint_as_float(lo[0]) * __builtin_amdgcn_exp2f(m0 - M) +
+                     __uint_as_float(lo[1]) * __builtin_amdgcn_exp2f(m1 - M);
+    m[g] = M;
+    inv[g] = 1.f / lt;
+  }
+
+  // ---- pass 2: per key frame, probabilities through LDS and the pair products. Columns of
+  // positions past ns (zero queries, whose uniform rows are not samples) write zeros.
+  bool pos_ok[kSgGroups];
+#pragma unroll
+  for (int g = 0; g < kSgGroups; ++g) pos_ok[g] = chunk * kGramChunk + 2 * g + (col >> 4) < a.ns;
+  const int my_key = lane & 31, sl = lane >> 5;
+  const int n_kt = (a.ns + 31) / 32;
+  float acc[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) acc[p] = 0.f;
+  for (int f2 = 0; f2 < F; ++f2) {
+    const int frame0 = a.T + f2 * a.ns;
+    for (int t = 0; t < n_kt; ++t) {
+      jd_u32x4 kop[4];
+      load_k(a.ks + (bh * a.keys_pad + min(frame0 + 32 * t + col, a.keys_pad - 1)) * kD + 8 * hh, kop);
+#pragma unroll
+      for (int g = 0; g < kSgGroups; ++g) {
+        const sa_f32x16 tt = score_tile_k(kop, qf[g]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kr = 8 * (i >> 2) + 4 * hh + (i & 3);
+          const float pv = (pos_ok[g] && 32 * t + kr < a.ns)
+                               ? __builtin_amdgcn_exp2f(fmaf(tt[i], a.scale_log2, -m[g])) * inv[g] : 0.f;
+          L[(g * 32 + kr) * kSgStride + col] = pv;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int g = 0; g < kSgGroups; ++g) {
+        float x[4 * kRead];
+        const float* rp = L + (g * 32 + my_key) * kSgStride + 16 * sl;
+#pragma unroll
+        for (int u = 0; u < kRead; ++u) {
+          const float4 v4 = *reinterpret_cast<const float4*>(rp + 4 * u);
+          x[4 * u] = v4.x;
+          x[4 * u + 1] = v4.y;
+          x[4 * u + 2] = v4.z;
+          x[4 * u + 3] = v4.w;
+        }
+        int p = 0;
+#pragma unroll
+        for (int f1 = 0; f1 < F; ++f1)
+#pragma unroll
+          for (int f3 = f1; f3 < F; ++f3) {
+            acc[p] = fmaf(x[f1], x[f3], acc[p]);
+            ++p;
+          }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    // lanes' sums -> LDS [lane][pair] -> lane p adds pair p over the 64 lanes in order
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      L[lane * NP + p] = acc[p];
+      acc[p] = 0.f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float* out = a.G + ((bh * F + f2) * a.n_chunks + chunk) * NP;
+    for (int p = lane; p < NP; p += 64) {
+      float sum = 0.f;
+      for (int q = 0; q < 64; ++q) sum += L[q * NP + p];
+      out[p] = sum;
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 struct FinishArgs {
   const float* share;  // [BH][rows] or null
   const float* G1;     // [BH][F][n_chunks][NP] partials or null
@@ -289,12 +470,23 @@ struct FinishArgs {
   int32_t* use;       // [BH]
 };
 
+// Block sum over the 256 threads in a fixed order (per-wave shuffles, then the four waves).
+__device__ float block_sum(float x, float* red /* LDS [4] */) {
+  x = wave_sum_f(x);
+  const int t = threadIdx.x;
+  __syncthreads();
+  if ((t & 63) == 0) red[t >> 6] = x;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 // Mean cosine similarity of the patterns sharing a key frame, from one head's Gram partials:
 // col = mean over f2 of mean over (f1, f3) of G[f2][f1][f3] / sqrt(G[f2][f1][f1] G[f2][f3][f3]).
-__device__ float col_sim(const float* Gp, int F, int n_chunks, float* gs /* LDS [F * NP] */) {
-  const int lane = threadIdx.x;
+__device__ float col_sim(const float* Gp, int F, int n_chunks, float* gs /* LDS [F * NP] */, float* red) {
+  const int t = threadIdx.x;
   const int NP = F * (F + 1) / 2;
-  for (int e = lane; e < F * NP; e += 64) {
+  __syncthreads();
+  for (int e = t; e < F * NP; e += 256) {
     const int f2 = e / NP, p = e - f2 * NP;
     float s = 0.f;
     for (int c = 0; c < n_chunks; ++c) s += Gp[((int64_t)f2 * n_chunks + c) * NP + p];
@@ -310,31 +502,31 @@ __device__ float col_sim(const float* Gp, int F, int n_chunks, float* gs /* LDS 
     return g[i * F - i * (i - 1) / 2 + (j - i)];
   };
   float part = 0.f;
-  for (int u = lane; u < F * F * F; u += 64) {
+  for (int u = t; u < F * F * F; u += 256) {
     const int f2 = u / (F * F), f1 = (u / F) % F, f3 = u % F;
     const float* g = gs + f2 * NP;
     part += at(g, f1, f3) / sqrtf(at(g, f1, f1) * at(g, f3, f3));
   }
-  const float tot = wave_sum_f(part);
-  __syncthreads();
-  return tot / (float)(F * F * F);
+  return block_sum(part, red) / (float)(F * F * F);
 }
 
-__global__ __launch_bounds__(64) void finish_kernel(FinishArgs a) {
-  __shared__ float gs[16 * 136];
+// One 256-thread workgroup per head.
+__global__ __launch_bounds__(256) void finish_kernel(FinishArgs a) {
+  __shared__ float gs[12 * 78];
+  __shared__ float red[4];
   const int bh = blockIdx.x;
   if (bh >= a.BH) return;
-  const int lane = threadIdx.x;
+  const int t = threadIdx.x;
   float s = 0.f;
   if (a.share) {
-    for (int r = lane; r < a.rows; r += 64) s += a.share[(int64_t)bh * a.rows + r];
-    s = wave_sum_f(s) / (float)a.rows;
+    for (int r = t; r < a.rows; r += 256) s += a.share[(int64_t)bh * a.rows + r];
+    s = block_sum(s, red) / (float)a.rows;
   }
   const int NP = a.F * (a.F + 1) / 2;
   const int64_t gstride = (int64_t)a.F * a.n_chunks * NP;
-  const float c1 = a.G1 ? col_sim(a.G1 + bh * gstride, a.F, a.n_chunks, gs) : 0.f;
-  const float c2 = a.G2 ? col_sim(a.G2 + bh * gstride, a.F, a.n_chunks, gs) : 0.f;
-  if (lane == 0) {
+  const float c1 = a.G1 ? col_sim(a.G1 + bh * gstride, a.F, a.n_chunks, gs, red) : 0.f;
+  const float c2 = a.G2 ? col_sim(a.G2 + bh * gstride, a.F, a.n_chunks, gs, red) : 0.f;
+  if (t == 0) {
     a.share_mean[bh] = s;
     a.col1[bh] = c1;
     a.col2[bh] = c2;
@@ -413,6 +605,31 @@ extern "C" int sa_pattern_judge_finish(const float* share, const float* G1, cons
   a.share = share; a.G1 = G1; a.G2 = G2; a.BH = BH; a.rows = rows; a.F = F;
   a.n_chunks = (ns + kGramChunk - 1) / kGramChunk;
   a.sparse_thr = sparse_thr; a.sim_thr = sim_thr; a.share_mean = share_mean; a.col1 = col1; a.col2 = col2; a.use = use;
-  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)BH), dim3(64), 0, sa::as_stream(stream), a);
+  hipLaunchKernelGGL(finish_kernel, dim3((unsigned)BH), dim3(256), 0, sa::as_stream(stream), a);
+  return sa::check_launch(fn);
+}
+
+extern "C" int sa_pattern_sim_gram(const uint16_t* q_rows, const uint16_t* k_rows, int BH, int F, int ns, int T,
+                                   int rows_pad, int keys_pad, float sm_scale, float bias, float* G, void* stream) {
+  const char* fn = "sa_pattern_sim_gram";
+  SA_REQUIRE(q_rows && k_rows && G, "%s: null pointer", fn);
+  SA_REQUIRE(BH > 0 && F >= 1 && F <= 12 && ns > 0 && T >= 0, "%s: bad shape (1 <= F <= 12)", fn);
+  SA_REQUIRE(rows_pad % 32 == 0 && rows_pad >= F * ns && keys_pad % 32 == 0 && keys_pad >= T + F * ns,
+             "%s: rows_pad/keys_pad must be multiples of 32 covering F*ns / T+F*ns", fn);
+  SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f && std::isfinite(bias), "%s: bad sm_scale/bias", fn);
+  SimGramArgs a;
+  a.qs = q_rows; a.ks = k_rows; a.ns = ns; a.T = T; a.keys = T + F * ns; a.keys_pad = keys_pad; a.rows_pad = rows_pad;
+  a.scale_log2 = sm_scale * kLog2e; a.bias_log2 = bias * kLog2e; a.G = G;
+  a.n_chunks = (ns + kGramChunk - 1) / kGramChunk;
+  a.total = (int64_t)BH * a.n_chunks;
+  const dim3 grid((unsigned)((a.total + 3) / 4)), blk(256);
+  hipStream_t s = sa::as_stream(stream);
+  switch (F) {
+#define SA_SG_CASE(n) \
+  case n: hipLaunchKernelGGL(simgram_kernel<n>, grid, blk, 0, s, a); break;
+    SA_SG_CASE(1) SA_SG_CASE(2) SA_SG_CASE(3) SA_SG_CASE(4) SA_SG_CASE(5) SA_SG_CASE(6)
+    SA_SG_CASE(7) SA_SG_CASE(8) SA_SG_CASE(9) SA_SG_CASE(10) SA_SG_CASE(11) SA_SG_CASE(12)
+#undef SA_SG_CASE
+  }
   return sa::check_launch(fn);
 }

@@ -220,7 +220,7 @@ class ParternAttentionColVersion_V2:
 
 SPARSE_KEEP, SPARSE_THR, SIM_THR = 0.2, 0.9, 0.9
 _HEAD_CHUNK_BYTES = 4 << 30  # probability workspace per chunk of heads
-_GRAM_CHUNK = 20             # sample positions per Gram partial (kGramChunk in judge.hip)
+_GRAM_CHUNK = 8              # sample positions per Gram partial (kGramChunk in judge.hip)
 
 
 def _pad32(n: int) -> int:
@@ -267,15 +267,35 @@ def _sparsity_rows(q, k, g: PatternGeometry, idx_q):
     return share
 
 
-def _similarity_gram(q, k, g: PatternGeometry, index_k):
-    """Gram matrices [B*H, F, F(F+1)/2] of the sampled frame-pair attention patterns."""
-    B, H = q.shape[:2]
+def _similarity_inputs(q, k, g: PatternGeometry, index_k):
     T, F, ns = g.text_length, g.frames, g.sample_num
     nv = F * ns
     qs = _compact(q, index_k[T:], _pad32(nv))
     ks = _compact(k, index_k, _pad32(T + nv))
+    B, H = q.shape[:2]
     G = torch.empty(B * H, F, -(-ns // _GRAM_CHUNK), F * (F + 1) // 2, dtype=torch.float32, device=q.device)
-    for h0, h1 in _chunks(B * H, nv * _pad32(nv) * 4):
+    return qs, ks, G
+
+
+def _similarity_gram(q, k, g: PatternGeometry, index_k):
+    """Gram partials [B*H, F, ceil(ns/8), F(F+1)/2] of the sampled frame-pair attention patterns,
+    computed without writing the probabilities (one fused kernel)."""
+    T, F, ns = g.text_length, g.frames, g.sample_num
+    qs, ks, G = _similarity_inputs(q, k, g, index_k)
+    with torch.cuda.device(q.device):
+        _lib.check(_lib.load().sa_pattern_sim_gram(
+            qs.data_ptr(), ks.data_ptr(), qs.shape[0], F, ns, T, qs.shape[1], ks.shape[1], scale_factor,
+            composition(g), G.data_ptr(), _lib.stream_of(q)), "sa_pattern_sim_gram")
+    return G
+
+
+def _similarity_gram_via_probs(q, k, g: PatternGeometry, index_k):
+    """The same partials through the written probabilities (sa_sampled_probs + sa_pattern_gram)."""
+    T, F, ns = g.text_length, g.frames, g.sample_num
+    nv = F * ns
+    qs, ks, G = _similarity_inputs(q, k, g, index_k)
+    BH = qs.shape[0]
+    for h0, h1 in _chunks(BH, nv * _pad32(nv) * 4):
         P = torch.empty(h1 - h0, nv, _pad32(nv), dtype=torch.float32, device=q.device)
         _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, composition(g), T, T + nv, P)
         with torch.cuda.device(q.device):

@@ -154,6 +154,18 @@ def test_judges_match_oracle(dev):
     assert torch.equal(use.cpu(), want)
 
 
+def test_fused_gram_matches_written_probabilities(dev):
+    # sa_pattern_sim_gram (probabilities kept on chip) against sa_sampled_probs + sa_pattern_gram
+    case("fused similarity Gram")
+    q, k = _judge_inputs()
+    _, ik = pa.get_indexs(G)
+    qd, kd = q.to(dev), k.to(dev)
+    fused = pa._similarity_gram(qd, kd, G, ik)
+    written = pa._similarity_gram_via_probs(qd, kd, G, ik)
+    assert fused.shape == written.shape
+    assert torch.allclose(fused, written, rtol=2e-5, atol=1e-9), (fused - written).abs().max()
+
+
 def test_combined_attn_head_routing(dev):
     # Heads routed by unified_judge: pattern heads equal the pattern attention on those heads,
     # the others equal SparseGen_Plus's block-sparse attention on the remaining heads.
