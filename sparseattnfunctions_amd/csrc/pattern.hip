@@ -28,11 +28,14 @@ __device__ inline float bf(uint16_t x) { return __uint_as_float((uint32_t)x << 1
 // ---------------------------------------------------------------------------------------
 // maps_kernel: one wave per (bh, f1). Masses m[row][c] (bf16, column 0 = text, 1 + f2 =
 // frame f2) of the ns sampled rows of frame f1: img2text[f1] = sum_rows m[.][0] / ns,
-// img2img[f1][f2] = sum_rows m[.][1 + f2] / ns. Lane c sums column c over the rows in order.
+// img2img[f1][f2] = sum_rows m[.][1 + f2] / ns. Lane l adds rows l, l + 64, ... (16-byte
+// loads of columns 0-15, and column 16 when F = 16); the lanes' sums are then added by a
+// fixed butterfly.
 struct MapsArgs {
   const uint16_t* m;
   int64_t m_sb, m_sh, m_sl;
   int H, F, ns;
+  int vec_ok;       // rows 16-byte aligned
   float* img2text;  // [BH][F]
   float* img2img;   // [BH][F][F]
   int64_t total;    // BH * F
@@ -45,15 +48,40 @@ __global__ __launch_bounds__(64) void maps_kernel(MapsArgs a) {
   const int64_t bh = w / a.F;
   const int f1 = (int)(w - bh * a.F);
   const int64_t b = bh / a.H, h = bh - b * a.H;
-  if (lane > a.F) return;
-  const uint16_t* p = a.m + b * a.m_sb + h * a.m_sh + (int64_t)f1 * a.ns * a.m_sl + lane;
-  float s = 0.f;
-  for (int r = 0; r < a.ns; ++r) s += bf(p[(int64_t)r * a.m_sl]);
-  s /= (float)a.ns;
-  if (lane == 0)
-    a.img2text[bh * a.F + f1] = s;
-  else
-    a.img2img[(bh * a.F + f1) * a.F + (lane - 1)] = s;
+  const int ncol = a.F + 1;  // <= 17
+  const uint16_t* base = a.m + b * a.m_sb + h * a.m_sh + (int64_t)f1 * a.ns * a.m_sl;
+  float s[17];
+#pragma unroll
+  for (int c = 0; c < 17; ++c) s[c] = 0.f;
+  for (int r = lane; r < a.ns; r += 64) {
+    const uint16_t* row = base + (int64_t)r * a.m_sl;
+    if (a.vec_ok) {
+      const uint4 w0 = *reinterpret_cast<const uint4*>(row);
+      const uint4 w1 = *reinterpret_cast<const uint4*>(row + 8);
+      const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        s[2 * q] += __uint_as_float(u[q] << 16);
+        s[2 * q + 1] += __uint_as_float(u[q] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) s[c] += c < ncol ? bf(row[c]) : 0.f;
+    }
+    if (ncol > 16) s[16] += bf(row[16]);
+  }
+#pragma unroll
+  for (int c = 0; c < 17; ++c) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s[c] += __shfl_xor(s[c], o);
+  }
+  if (lane == 0) {
+    const float inv = 1.f / (float)a.ns;
+    a.img2text[bh * a.F + f1] = s[0] * inv;
+#pragma unroll
+    for (int c = 1; c < 17; ++c)
+      if (c < ncol) a.img2img[(bh * a.F + f1) * a.F + (c - 1)] = s[c] * inv;
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -350,6 +378,9 @@ extern "C" int sa_pattern_maps(const uint16_t* map_mass, const int64_t map_strid
   MapsArgs ma;
   ma.m = map_mass; ma.m_sb = map_strides[0]; ma.m_sh = map_strides[1]; ma.m_sl = map_strides[2];
   ma.H = H; ma.F = F; ma.ns = ns; ma.img2text = img2text; ma.img2img = img2img; ma.total = (int64_t)B * H * F;
+  // 16-byte loads of columns 0-15: rows aligned and at least 16 elements apart
+  ma.vec_ok = (reinterpret_cast<uintptr_t>(map_mass) % 16 == 0 && ma.m_sl >= 16 && ma.m_sl % 8 == 0 &&
+               ma.m_sb % 8 == 0 && ma.m_sh % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL(maps_kernel, dim3((unsigned)ma.total), dim3(64), 0, sa::as_stream(stream), ma);
   return sa::check_launch(fn);
 }
