@@ -45,6 +45,19 @@ def test_pooled_attention_matches_oracle(dev, bs, causal, Hk):
                            torch.zeros_like(po.cpu()[..., torch.ones(nd, nd, dtype=torch.bool).triu(1)]))
 
 
+@pytest.mark.parametrize("L", [40, 70, 130])
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pooled_attention_short_sequences(dev, L, bs, causal):
+    # fewer tokens than one or two blocks: partial last key and query blocks in every mode
+    case(f"attn_with_pooling L={L} bs={bs} causal={causal}")
+    q, k, v = _qkv(L + bs + causal, 1, 2, 1, L)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, 0.125, bs)
+    want_o, want_po = pooled_attention(q, k, v, causal, 0.125, bs)
+    assert (o.cpu().double() - want_o).abs().max().item() <= 2e-2
+    assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7)
+
+
 def test_pooled_attention_large_scores(dev):
     # scores of several hundred: the kernel's safe pass; Po must not depend on it
     case("attn_with_pooling large scores")
