@@ -246,14 +246,14 @@ int sa_energy_kv_list(const float* scores, int BH, int nqb, int nkb, int mode, f
 /*
  * Per-head token gather out[b,h,j] = x[b,h, idx[(b*H + h)*L_out + j]] (zero row outside
  * [0, L_in)). Replaces the per-head query-frame gather gather_q_chunk of the pattern
- * attention (partern_attention.py:379-385, torch.gather with per-head frame indices).
+ * attention (partern_attention.py:378-384, torch.gather with per-head frame indices).
  */
 int sa_gather_tokens_heads(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L_in,
                            int D, const int32_t* idx, int L_out, uint16_t* out,
                            const int64_t out_strides[3], void* stream);
 
 /*
- * Frame maps of the pattern attention (get_weight_for_patch, partern_attention.py:336-356)
+ * Frame maps of the pattern attention (get_weight_for_patch, partern_attention.py:321-358)
  * from the sampled attention's segment masses map_mass [B,H,F*ns,>=F+1] (bf16; row = sampled
  * video query, column 0 = mass on the text keys, 1 + f = mass on frame f's samples):
  *   img2text[bh][f] = sum of column 0 over frame f's ns rows / ns      (fp32 [B*H][F])
@@ -263,7 +263,7 @@ int sa_pattern_maps(const uint16_t* map_mass, const int64_t map_strides[3], int 
                     int ns, float* img2text, float* img2img, void* stream);
 
 /*
- * Per-head plan of the pattern attention (partern_attention.py:215-276, 393-430) from the
+ * Per-head plan of the pattern attention (partern_attention.py:262-315, 412-435) from the
  * first-frame masses ff_mass [B,H,S,>=F+1] (bf16; column 0 text, 1 + i frame i) and img2img:
  *   stats   fp32 [B*H][F+1][3]: sum, min, max of each mass column over the S rows;
  *   fac     fp32 [B*H][F+1][4]: the modify factor x -> constrained_mod_factor(x / mean(x))
@@ -281,7 +281,7 @@ int sa_pattern_plan(const uint16_t* ff_mass, const int64_t ff_strides[3], const 
                     int32_t* frame_case, float* inv_map0, int32_t* q_idx, void* stream);
 
 /*
- * Final mix of the pattern attention (partern_attention.py:455-460): for video row f1*S + r,
+ * Final mix of the pattern attention (partern_attention.py:447-452): for video row f1*S + r,
  *   out[T + f1*S + r] = sum_i img2img[f1][i] * s_i(r) * o_frames[i*S + r]
  *                       + img2text[f1] * mft(r) * o_text[f1*S + r]
  * with s_i(r) the frame-i modify factor (frame_case 0) or ff_mass[r][1+i] * inv_map0[i]
@@ -297,7 +297,7 @@ int sa_pattern_combine(const uint16_t* o_frames, const int64_t of_strides[3], co
 
 /*
  * Softmax probabilities of sampled queries over sampled keys, for the head-routing judges
- * (judge_sparsity / judge_similarity, partern_attention.py:470-514):
+ * (judge_sparsity / judge_similarity, partern_attention.py:468-514):
  *   P[bh][r][c - c_lo] = softmax_c(q_rows[bh][r] . k_rows[bh][c] * sm_scale + (c < n_bias ? bias : 0))
  * over all `keys` keys, written for c in [c_lo, c_hi) and r < rows.
  *   q_rows [BH][rows_pad][64], k_rows [BH][keys_pad][64] bf16 contiguous (pads: multiples of
@@ -309,14 +309,14 @@ int sa_sampled_probs(const uint16_t* q_rows, const uint16_t* k_rows, int BH, int
 
 /*
  * Per row of P (n >= 0 entries, n <= 16384): the sum of its K largest entries, 1 <= K <= n
- * (judge_sparsity's sorted-prefix share, partern_attention.py:476-478). share fp32 [BH][rows].
+ * (judge_sparsity's sorted-prefix share, partern_attention.py:474-475). share fp32 [BH][rows].
  */
 int sa_topk_share(const float* P, int64_t p_bh_stride, int64_t p_row_stride, int BH, int rows,
                   int n, int K, float* share, void* stream);
 
 /*
  * Gram matrices of the sampled frame-pair attention patterns (judge_similarity,
- * partern_attention.py:497-510): with P the [F*ns x F*ns] video part of the sampled
+ * partern_attention.py:502-512): with P the [F*ns x F*ns] video part of the sampled
  * probabilities, G[bh][f2][chunk][pair(f1,f3)] = sum over s1 in the chunk (8 positions)
  * and all s2 of P[f1*ns + s1][f2*ns + s2] * P[f3*ns + s1][f2*ns + s2], f1 <= f3 (pairs in
  * row-major upper-triangle order). F <= 12, ns <= 512.
@@ -326,7 +326,7 @@ int sa_pattern_gram(const float* P, int64_t p_bh_stride, int64_t p_row_stride, i
 
 /*
  * The Gram partials of sa_pattern_gram computed straight from the sampled rows, without
- * writing the probabilities (judge_similarity, partern_attention.py:480-514): q_rows
+ * writing the probabilities (judge_similarity, partern_attention.py:477-514): q_rows
  * [BH][rows_pad][64] holds the F*ns sampled video queries (row f*ns + s), k_rows
  * [BH][keys_pad][64] the T text keys then the F*ns sampled keys (bf16 contiguous, pads:
  * multiples of 32); the probabilities are softmax over all T + F*ns keys of

@@ -2,9 +2,9 @@
 oracle/__init__.py).
 
 Restates, in float64 with the random sample positions passed in, the reference's
-  * ParternAttentionColVersion_V2.get_weight_for_patch / forward (partern_attention.py:318-463),
-  * constrained_mod_factor (:215-276),
-  * judge_sparsity / judge_similarity / unified_judge (:470-521),
+  * ParternAttentionColVersion_V2.get_weight_for_patch / forward (partern_attention.py:318-456),
+  * constrained_mod_factor (:262-315),
+  * judge_sparsity / judge_similarity / unified_judge (:468-521),
 for a geometry of `frames` frames of height x width tokens after `text` text tokens, with
 `ns` sampled positions per frame.
 
@@ -40,7 +40,7 @@ def index_k(p, frames, S, text):
 
 
 def weight_for_patch(q, k, p, frames, S, text):
-    """(img2img_map [B,H,F,F], img2text_map [B,H,F,1]) of get_weight_for_patch (:336-356)."""
+    """(img2img_map [B,H,F,F], img2text_map [B,H,F,1]) of get_weight_for_patch (:321-358)."""
     ns = p.numel()
     idx = index_k(p, frames, S, text)
     qs, ks = q.double()[:, :, idx], k.double()[:, :, idx]
@@ -55,7 +55,7 @@ def weight_for_patch(q, k, p, frames, S, text):
 
 
 def constrained_mod_factor(m, lo, hi):
-    """:215-276 (m [B,H,L,1]); the adjustment decision is taken over every head at once."""
+    """:262-315 (m [B,H,L,1]); the adjustment decision is taken over every head at once."""
     osum = m.sum(dim=(-2, -1), keepdim=True)
     cmin = m.min(dim=-2, keepdim=True)[0]
     cmax = m.max(dim=-2, keepdim=True)[0]
@@ -73,7 +73,7 @@ def constrained_mod_factor(m, lo, hi):
 
 
 def pattern_v2(q, k, v, p, frames, S, text, return_parts=False):
-    """ParternAttentionColVersion_V2.forward (:376-463) in float64; returns [B,H,L,D]."""
+    """ParternAttentionColVersion_V2.forward (:377-453) in float64; returns [B,H,L,D]."""
     q, k, v = q.double(), k.double(), v.double()
     B, H, L, D = q.shape
     T, F = text, frames
@@ -109,7 +109,7 @@ def pattern_v2(q, k, v, p, frames, S, text, return_parts=False):
 
 
 def judge_sparsity(q, k, idx_q, S, text, keep=0.2, thr=0.9):
-    """(:470-479): sampled first-frame queries vs every third key; a head is sparse when the
+    """(:468-476): sampled first-frame queries vs every third key; a head is sparse when the
     mean (over queries) share of its top `keep` keys exceeds `thr`. Returns (bool [B,H], share)."""
     qs = q.double()[:, :, idx_q + text]
     ks = k.double()[:, :, ::3]
@@ -120,7 +120,7 @@ def judge_sparsity(q, k, idx_q, S, text, keep=0.2, thr=0.9):
 
 
 def judge_similarity(q, k, p, frames, S, text, thr=0.9):
-    """(:480-514): cosine similarity of the sampled frame-pair attention patterns; a head is
+    """(:477-514): cosine similarity of the sampled frame-pair attention patterns; a head is
     self-similar when the mean similarity of patterns sharing a key frame exceeds `thr`.
     Returns (bool [B,H], col_sim)."""
     ns = p.numel()

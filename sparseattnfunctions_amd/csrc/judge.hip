@@ -1,4 +1,4 @@
-// Head routing of the 1.5-5B pattern attention (unified_judge, partern_attention.py:464-521)
+// Head routing of the 1.5-5B pattern attention (unified_judge, partern_attention.py:463-521)
 // for gfx950.
 //
 //   probs_kernel       one wave per (head, 32 sampled query rows): S^T = K Q^T with
@@ -6,10 +6,10 @@
 //                      on the first keys), row max and sum in a first pass, then the
 //                      probabilities of a key range written row-major (through LDS, 128-byte
 //                      rows) in a second pass;
-//   share_kernel       judge_sparsity (:470-479): per query row, the probability mass of its
+//   share_kernel       judge_sparsity (:468-476): per query row, the probability mass of its
 //                      K largest entries (K-th largest found by a 32-step search on the fp32
 //                      bit patterns), one workgroup per row;
-//   gram_kernel        judge_similarity (:480-514): for key frame f2, the Gram matrix
+//   gram_kernel        judge_similarity (:477-514): for key frame f2, the Gram matrix
 //                      G[f1][f3] = sum_{s1,s2} P[f1 s1][f2 s2] * P[f3 s1][f2 s2] of the
 //                      frame-pair patterns (their inner products and norms), as partial sums
 //                      over chunks of s1;

@@ -1,21 +1,21 @@
 // Frame-pattern attention of the 1.5-5B geometry (ParternAttentionColVersion_V2,
-// partern_attention.py:318-463) for gfx950: the small per-head planning kernels and the final
+// partern_attention.py:318-456) for gfx950: the small per-head planning kernels and the final
 // combine. The attention-shaped parts (text rows, first-frame masses, sampled frame maps,
 // video-to-text attention, per-frame attention) run in the block-sparse attention kernel; the
 // per-segment probability masses come out of it by attending to a 0/1 segment-indicator V.
 //
 //   plan: maps_kernel      img2text_map[f] and img2img_map[f1][f2] from the sampled
-//                          attention's segment masses (get_weight_for_patch, :336-356);
+//                          attention's segment masses (get_weight_for_patch, :321-358);
 //         fstats_kernel    per head and factor: sum, min and max of the first-frame masses
 //                          (text mass for modify_factor_text, frame-i mass for frame i);
-//         select_kernel    constrained_mod_factor (:215-276) as a per-element affine map +
+//         select_kernel    constrained_mod_factor (:262-315) as a per-element affine map +
 //                          clamp, with the cross-head "any head out of range" decision, and
 //                          the case of every key frame (first-frame masses where
-//                          img2img_map[0][i] >= 0.1, :414-423);
+//                          img2img_map[0][i] >= 0.1, :435);
 //         qidx_kernel      the per-head query-row gather table (query frame = argmax over the
 //                          img2img_map column, or the first frame);
 //   combine_kernel         out = sum_i img2img[f1][i] * scale_i(r) * O_i[r]
-//                                + img2text[f1] * mft(r) * O_text[f1*S + r]   (:455-460).
+//                                + img2text[f1] * mft(r) * O_text[f1*S + r]   (:447-452).
 #include "sa_common.h"
 
 namespace {

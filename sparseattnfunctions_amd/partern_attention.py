@@ -1,11 +1,11 @@
 """Frame-pattern attention and head routing of special_attentions/partern_attention.py, on MI355X.
 
-  * `ParternAttentionColVersion_V2` (:318-463): text rows attend everything; every video
+  * `ParternAttentionColVersion_V2` (:318-456): text rows attend everything; every video
     frame's output is a mix, weighted by a sampled frame-to-frame map, of per-key-frame
     attention outputs computed once from a representative query frame, plus a video-to-text
     term scaled by first-frame text masses.
-  * `constrained_mod_factor` (:215-276), `get_indexs` (:17-31).
-  * `judge_sparsity`, `judge_similarity`, `unified_judge` (:464-521): whether a head suits
+  * `constrained_mod_factor` (:262-315), `get_indexs` (:17-31).
+  * `judge_sparsity`, `judge_similarity`, `unified_judge` (:463-521): whether a head suits
     the pattern approximation.
 
 The geometry defaults to the reference's 1.5-5B constants (11 frames of 48 x 85 tokens after
@@ -126,7 +126,7 @@ class ParternAttentionColVersion_V2:
         return _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
 
     def sampled_masses(self, q, k, index_k):
-        """Segment masses of the sampled attention (get_weight_for_patch, :336-356): for every
+        """Segment masses of the sampled attention (get_weight_for_patch, :321-358): for every
         sampled video row, the softmax mass (with log(ns/S) added to text keys) on the text
         keys (column 0) and on each frame's samples (column 1 + f). bf16 [B, H, F*ns, 64]."""
         g = self.geometry
@@ -149,7 +149,7 @@ class ParternAttentionColVersion_V2:
         if index_k is None:
             _, index_k = get_indexs(g)
         out = torch.empty_like(q)
-        # Text rows over every key (the reference's SDPA, :455).
+        # Text rows over every key (the reference's SDPA, :442).
         block_sparse_attention(q[:, :, :T], k, v, _dense(B, H, T, L, dev), scale_factor, out=out[:, :, :T])
         # First-frame rows over every key: per-segment masses (text, frame i).
         ff_mass = block_sparse_attention(q[:, :, T:T + S], k, _bcast(_frame_indicator(g, dev), B, H),
@@ -216,7 +216,7 @@ class ParternAttentionColVersion_V2:
         return self.forward(*args, **kwds)
 
 
-# ---- head routing (partern_attention.py:464-521) ---------------------------------------------
+# ---- head routing (partern_attention.py:463-521) ---------------------------------------------
 
 SPARSE_KEEP, SPARSE_THR, SIM_THR = 0.2, 0.9, 0.9
 _HEAD_CHUNK_BYTES = 4 << 30  # probability workspace per chunk of heads
@@ -318,7 +318,7 @@ def _finish(share, G1, G2, BH, rows, F, ns, device):
 
 def judge_sparsity(q, k, geometry: PatternGeometry = DEFAULT, idx_q=None, return_share=False):
     """True for heads whose sampled first-frame queries put > 90 % of their mass on the top
-    20 % of (every third) key (:470-479). idx_q: first-frame positions (default: a randperm)."""
+    20 % of (every third) key (:468-476). idx_q: first-frame positions (default: a randperm)."""
     g = geometry
     q, k = _prep_qkv(q), _prep_qkv(k)
     _lib.require_gpu(q, k)
@@ -333,7 +333,7 @@ def judge_sparsity(q, k, geometry: PatternGeometry = DEFAULT, idx_q=None, return
 
 def judge_similarity(q, k, geometry: PatternGeometry = DEFAULT, index_k=None, return_sim=False):
     """True for heads whose sampled frame-pair attention patterns sharing a key frame have a
-    mean cosine similarity > 0.9 (:480-514)."""
+    mean cosine similarity > 0.9 (:477-514)."""
     g = geometry
     q, k = _prep_qkv(q), _prep_qkv(k)
     _lib.require_gpu(q, k)
