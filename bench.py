@@ -174,9 +174,22 @@ def other_configs(q, k, v, dev):
     ms_judge = time_fn(lambda: pa.unified_judge(q6, k6, g, draws=draws), iters=3, warmup=1)
     T, S, F = g.text_length, g.S, g.frames
     f_pat = 2 * 48 * 4 * 64 * (T * g.L + S * g.L + F * S * T + F * g.sample_num * (T + F * g.sample_num) + F * S * S)
+    # The routed CombinedAttn body (combined_attn.py:42-101) on the same geometry. The frames of
+    # the first 24 heads of each batch item are made copies of the first frame (self-similar and
+    # not sparse: routed to the pattern attention); the other heads stay random (routed to
+    # SparseGen_Plus, whose energy rule keeps most blocks of random inputs).
+    from sparseattnfunctions_amd.combined_attn import CombinedAttn
+
+    for x in (q6, k6):
+        x[:, :24, T + S:] = x[:, :24, T:T + S].repeat(1, 1, F - 1, 1)
+    routed = CombinedAttn(warmup_epoch=0, head_routing=True)
+    routed(q6, k6, v6)
+    n_pattern_heads = int(routed.last_routing.sum().item())
+    ms_routed = time_fn(lambda: routed(q6, k6, v6), iters=3, warmup=1)
     out["pattern_1_5b"] = {"pattern_ms": round(ms_pat, 3), "pattern_tflops": _tflops(f_pat, ms_pat),
-                           "unified_judge_ms": round(ms_judge, 3), "heads": 96, "L": g.L}
-    del q6, k6, v6
+                           "unified_judge_ms": round(ms_judge, 3), "heads": 96, "L": g.L,
+                           "routed_call_ms": round(ms_routed, 3), "routed_pattern_heads": n_pattern_heads}
+    del q6, k6, v6, routed
 
     # Sliding-tile attention (default config) on the C2 inputs: the fused call (query and
     # output permutations inside the kernel) against permute-copies + attention + copy back.
