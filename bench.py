@@ -269,8 +269,8 @@ def main():
                     help="also run one plain 1 GiB device copy (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only (the hot path is single-GPU; see "
-              "DESIGN.md for how it would shard); use --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only. The path is independent per (batch, head) "
+              "and would shard by heads with no exchange; use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention
