@@ -541,6 +541,8 @@ extern "C" int sa_sampled_probs(const uint16_t* q_rows, const uint16_t* k_rows, 
                                 float* P, int64_t p_bh_stride, int64_t p_row_stride, void* stream) {
   const char* fn = "sa_sampled_probs";
   SA_REQUIRE(q_rows && k_rows && P, "%s: null pointer", fn);
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(q_rows) % 16 == 0 && reinterpret_cast<uintptr_t>(k_rows) % 16 == 0,
+             "%s: q_rows/k_rows must be 16-byte aligned", fn);
   SA_REQUIRE(BH > 0 && rows > 0 && keys > 0, "%s: bad shape", fn);
   SA_REQUIRE(rows_pad % 32 == 0 && rows_pad >= rows && keys_pad % 32 == 0 && keys_pad >= keys,
              "%s: rows_pad/keys_pad must be multiples of 32 covering rows/keys", fn);
@@ -613,6 +615,8 @@ extern "C" int sa_pattern_sim_gram(const uint16_t* q_rows, const uint16_t* k_row
                                    int rows_pad, int keys_pad, float sm_scale, float bias, float* G, void* stream) {
   const char* fn = "sa_pattern_sim_gram";
   SA_REQUIRE(q_rows && k_rows && G, "%s: null pointer", fn);
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(q_rows) % 16 == 0 && reinterpret_cast<uintptr_t>(k_rows) % 16 == 0,
+             "%s: q_rows/k_rows must be 16-byte aligned", fn);
   SA_REQUIRE(BH > 0 && F >= 1 && F <= 12 && ns > 0 && T >= 0, "%s: bad shape (1 <= F <= 12)", fn);
   SA_REQUIRE(rows_pad % 32 == 0 && rows_pad >= F * ns && keys_pad % 32 == 0 && keys_pad >= T + F * ns,
              "%s: rows_pad/keys_pad must be multiples of 32 covering F*ns / T+F*ns", fn);
