@@ -6,7 +6,7 @@
 //
 //   plan: maps_kernel      img2text_map[f] and img2img_map[f1][f2] from the sampled
 //                          attention's segment masses (get_weight_for_patch, :321-358);
-//         fstats_kernel    per head and factor: sum, min and max of the first-frame masses
+//         fstats_kernel    per head: sum, min and max of each column of the first-frame masses
 //                          (text mass for modify_factor_text, frame-i mass for frame i);
 //         select_kernel    constrained_mod_factor (:262-315) as a per-element affine map +
 //                          clamp, with the cross-head "any head out of range" decision, and
@@ -85,49 +85,80 @@ __global__ __launch_bounds__(64) void maps_kernel(MapsArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// fstats_kernel: one workgroup of 256 per (bh, factor j); x[r] = mass column j of first-frame
-// row r (j = 0 text, 1 + i frame i). Writes sum, min, max of x over r < S.
+// fstats_kernel: one workgroup of 256 per bh; x_j[r] = mass column j of first-frame row r
+// (j = 0 text, 1 + i frame i). Writes sum, min, max of every x_j over r < S. Thread t takes
+// rows t, t + 256, ... (16-byte loads of columns 0-15, column 16 when there are 17); the
+// threads' partials are combined by a fixed butterfly per wave, then the 4 waves in order.
 struct StatsArgs {
   const uint16_t* m;
   int64_t m_sb, m_sh, m_sl;
   int H, S, n_fac;
-  float* stats;  // [BH][n_fac][3]
-  int64_t total;
+  int vec_ok;     // rows 16-byte aligned and at least 16 elements apart
+  float* stats;   // [BH][n_fac][3]
+  int64_t total;  // BH
 };
 
 __global__ __launch_bounds__(256) void fstats_kernel(StatsArgs a) {
-  __shared__ float red[3][256];
-  const int64_t w = blockIdx.x;
-  if (w >= a.total) return;
-  const int t = threadIdx.x;
-  const int64_t bh = w / a.n_fac;
-  const int j = (int)(w - bh * a.n_fac);
+  __shared__ float red[4][17][3];
+  const int64_t bh = blockIdx.x;
+  if (bh >= a.total) return;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t b = bh / a.H, h = bh - b * a.H;
-  const uint16_t* p = a.m + b * a.m_sb + h * a.m_sh + j;
-  float s = 0.f, mn = INFINITY, mx = -INFINITY;
+  const uint16_t* base = a.m + b * a.m_sb + h * a.m_sh;
+  float su[17], mn[17], mx[17];
+#pragma unroll
+  for (int c = 0; c < 17; ++c) {
+    su[c] = 0.f;
+    mn[c] = INFINITY;
+    mx[c] = -INFINITY;
+  }
   for (int r = t; r < a.S; r += 256) {
-    const float x = bf(p[(int64_t)r * a.m_sl]);
-    s += x;
-    mn = fminf(mn, x);
-    mx = fmaxf(mx, x);
-  }
-  red[0][t] = s;
-  red[1][t] = mn;
-  red[2][t] = mx;
-  __syncthreads();
-  for (int k = 128; k > 0; k >>= 1) {
-    if (t < k) {
-      red[0][t] += red[0][t + k];
-      red[1][t] = fminf(red[1][t], red[1][t + k]);
-      red[2][t] = fmaxf(red[2][t], red[2][t + k]);
+    const uint16_t* row = base + (int64_t)r * a.m_sl;
+    float x[17];
+    if (a.vec_ok) {
+      const uint4 w0 = *reinterpret_cast<const uint4*>(row);
+      const uint4 w1 = *reinterpret_cast<const uint4*>(row + 8);
+      const uint32_t u[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        x[2 * q] = __uint_as_float(u[q] << 16);
+        x[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; ++c) x[c] = c < a.n_fac ? bf(row[c]) : 0.f;
     }
-    __syncthreads();
+    x[16] = a.n_fac > 16 ? bf(row[16]) : 0.f;
+#pragma unroll
+    for (int c = 0; c < 17; ++c) {
+      su[c] += x[c];
+      mn[c] = fminf(mn[c], x[c]);
+      mx[c] = fmaxf(mx[c], x[c]);
+    }
   }
-  if (t == 0) {
-    float* o = a.stats + (bh * a.n_fac + j) * 3;
-    o[0] = red[0][0];
-    o[1] = red[1][0];
-    o[2] = red[2][0];
+#pragma unroll
+  for (int c = 0; c < 17; ++c) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      su[c] += __shfl_xor(su[c], o);
+      mn[c] = fminf(mn[c], __shfl_xor(mn[c], o));
+      mx[c] = fmaxf(mx[c], __shfl_xor(mx[c], o));
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int c = 0; c < 17; ++c) {
+      red[wave][c][0] = su[c];
+      red[wave][c][1] = mn[c];
+      red[wave][c][2] = mx[c];
+    }
+  }
+  __syncthreads();
+  if (t < a.n_fac) {
+    float* o = a.stats + (bh * a.n_fac + t) * 3;
+    o[0] = ((red[0][t][0] + red[1][t][0]) + red[2][t][0]) + red[3][t][0];
+    o[1] = fminf(fminf(red[0][t][1], red[1][t][1]), fminf(red[2][t][1], red[3][t][1]));
+    o[2] = fmaxf(fmaxf(red[0][t][2], red[1][t][2]), fmaxf(red[2][t][2], red[3][t][2]));
   }
 }
 
@@ -398,7 +429,9 @@ extern "C" int sa_pattern_plan(const uint16_t* ff_mass, const int64_t ff_strides
   const int BH = B * H;
   StatsArgs sa_;
   sa_.m = ff_mass; sa_.m_sb = ff_strides[0]; sa_.m_sh = ff_strides[1]; sa_.m_sl = ff_strides[2];
-  sa_.H = H; sa_.S = S; sa_.n_fac = 1 + F; sa_.stats = stats; sa_.total = (int64_t)BH * (1 + F);
+  sa_.H = H; sa_.S = S; sa_.n_fac = 1 + F; sa_.stats = stats; sa_.total = BH;
+  sa_.vec_ok = (reinterpret_cast<uintptr_t>(ff_mass) % 16 == 0 && sa_.m_sl >= 16 && sa_.m_sl % 8 == 0 &&
+                sa_.m_sb % 8 == 0 && sa_.m_sh % 8 == 0) ? 1 : 0;
   hipLaunchKernelGGL(fstats_kernel, dim3((unsigned)sa_.total), dim3(256), 0, s, sa_);
   SelectArgs se;
   se.stats = stats; se.img2img = img2img; se.BH = BH; se.F = F; se.S = S; se.T = T; se.n_fac = 1 + F;
