@@ -7,8 +7,9 @@
 //                      probabilities of a key range written row-major (through LDS, 128-byte
 //                      rows) in a second pass;
 //   share_kernel       judge_sparsity (:468-476): per query row, the probability mass of its
-//                      K largest entries (K-th largest found by a 32-step search on the fp32
-//                      bit patterns), one workgroup per row;
+//                      K largest entries (K-th largest found by a bit search on the fp32
+//                      bit patterns, its last bits over the compacted bucket), one workgroup
+//                      per row;
 //   gram_kernel        judge_similarity (:477-514): for key frame f2, the Gram matrix
 //                      G[f1][f3] = sum_{s1,s2} P[f1 s1][f2 s2] * P[f3 s1][f2 s2] of the
 //                      frame-pair patterns (their inner products and norms), as partial sums
@@ -157,6 +158,7 @@ struct ShareArgs {
   const float* P;
   int64_t p_bh, p_row;
   int rows, n, K;
+  int vec_ok;  // P, p_bh and p_row multiples of 16 bytes
   float* share;  // [BH][rows]
   int64_t total;
 };
@@ -172,36 +174,121 @@ __device__ inline float wave_sum_f(float x) {
   return x;
 }
 
-// Thread t holds entries t, t + 256, ... (at most 64 of them) in registers.
+// Thread t holds entries t, t + 256, ... (at most 64 of them) in registers. The K-th largest
+// bit pattern (p >= 0: bit patterns order as the values) is the largest thr with
+// #{v >= thr} >= K, found bit by bit from the top. The first kShareHi bits are searched over
+// every entry. The entries that share those bits (the bucket) are then compacted into LDS in
+// thread order, and one wave finishes the search over them; entries above the bucket always
+// count. A bucket larger than kShareCap entries continues the search over every entry.
+constexpr int kShareHi = 12;
+constexpr int kShareCap = 2048;
+
+__device__ inline uint32_t wave_incl_scan_u(uint32_t x, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
 __global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
   constexpr int kPer = 64;
   __shared__ uint32_t part_u[2][4];
   __shared__ float part_f[4];
+  __shared__ uint32_t buck[kShareCap];
+  __shared__ uint32_t wtot[2][4];
+  __shared__ uint32_t thr_out;
   const int64_t w = blockIdx.x;
   if (w >= a.total) return;
-  const int t = threadIdx.x, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t bh = w / a.rows;
   const int r = (int)(w - bh * a.rows);
   const float* src = a.P + bh * a.p_bh + (int64_t)r * a.p_row;
-  uint32_t v[kPer];  // p >= 0: the bit patterns order as the values; 0 past n
+  uint32_t v[kPer];  // 0 past n; the order of the entries does not matter below
+  if (a.vec_ok) {    // 16-byte loads: entries 4t + 1024q .. +3
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = t + 256 * j;
-    v[j] = i < a.n ? __float_as_uint(src[i]) : 0u;
+    for (int q = 0; q < kPer / 4; ++q) {
+      const int i = 4 * t + 1024 * q;
+      if (i + 4 <= a.n) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src + i);
+        v[4 * q] = u.x;
+        v[4 * q + 1] = u.y;
+        v[4 * q + 2] = u.z;
+        v[4 * q + 3] = u.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * q + e] = i + e < a.n ? __float_as_uint(src[i + e]) : 0u;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = t + 256 * j;
+      v[j] = i < a.n ? __float_as_uint(src[i]) : 0u;
+    }
   }
-  // K-th largest bit pattern: largest thr with #{v >= thr} >= K (double-buffered partials,
-  // one barrier per step).
-  uint32_t thr = 0;
-  for (int bit = 31; bit >= 0; --bit) {
+  // Counting step over every entry (double-buffered partials, one barrier per step).
+  auto step = [&](uint32_t thr, int bit) {
     const uint32_t cand = thr | (1u << bit);
     uint32_t c = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) c += v[j] >= cand;
     c = wave_sum_u(c);
-    if ((t & 63) == 0) part_u[bit & 1][wave] = c;
+    if (lane == 0) part_u[bit & 1][wave] = c;
     __syncthreads();
     const uint32_t tot = part_u[bit & 1][0] + part_u[bit & 1][1] + part_u[bit & 1][2] + part_u[bit & 1][3];
-    if (tot >= (uint32_t)a.K) thr = cand;
+    return tot >= (uint32_t)a.K ? cand : thr;
+  };
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 32 - kShareHi; --bit) thr = step(thr, bit);
+  // Bucket: entries whose top kShareHi bits equal thr's; above: entries with larger top bits.
+  const uint32_t hi = thr >> (32 - kShareHi);
+  uint32_t nb = 0, above = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint32_t tb = v[j] >> (32 - kShareHi);
+    nb += tb == hi;
+    above += tb > hi;
+  }
+  const uint32_t nb_incl = wave_incl_scan_u(nb, lane);
+  const uint32_t above_w = wave_sum_u(above);
+  if (lane == 63) wtot[0][wave] = nb_incl;
+  if (lane == 0) wtot[1][wave] = above_w;
+  __syncthreads();
+  uint32_t nb_off = nb_incl - nb;
+  for (int q = 0; q < wave; ++q) nb_off += wtot[0][q];
+  const uint32_t nb_tot = wtot[0][0] + wtot[0][1] + wtot[0][2] + wtot[0][3];
+  const uint32_t above_tot = wtot[1][0] + wtot[1][1] + wtot[1][2] + wtot[1][3];
+  if (nb_tot <= (uint32_t)kShareCap) {
+    uint32_t o = nb_off;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+      if ((v[j] >> (32 - kShareHi)) == hi) buck[o++] = v[j];
+    __syncthreads();
+    if (wave == 0) {
+      // want-th largest in the bucket, want = K - above_tot >= 1 (the top bits are maximal)
+      const uint32_t want = (uint32_t)a.K - above_tot;
+      uint32_t x[kShareCap / 64];
+#pragma unroll
+      for (int i = 0; i < kShareCap / 64; ++i) {
+        const uint32_t idx = (uint32_t)(lane + 64 * i);
+        x[i] = idx < nb_tot ? buck[idx] : 0u;  // 0 is below every candidate (it has bits set)
+      }
+      uint32_t th = thr;
+      for (int bit = 31 - kShareHi; bit >= 0; --bit) {
+        const uint32_t cand = th | (1u << bit);
+        uint32_t c = 0;
+#pragma unroll
+        for (int i = 0; i < kShareCap / 64; ++i) c += x[i] >= cand;
+        if (wave_sum_u(c) >= want) th = cand;
+      }
+      if (lane == 0) thr_out = th;
+    }
+    __syncthreads();
+    thr = thr_out;
+  } else {
+    for (int bit = 31 - kShareHi; bit >= 0; --bit) thr = step(thr, bit);
   }
   // Mass above thr, plus thr for the ties needed to make K.
   float sum = 0.f;
@@ -216,7 +303,7 @@ __global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
   sum = wave_sum_f(sum);
   gt = wave_sum_u(gt);
   __syncthreads();
-  if ((t & 63) == 0) {
+  if (lane == 0) {
     part_f[wave] = sum;
     part_u[0][wave] = gt;
   }
@@ -568,6 +655,7 @@ extern "C" int sa_topk_share(const float* P, int64_t p_bh_stride, int64_t p_row_
   if (n > 16384) return sa::fail(SA_ERR_UNSUPPORTED, "%s: n=%d > 16384", fn, n);
   ShareArgs a;
   a.P = P; a.p_bh = p_bh_stride; a.p_row = p_row_stride; a.rows = rows; a.n = n; a.K = K; a.share = share;
+  a.vec_ok = (reinterpret_cast<uintptr_t>(P) % 16 == 0 && p_bh_stride % 4 == 0 && p_row_stride % 4 == 0) ? 1 : 0;
   a.total = (int64_t)BH * rows;
   hipLaunchKernelGGL(share_kernel, dim3((unsigned)a.total), dim3(256), 0, sa::as_stream(stream), a);
   return sa::check_launch(fn);
