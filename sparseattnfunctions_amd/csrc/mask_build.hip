@@ -23,6 +23,7 @@ constexpr int kPoolD = 64;        // head dim handled by the pooling kernel
 constexpr int kRowsPerWG = 16;    // score rows per top-k workgroup (4 per wave)
 constexpr int kColChunk = 64;     // key blocks staged in LDS per step
 constexpr int kKpStride = 68;     // LDS stride (floats) of a staged pooled-K row (float4, conflict-free)
+static_assert(kColChunk == 64, "topk_kernel maps chunk e to the wave's key column 64e + lane");
 
 // ---------------------------------------------------------------------------------------
 // Pooling: wave = 8 blocks; lane = (block lane>>3, dims 8*(lane&7)..+7); each lane sums its
@@ -105,22 +106,40 @@ __device__ inline uint32_t order_bits(float f) {
 // writes the union with text rows/columns and the local window as the ascending kv list.
 template <int NCH>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
-  constexpr int NPAD = 64 * NCH;
-  __shared__ float s_lds[kRowsPerWG][NPAD];
   __shared__ __attribute__((aligned(16))) float q_lds[kRowsPerWG][kPoolD];
   __shared__ __attribute__((aligned(16))) float k_lds[kColChunk * kKpStride];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: rows are wave-uniform
   const int bh = blockIdx.x / a.row_groups;
   const int r0 = (blockIdx.x - bh * a.row_groups) * kRowsPerWG;
   const int64_t row_base = (int64_t)bh * a.nqb;
+  const int nch = (a.nkb + 63) >> 6;
+  const int k = a.topk < a.nkb ? a.topk : a.nkb;
+
+  // Lane `lane` of wave w holds column 64e + lane of rows 4w..4w+3 as ordered keys (0 =
+  // unused). The score loop below produces exactly this mapping, so the scores go from
+  // the FMA accumulators into the keys without an LDS round trip; the workgroup's LDS is
+  // only the staged q rows and one 64-column chunk of pooled K.
+  uint32_t key[4][NCH];
+  bool live[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) live[u] = r0 + wave * 4 + u < a.nqb;  // wave-uniform
 
   if (a.scores_in) {
-    for (int e = tid; e < kRowsPerWG * a.nkb; e += 256) {
-      const int rr = e / a.nkb, c = e - rr * a.nkb;
-      if (r0 + rr < a.nqb) s_lds[rr][c] = a.scores_in[(row_base + r0 + rr) * a.nkb + c];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t row = row_base + r0 + wave * 4 + u;
+#pragma unroll
+      for (int e = 0; e < NCH; ++e) {
+        const int c = 64 * e + lane;
+        const bool valid = live[u] && e < nch && c < a.nkb;
+        float sc = 0.f;
+        if (valid) sc = a.scores_in[row * a.nkb + c];
+        key[u][e] = valid ? order_bits(sc) : 0u;
+        if (a.scores_out && valid) a.scores_out[row * a.nkb + c] = sc;
+      }
     }
   } else {
     // q rows and 64-column chunks of pooled K staged as float4; score = fmaf chain over
@@ -133,60 +152,61 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       *reinterpret_cast<float4*>(&q_lds[rr][4 * d4]) = v;
     }
     const float* kpb = a.kp + (int64_t)bh * a.nkb * kPoolD;
-    for (int c0 = 0; c0 < a.nkb; c0 += kColChunk) {
-      __syncthreads();
-      const int nc = min(kColChunk, a.nkb - c0);
-      for (int e = tid; e < nc * (kPoolD / 4); e += 256) {
-        const int c = e >> 4, d4 = e & 15;
-        *reinterpret_cast<float4*>(&k_lds[c * kKpStride + 4 * d4]) =
-            *reinterpret_cast<const float4*>(kpb + (int64_t)(c0 + c) * kPoolD + 4 * d4);
-      }
-      __syncthreads();
-      const int c = tid & 63;
-      const int rg = (tid >> 6) * 4;
-      if (c < nc) {
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int d = 0; d < kPoolD; d += 4) {
-          const float4 kv = *reinterpret_cast<const float4*>(&k_lds[c * kKpStride + d]);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float4 qv = *reinterpret_cast<const float4*>(&q_lds[rg + u][d]);
-            acc[u] = fmaf(qv.x, kv.x, acc[u]);
-            acc[u] = fmaf(qv.y, kv.y, acc[u]);
-            acc[u] = fmaf(qv.z, kv.z, acc[u]);
-            acc[u] = fmaf(qv.w, kv.w, acc[u]);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) s_lds[rg + u][c0 + c] = acc[u];
-      }
-    }
-  }
-  __syncthreads();
-
-  const int nch = (a.nkb + 63) >> 6;
-  const int k = a.topk < a.nkb ? a.topk : a.nkb;
-  // The wave's 4 rows are selected together: their 32-step searches are independent chains
-  // of ballot -> popcount -> compare, interleaved to hide each other's latency.
-  uint32_t key[4][NCH];  // ordered keys of this lane's columns c = 64e + lane (0 = unused)
-  bool live[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int rr = wave * 4 + u;
-    live[u] = r0 + rr < a.nqb;  // wave-uniform
-    const int64_t row = row_base + r0 + rr;
+    const int rg = wave * 4;
 #pragma unroll
     for (int e = 0; e < NCH; ++e) {
-      const int c = 64 * e + lane;
-      const bool valid = live[u] && e < nch && c < a.nkb;
-      key[u][e] = valid ? order_bits(s_lds[rr][c]) : 0u;
-      if (a.scores_out && valid) a.scores_out[row * a.nkb + c] = s_lds[rr][c];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) key[u][e] = 0u;
+      if (e < nch) {  // workgroup-uniform, so the barriers below are too
+        const int c0 = e * kColChunk;
+        __syncthreads();
+        const int nc = min(kColChunk, a.nkb - c0);
+        for (int i = tid; i < nc * (kPoolD / 4); i += 256) {
+          const int c = i >> 4, d4 = i & 15;
+          *reinterpret_cast<float4*>(&k_lds[c * kKpStride + 4 * d4]) =
+              *reinterpret_cast<const float4*>(kpb + (int64_t)(c0 + c) * kPoolD + 4 * d4);
+        }
+        __syncthreads();
+        if (lane < nc) {
+          float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+          for (int d = 0; d < kPoolD; d += 4) {
+            const float4 kv = *reinterpret_cast<const float4*>(&k_lds[lane * kKpStride + d]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const float4 qv = *reinterpret_cast<const float4*>(&q_lds[rg + u][d]);
+              acc[u] = fmaf(qv.x, kv.x, acc[u]);
+              acc[u] = fmaf(qv.y, kv.y, acc[u]);
+              acc[u] = fmaf(qv.z, kv.z, acc[u]);
+              acc[u] = fmaf(qv.w, kv.w, acc[u]);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (!live[u]) continue;
+            key[u][e] = order_bits(acc[u]);
+            if (a.scores_out) a.scores_out[(row_base + r0 + rg + u) * a.nkb + c0 + lane] = acc[u];
+          }
+        }
+      }
     }
   }
+
+  // The wave's 4 rows are selected together: their 32-step searches are independent chains
+  // of ballot -> popcount -> compare, interleaved to hide each other's latency.
+  // The search keeps thr = the largest prefix with count(key >= thr) >= k. Once a candidate
+  // has exactly k keys at or above it, every later accepted candidate has exactly k as well,
+  // and the k-th largest key is the smallest of those k: count(key >= m + 1) < k for that
+  // minimum m. So the wave stops when each of its rows has seen an exact count, and every
+  // row then takes thr = min{key >= thr} (for a row that ran all 32 steps thr is already a
+  // key, and the minimum returns it). On C2 rows this ends the search after ~20 of 32 steps.
   uint32_t thr[4] = {0u, 0u, 0u, 0u};  // the k-th largest key (0 when k == 0: nothing selected)
   if (k > 0) {
-    for (int bit = 31; bit >= 0; --bit) {
+    // Bit u set: row u has seen an exact count (rows past nqb never search). Scalar.
+    int exact = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) exact |= live[u] ? 0 : 1 << u;
+    for (int bit = 31; bit >= 0 && exact != 15; --bit) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const uint32_t cand = thr[u] | (1u << bit);
@@ -194,7 +214,17 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 #pragma unroll
         for (int e = 0; e < NCH; ++e) count += __popcll(__ballot(key[u][e] >= cand));
         if (count >= k) thr[u] = cand;
+        exact |= count == k ? 1 << u : 0;
       }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t m = 0xffffffffu;
+#pragma unroll
+      for (int e = 0; e < NCH; ++e) m = key[u][e] >= thr[u] ? min(m, key[u][e]) : m;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) m = min(m, (uint32_t)__shfl_xor((int)m, off));
+      thr[u] = m;
     }
   }
 #pragma unroll
