@@ -91,7 +91,15 @@ struct FwdArgs {
   float* pool_r;
   int pool_ncol;
   int pool_lpad;
-  float* pool_lse;
+  float* pool_lse;  // null: not stored
+  // Fused pooled map (pool_po non-null; pooled block size = kPool): after its item the wave
+  // forms the Po rows of its own query rows, Po[i][c] = max over the rows r of query block i
+  // of exp2(R[c][r] - lse[r]), each Po row then divided by its sum. Po rows and columns are
+  // kPool-token blocks; Po is [B][H][pool_nd][pool_nd] with a unit last stride.
+  float* pool_po;
+  int64_t po_sb, po_sh, po_si;
+  int pool_nd;      // cdiv(Lq, kPool)
+  int pool_causal;  // columns past the query's diagonal 64-key tile were never computed: 0
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
@@ -537,15 +545,17 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   }
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
+  float row_lse = 0.f;  // pooling: log2-sum-exp2 of row qb * 64 + lane
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const float l_tot = xhalf_sum(l[g]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if constexpr (kPool != 0) {
       // log2-sum-exp2 of the row: P = exp2(S * sc - m) / l_tot (m = -inf: the fast pass, 0).
-      if (g == hh)
-        a.pool_lse[(int64_t)bh * a.pool_lpad + qb * kBlock + lane] =
-            (m[g] == -INFINITY ? 0.f : m[g]) + log2f(l_tot);
+      if (g == hh) {
+        row_lse = (m[g] == -INFINITY ? 0.f : m[g]) + log2f(l_tot);
+        if (a.pool_lse) a.pool_lse[(int64_t)bh * a.pool_lpad + qb * kBlock + lane] = row_lse;
+      }
     }
     int row = qb * kBlock + 32 * g + col;
     bool store = row < a.Lq;
@@ -565,6 +575,60 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
               make_uint2(cvt_pk_bf16(A[4 * q4] * inv, A[4 * q4 + 1] * inv),
                          cvt_pk_bf16(A[4 * q4 + 2] * inv, A[4 * q4 + 3] * inv));
         }
+      }
+    }
+  }
+
+  if constexpr (kPool != 0) {
+    if (a.pool_po) {
+      // Fused pooled map. Lane l reads back the maxima it stored for row qb * 64 + l
+      // (R[c][l] at pool_r[... + c * 64 + l]: its own stores, so program order makes them
+      // visible). Po row of the lane: query block qb (64-row blocks) or 2 qb + hh (32-row
+      // blocks: each lane half is one Po row). Per chunk of 32 columns every lane forms
+      // x[j] = exp2(R - lse) (0 for rows past Lq and columns never computed), and a
+      // butterfly over the 32 lanes of each half takes the maxima: at the stage of offset
+      // o the lane keeps the half of its o * 2 values selected by lane bit o and takes the
+      // maximum with its partner's copy of that half, so lane l ends with column l & 31
+      // (a last exchange across the halves for 64-row blocks). One store per chunk writes
+      // the row's 32 columns; a second pass divides the row by its sum, reading back the
+      // same lanes' own stores.
+      constexpr int kCols = kBlock / kPool;  // columns per 64-key tile
+      const bool row_ok = qb * kBlock + lane < a.Lq;
+      const int ncol = a.pool_nd;
+      const int cend = a.pool_causal ? min(ncol, (qb + 1) * kCols) : ncol;
+      const float* rb = a.pool_r + ((int64_t)bh * a.nqb + qb) * a.pool_ncol * kBlock + lane;
+      const int pr = qb * kCols + (kCols == 2 ? hh : 0);
+      const bool writer = pr < a.pool_nd && (kCols == 2 || hh == 0);
+      float* po = a.pool_po + b * a.po_sb + h * a.po_sh + (int64_t)min(pr, a.pool_nd - 1) * a.po_si;
+      const int j_lane = lane & 31;
+      float tot = 0.f;  // this lane's columns, then summed over the 32 lanes
+      for (int c0 = 0; c0 < ncol; c0 += 32) {
+        // Every load is issued (at a computed column, clamped) before any is used.
+        float x[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) x[j] = rb[(int64_t)min(c0 + j, cend - 1) * kBlock];
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          x[j] = __builtin_amdgcn_exp2f(((c0 + j < cend && row_ok) ? x[j] : -INFINITY) - row_lse);
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+          const bool up = (lane & o) != 0;
+#pragma unroll
+          for (int i = 0; i < o; ++i) {
+            const float send = up ? x[i] : x[i + o];
+            const float keep = up ? x[i + o] : x[i];
+            x[i] = fmaxf(keep, __shfl_xor(send, o));
+          }
+        }
+        float vmax = x[0];  // column c0 + (lane & 31)
+        if (kCols == 1) vmax = fmaxf(vmax, __shfl_xor(vmax, 32));
+        tot += vmax;
+        if (writer && c0 + j_lane < ncol) po[c0 + j_lane] = vmax;
+      }
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) tot += __shfl_xor(tot, o);
+      if (writer) {
+        for (int c = j_lane; c < ncol; c += 32) po[c] = po[c] / tot;
       }
     }
   }
@@ -610,6 +674,14 @@ extern "C" int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int 
 
 namespace {
 
+// Fused pooled map of a pooling-mode launch (FwdArgs::pool_po): Po [B][H][nd][nd] fp32.
+struct PoolOut {
+  float* po;
+  int64_t sb, sh, si;
+  int nd;
+  int causal;
+};
+
 int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
                const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B,
                int H, int Lq, int Lk, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
@@ -617,7 +689,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
                const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
-               float* pool_lse = nullptr) {
+               float* pool_lse = nullptr, const PoolOut* pool_out = nullptr) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -684,8 +756,16 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.pool_ncol = pool_cols ? nkb * (kBlock / pool_cols) : 0;
   a.pool_lpad = nqb * kBlock;
   a.pool_lse = pool_lse;
-  SA_REQUIRE(pool_cols == 0 || (pool_r && pool_lse && !q_rows && !o_rows),
+  a.pool_po = pool_out ? pool_out->po : nullptr;
+  a.po_sb = pool_out ? pool_out->sb : 0;
+  a.po_sh = pool_out ? pool_out->sh : 0;
+  a.po_si = pool_out ? pool_out->si : 0;
+  a.pool_nd = pool_out ? pool_out->nd : 0;
+  a.pool_causal = pool_out ? pool_out->causal : 0;
+  SA_REQUIRE(pool_cols == 0 || (pool_r && (pool_lse || pool_out) && !q_rows && !o_rows),
              "%s: pooling needs its buffers and no row maps", fn);
+  SA_REQUIRE(!pool_out || (pool_out->po && pool_cols && Lq == Lk && pool_out->nd == sa::cdiv(Lq, pool_cols)),
+             "%s: fused pooled map needs pooling columns of the map's block size", fn);
 
   hipStream_t s = sa::as_stream(stream);
   const dim3 g((unsigned)grid), blk(64 * kWaves);
@@ -748,7 +828,9 @@ extern "C" int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_str
 // ---------------------------------------------------------------------------------------
 // Pooled attention map (attn_with_pooling, utils/attn_pooling_kernel.py:18-289): the
 // attention kernel in pooling mode stores each row's maximum scaled logit per 32- or 64-key
-// column and its log2-sum-exp2; pool_reduce_kernel turns them into
+// column. For 32- and 64-token blocks the same kernel then forms Po from them (FwdArgs::
+// pool_po); for 128-token blocks it also stores the rows' log2-sum-exp2, and
+// pool_reduce_kernel turns them into
 //   Po[i][j] = max over rows r of query block i, keys of key block j of exp2(R[c][r] - lse[r])
 // (the largest softmax probability of the block), each row of Po divided by its sum.
 namespace {
@@ -939,6 +1021,14 @@ extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3]
   if (int rc = sa::check_launch(fn)) return rc;
   float* r = reinterpret_cast<float*>(ws + p.r);
   float* lse = reinterpret_cast<float*>(ws + p.lse);
+  if (block_size == p.G) {
+    // 32- or 64-token blocks: one wave's 64 query rows are one or two whole Po rows, so
+    // the attention kernel forms them itself (no log-sum-exp buffer, no reduce launch).
+    const PoolOut po_out{po, po_strides[0], po_strides[1], po_strides[2], nd, causal ? 1 : 0};
+    return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, L, D, la.idx, la.cnt,
+                      p.nkb, true, causal ? la.slot : nullptr, causal ? la.mask : nullptr, nullptr, nullptr,
+                      sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, nullptr, &po_out);
+  }
   if (int rc = launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, L, D, la.idx, la.cnt,
                           p.nkb, true, causal ? la.slot : nullptr, causal ? la.mask : nullptr, nullptr, nullptr,
                           sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, lse))

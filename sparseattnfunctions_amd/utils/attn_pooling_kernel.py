@@ -8,9 +8,11 @@ its sum. It is a block-score map for the mask builders, e.g.
 
 One call runs the block-sparse attention kernel over every key block (causal: the blocks up
 to the diagonal, the diagonal tile masked to keys <= query) in its pooling mode. Each query
-row stores its largest scaled logit per 32- or 64-key column and its log-sum-exp to a
-workspace. A reduce kernel then forms Po = max over the block's rows of exp2(R - lse) and
-normalises it. The probability matrix itself is never written.
+row stores its largest scaled logit R per 32- or 64-key column to a workspace. For block
+sizes 32 and 64 each wave's 64 query rows are whole Po rows, and the wave forms them after
+its rows: Po = max over the block's rows of exp2(R - lse), normalised. For block size 128 the
+rows' log-sum-exps are stored too, and a reduce kernel does this over two waves' rows. The
+probability matrix itself is never written.
 
 Differences from the reference: q, k and v must be bf16 (the reference also accepts fp16 and
 fp32, and casts bf16 up to fp32). head_dim must be 64. The rows of a last, partial query
