@@ -155,7 +155,7 @@ __device__ inline uint2 lds_read_tr16(const lds_u8* p) {
 typedef unsigned sa_u32x2v __attribute__((ext_vector_type(2)));
 // The same read issued as inline assembly: the compiler's wait analysis cannot tell these
 // reads from the copies still landing in the other LDS buffers and would otherwise wait for
-// all of them; the caller waits for the reads explicitly (lgkm_wait_vop).
+// all of them; the caller waits for the reads explicitly (lgkm_wait_pair).
 template <int kOff>
 __device__ inline sa_u32x2v lds_read_tr16_asm(uint32_t addr) {
   sa_u32x2v r;
@@ -174,6 +174,21 @@ __device__ inline void dma_tile(const void* base, uint32_t bytes, uint32_t tile_
   for (int i = 0; i < 8; ++i)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_u8*)(dst + 1024 * i), 16,
                                              tile_off + 8 * i * row_bytes + goff[i & 1], 0, 0, 0);
+}
+
+// Waits until at most n LDS reads are outstanding (n in 0..14, even), tying the wait to
+// the two registers it makes valid so that nothing reads them earlier.
+__device__ __forceinline__ void lgkm_wait_pair(int n, sa_u32x2v& a, sa_u32x2v& b) {
+  switch (n) {
+    case 14: asm volatile("s_waitcnt lgkmcnt(14)" : "+v"(a), "+v"(b)); break;
+    case 12: asm volatile("s_waitcnt lgkmcnt(12)" : "+v"(a), "+v"(b)); break;
+    case 10: asm volatile("s_waitcnt lgkmcnt(10)" : "+v"(a), "+v"(b)); break;
+    case 8: asm volatile("s_waitcnt lgkmcnt(8)" : "+v"(a), "+v"(b)); break;
+    case 6: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(a), "+v"(b)); break;
+    case 4: asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(a), "+v"(b)); break;
+    case 2: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(a), "+v"(b)); break;
+    default: asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b) : : "memory"); break;
+  }
 }
 
 // s_waitcnt encodings (gfx9): vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
@@ -475,35 +490,12 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
       // ---- V^T operands of this tile, then request the next tile's V.
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
-      sa_u32x2v vr[2][2][2][2];  // [dc][t][c][u]
-#pragma unroll
-      for (int dc = 0; dc < 2; ++dc)
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint32_t base = (uint32_t)(uintptr_t)(vl + vro[dc][t]);
-          vr[dc][t][0][0] = lds_read_tr16_asm<0>(base);
-          vr[dc][t][0][1] = lds_read_tr16_asm<2048>(base);
-          vr[dc][t][1][0] = lds_read_tr16_asm<4096>(base);
-          vr[dc][t][1][1] = lds_read_tr16_asm<6144>(base);
-        }
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(vr[0][0][0][0]), "+v"(vr[0][0][0][1]), "+v"(vr[0][0][1][0]), "+v"(vr[0][0][1][1]),
-                     "+v"(vr[0][1][0][0]), "+v"(vr[0][1][0][1]), "+v"(vr[0][1][1][0]), "+v"(vr[0][1][1][1]),
-                     "+v"(vr[1][0][0][0]), "+v"(vr[1][0][0][1]), "+v"(vr[1][0][1][0]), "+v"(vr[1][0][1][1]),
-                     "+v"(vr[1][1][0][0]), "+v"(vr[1][1][0][1]), "+v"(vr[1][1][1][0]), "+v"(vr[1][1][1][1]));
-      sa_u32x4v vop[2][2][2];
-#pragma unroll
-      for (int dc = 0; dc < 2; ++dc)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int u = 0; u < 2; ++u)
-            vop[dc][c][u] = sa_u32x4v{vr[dc][0][c][u].x, vr[dc][0][c][u].y, vr[dc][1][c][u].x, vr[dc][1][c][u].y};
-      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-      issue_v(kb_next);
-
-      // ---- O^T += V^T P^T over the tile's four 16-key steps.
-      
+      // The reads are issued in the order the P·V MFMAs consume them, and each MFMA pair
+      // waits only for its own two reads (LDS reads return in order; the full wait first
+      // leaves no scalar load outstanding, so the counts are exact). The next tile's V
+      // copy overwrites this buffer, so it is requested after the last read has landed.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      sa_u32x2v vr[2][2][2][2];  // [c][u][dc][t]
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -511,12 +503,32 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int dc = 0; dc < 2; ++dc)
 #pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const uint32_t base = (uint32_t)(uintptr_t)(vl + vro[dc][t]);
+              vr[c][u][dc][t] = (c == 0 ? (u == 0 ? lds_read_tr16_asm<0>(base) : lds_read_tr16_asm<2048>(base))
+                                        : (u == 0 ? lds_read_tr16_asm<4096>(base) : lds_read_tr16_asm<6144>(base)));
+            }
+
+      // ---- O^T += V^T P^T over the tile's four 16-key steps.
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int dc = 0; dc < 2; ++dc) {
+            constexpr int kReads = 16;
+            const int done = 2 * ((c * 2 + u) * 2 + dc) + 2;  // reads this MFMA pair needs
+            lgkm_wait_pair(kReads - done, vr[c][u][dc][0], vr[c][u][dc][1]);
+            const sa_u32x4v vop = {vr[c][u][dc][0].x, vr[c][u][dc][0].y, vr[c][u][dc][1].x, vr[c][u][dc][1].y};
+#pragma unroll
             for (int g = 0; g < 2; ++g)
-              acc[dc][g] = mfma32(as_bf16x8(vop[dc][c][u]),
+              acc[dc][g] = mfma32(as_bf16x8(vop),
                                   as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
                                                       P[g][c][4 * u + 3]}),
                                   acc[dc][g]);
-      
+          }
+      issue_v(kb_next);
+
       it = it + 1;
       kb = kb_next;
     }
