@@ -373,14 +373,15 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
 
 // ---------------------------------------------------------------------------------------
 // simgram_kernel: judge_similarity with the probabilities kept on chip. One wave per (bh,
-// chunk of kGramChunk = 8 sample positions s1). Its four 32-column query groups hold, for
-// two positions each, the F frames' rows f1*ns + s1 (column 16*(s1 & 1) + f1; columns with
-// f1 >= F and positions past ns are zero queries whose results are never used).
+// chunk of kGramChunk = 8 sample positions s1). Its three 32-column query groups hold the
+// F frames' rows f1*ns + s1 of the 8 positions, 12 columns per position: flat column
+// 32 g + col = 12 j + f1 for position j of the chunk (columns with f1 >= F and positions
+// past ns are zero queries whose results are never used).
 //   pass 1: row max and sum over every key, bias on the T text keys (as probs_kernel);
 //   pass 2, per key frame f2: the probabilities of the frame's ns keys, 32 at a time, go
-//           through LDS ([group][key][column]); lane (key k, half sl) then adds, for each
-//           group, the products P[f1][k] P[f3][k] of its position's F rows into F(F+1)/2
-//           per-lane sums. After the frame the 64 lanes' sums are added through LDS, in lane
+//           through LDS ([key][flat column]); lane (key k, half sl) then adds, for each of
+//           its positions 4 sl .. 4 sl + 3, the products P[f1][k] P[f3][k] of the
+//           position's F rows into F(F+1)/2 per-lane sums. After the frame the 64 lanes' sums are added through LDS, in lane
 //           order, into G[bh][f2][chunk][pair].
 struct SimGramArgs {
   const uint16_t* qs;  // [BH][rows_pad][64], row f*ns + s
@@ -392,15 +393,19 @@ struct SimGramArgs {
   int64_t total;  // BH * n_chunks
 };
 
-constexpr int kSgGroups = kGramChunk / 2;  // query groups per wave
-constexpr int kSgStride = 36;              // LDS row stride of the P tiles (conflict-free b128 reads)
+constexpr int kSgWidth = 12;                            // columns per position (F <= 12)
+constexpr int kSgGroups = kGramChunk * kSgWidth / 32;  // query groups per wave
+static_assert(kGramChunk * kSgWidth == 32 * kSgGroups, "positions fill whole query groups");
+// LDS row stride (floats) of the P tile [key][flat column]: stride / 4 odd, so a b128 read
+// by 16 lanes of consecutive keys covers 16 distinct 4-bank chunks (64 banks).
+constexpr int kSgStride = 32 * kSgGroups + 4;
 
 template <int F>
 __global__ __launch_bounds__(256, 2) void simgram_kernel(SimGramArgs a) {
   static_assert(F >= 1 && F <= 12, "frames");
   constexpr int NP = F * (F + 1) / 2;
   constexpr int kRed = 64 * NP;
-  constexpr int kTile = kSgGroups * 32 * kSgStride;
+  constexpr int kTile = 32 * kSgStride;
   constexpr int kLds = kRed > kTile ? kRed : kTile;
   constexpr int kRead = (F + 3) / 4;  // 16-byte reads per row of F values
   __shared__ __attribute__((aligned(16))) float lds[4][kLds];
@@ -415,7 +420,8 @@ __global__ __launch_bounds__(256, 2) void simgram_kernel(SimGramArgs a) {
   sa_bf16x8 qf[kSgGroups][4];
 #pragma unroll
   for (int g = 0; g < kSgGroups; ++g) {
-    const int s1 = chunk * kGramChunk + 2 * g + (col >> 4), f1 = col & 15;
+    const int flat = 32 * g + col;
+    const int s1 = chunk * kGramChunk + flat / kSgWidth, f1 = flat % kSgWidth;
     const bool ok = f1 < F && s1 < a.ns;
     const uint16_t* qp = a.qs + (bh * a.rows_pad + (ok ? f1 * a.ns + s1 : 0)) * kD + 8 * hh;
 #pragma unroll
@@ -481,7 +487,10 @@ __global__ __launch_bounds__(256, 2) void simgram_kernel(SimGramArgs a) {
   // positions past ns (zero queries, whose uniform rows are not samples) write zeros.
   bool pos_ok[kSgGroups];
 #pragma unroll
-  for (int g = 0; g < kSgGroups; ++g) pos_ok[g] = chunk * kGramChunk + 2 * g + (col >> 4) < a.ns;
+  for (int g = 0; g < kSgGroups; ++g) {
+    const int flat = 32 * g + col;
+    pos_ok[g] = chunk * kGramChunk + flat / kSgWidth < a.ns && flat % kSgWidth < F;
+  }
   const int my_key = lane & 31, sl = lane >> 5;
   const int n_kt = (a.ns + 31) / 32;
   float acc[NP];
@@ -500,14 +509,14 @@ __global__ __launch_bounds__(256, 2) void simgram_kernel(SimGramArgs a) {
           const int kr = 8 * (i >> 2) + 4 * hh + (i & 3);
           const float pv = (pos_ok[g] && 32 * t + kr < a.ns)
                                ? __builtin_amdgcn_exp2f(fmaf(tt[i], a.scale_log2, -m[g])) * inv[g] : 0.f;
-          L[(g * 32 + kr) * kSgStride + col] = pv;
+          L[kr * kSgStride + 32 * g + col] = pv;
         }
       }
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int g = 0; g < kSgGroups; ++g) {
+      for (int j = 0; j < kGramChunk / 2; ++j) {
         float x[4 * kRead];
-        const float* rp = L + (g * 32 + my_key) * kSgStride + 16 * sl;
+        const float* rp = L + my_key * kSgStride + kSgWidth * (kGramChunk / 2 * sl + j);
 #pragma unroll
         for (int u = 0; u < kRead; ++u) {
           const float4 v4 = *reinterpret_cast<const float4*>(rp + 4 * u);
