@@ -33,9 +33,10 @@ namespace {
 
 constexpr int kD = 64;           // head dim handled here
 constexpr int kMaxC = 2 * kD + 2;  // channels of the per-head (k, |k|, v, |v|) metric
-constexpr int kTileS = 64;       // src rows per match workgroup
-constexpr int kTileD = 64;       // dst columns per staged tile
-constexpr int kTileLd = 68;      // channel-major LDS row: 64 rows + 4 pad (16-byte aligned)
+constexpr int kMTile = 128;      // src rows per match workgroup, dst columns per dst tile
+constexpr int kMChunk = 16;      // channels staged in LDS per step
+constexpr int kMLd = kMTile + 4;  // channel-major LDS row (16-byte aligned; 4-bank offset per row)
+constexpr int kMMaxSplits = 16;  // dst splits of the match grid
 constexpr int kRankTile = 1024;  // keys staged per rank step
 
 __device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -140,15 +141,18 @@ __global__ __launch_bounds__(256) void normalize_kernel(const float* in, int64_t
 
 // ---------------------------------------------------------------------------------------
 // Match: for each src, the dst of largest score (fmaf chain over channels) in this
-// workgroup's dst range; ties -> lowest dst position. Workgroup = 64 src x dst range,
-// thread (ty, tx) owns src rows 4ty..4ty+3 and dst columns 4tx..4tx+3 of each staged tile.
+// workgroup's dst range; ties -> lowest dst position. Workgroup = 128 src x dst range in
+// 128-column dst tiles; thread (ty, tx) owns src rows 8ty..8ty+7 and dst columns
+// 8tx..8tx+7 of each tile (64 accumulators: two 16-byte LDS reads per operand and channel
+// feed 64 FMAs). Channels are staged 16 at a time, channel-major (As[c][row], Bs[c][col]),
+// and every score still runs its fmaf chain over c = 0..C-1 in order.
 struct MatchArgs {
   const float* metric;  // [G][N][C]
   int G, N, C;
   const int32_t* a_idx;
   const int32_t* b_idx;
   int n_src, n_dst;
-  int splits, dst_per_split;
+  int splits, dst_per_split;  // dst_per_split: a multiple of kMTile
   float* part_max;  // [G][splits][n_src]
   int32_t* part_idx;
 };
@@ -156,59 +160,59 @@ struct MatchArgs {
 __device__ inline bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
 __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
-  extern __shared__ float sm[];
+  __shared__ __attribute__((aligned(16))) float As[kMChunk * kMLd];
+  __shared__ __attribute__((aligned(16))) float Bs[kMChunk * kMLd];
   const int C = a.C;
-  // Tiles are stored channel-major (As[c][row], Bs[c][col], kTileLd floats per channel) so
-  // that a thread reads its 4 rows and its 4 columns of one channel with one 16-byte read each.
-  float* As = sm;
-  float* Bs = sm + C * kTileLd;
   const int g = blockIdx.y, split = blockIdx.z;
-  const int s0 = blockIdx.x * kTileS;
+  const int s0 = blockIdx.x * kMTile;
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
   const float* mg = a.metric + (int64_t)g * a.N * C;
-  for (int e = tid; e < kTileS * C; e += 256) {
-    const int r = e / C, c = e - r * C;
-    const int s = s0 + r;
-    As[c * kTileLd + r] = s < a.n_src ? mg[(int64_t)a.a_idx[s] * C + c] : 0.f;
-  }
-  float best[4];
-  int bidx[4];
+  float best[8];
+  int bidx[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     best[i] = -INFINITY;
     bidx[i] = 0;
   }
   const int d_lo = split * a.dst_per_split;
   const int d_hi = min(a.n_dst, d_lo + a.dst_per_split);
-  for (int d0 = d_lo; d0 < d_hi; d0 += kTileD) {
-    __syncthreads();
-    for (int e = tid; e < kTileD * C; e += 256) {
-      const int r = e / C, c = e - r * C;
-      const int d = d0 + r;
-      Bs[c * kTileLd + r] = d < d_hi ? mg[(int64_t)a.b_idx[d] * C + c] : 0.f;
+  for (int d0 = d_lo; d0 < d_hi; d0 += kMTile) {
+    float acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+    for (int c0 = 0; c0 < C; c0 += kMChunk) {
+      const int nc = min(kMChunk, C - c0);
+      __syncthreads();
+      // Element e: row e / 16, channel c0 + e % 16 (16 consecutive channels of one row per
+      // 16 threads; the transposed stores hit 64 distinct banks per wave).
+      for (int e = tid; e < kMTile * kMChunk; e += 256) {
+        const int r = e >> 4, cc = e & 15;
+        const int s = s0 + r, d = d0 + r;
+        As[cc * kMLd + r] = (s < a.n_src && cc < nc) ? mg[(int64_t)a.a_idx[s] * C + c0 + cc] : 0.f;
+        Bs[cc * kMLd + r] = (d < d_hi && cc < nc) ? mg[(int64_t)a.b_idx[d] * C + c0 + cc] : 0.f;
+      }
+      __syncthreads();
+      for (int cc = 0; cc < nc; ++cc) {
+        const float4 a0 = *reinterpret_cast<const float4*>(As + cc * kMLd + 8 * ty);
+        const float4 a1 = *reinterpret_cast<const float4*>(As + cc * kMLd + 8 * ty + 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(Bs + cc * kMLd + 8 * tx);
+        const float4 b1 = *reinterpret_cast<const float4*>(Bs + cc * kMLd + 8 * tx + 4);
+        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+      }
     }
-    __syncthreads();
-    float acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-    for (int c = 0; c < C; ++c) {
-      const float4 a4 = *reinterpret_cast<const float4*>(As + c * kTileLd + 4 * ty);
-      const float4 b4 = *reinterpret_cast<const float4*>(Bs + c * kTileLd + 4 * tx);
-      const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-      const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int d = d0 + 4 * tx + j;
+    for (int j = 0; j < 8; ++j) {
+      const int d = d0 + 8 * tx + j;
       if (d < d_hi) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
           if (better(acc[i][j], d, best[i], bidx[i])) {
             best[i] = acc[i][j];
             bidx[i] = d;
@@ -221,7 +225,7 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const float ov = __shfl_xor(best[i], off, 16);
       const int oi = __shfl_xor(bidx[i], off, 16);
       if (better(ov, oi, best[i], bidx[i])) {
@@ -232,8 +236,8 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
   }
   if (tx == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int s = s0 + 4 * ty + i;
+    for (int i = 0; i < 8; ++i) {
+      const int s = s0 + 8 * ty + i;
       if (s < a.n_src) {
         const int64_t o = ((int64_t)g * a.splits + split) * a.n_src + s;
         a.part_max[o] = best[i];
@@ -241,6 +245,17 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
       }
     }
   }
+}
+
+// Dst splits of the match grid: whole 128-column tiles, at most kMMaxSplits splits.
+int match_tiles_per_split(int n_dst) {
+  const int n_dt = (n_dst + kMTile - 1) / kMTile;
+  return (n_dt + kMMaxSplits - 1) / kMMaxSplits;
+}
+int match_splits(int n_dst) {
+  const int n_dt = (n_dst + kMTile - 1) / kMTile;
+  const int per = match_tiles_per_split(n_dst);
+  return std::max(1, (n_dt + per - 1) / per);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -556,7 +571,7 @@ extern "C" int sa_tome_normalize(const float* metric, int64_t rows, int C, float
 
 extern "C" int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes) {
   SA_REQUIRE(bytes && G > 0 && n_src >= 0 && n_dst > 0, "sa_tome_match_workspace: bad arguments");
-  const int splits = std::max(1, std::min(16, n_dst / 256));
+  const int splits = match_splits(n_dst);
   *bytes = (int64_t)G * splits * std::max(n_src, 1) * 8;
   return sa::ok();
 }
@@ -572,22 +587,16 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
   sa_tome_match_workspace(m.G, m.n_src, m.n_dst, &need);
   SA_REQUIRE(ws_bytes >= need, "sa_tome_match: workspace %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   hipStream_t s = sa::as_stream(stream);
-  const int splits = std::max(1, std::min(16, m.n_dst / 256));
+  const int splits = match_splits(m.n_dst);
   float* part_max = reinterpret_cast<float*>(workspace);
   int32_t* part_idx = reinterpret_cast<int32_t*>(part_max + (int64_t)m.G * splits * std::max(m.n_src, 1));
   if (m.n_src > 0) {
     MatchArgs a;
     a.metric = metric; a.G = m.G; a.N = m.N; a.C = C; a.a_idx = m.a_idx; a.b_idx = m.b_idx;
     a.n_src = m.n_src; a.n_dst = m.n_dst; a.splits = splits;
-    a.dst_per_split = (m.n_dst + splits - 1) / splits;
+    a.dst_per_split = match_tiles_per_split(m.n_dst) * kMTile;
     a.part_max = part_max; a.part_idx = part_idx;
-    const size_t lds = (size_t)2 * C * kTileLd * sizeof(float);
-    if (lds > 65536) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(match_kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return sa::fail(SA_ERR_HIP, "sa_tome_match: LDS attribute: %s", hipGetErrorString(e));
-    }
-    hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kTileS - 1) / kTileS, m.G, splits), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kMTile - 1) / kMTile, m.G, splits), dim3(256), 0, s, a);
     if ((rc = sa::check_launch("sa_tome_match/match"))) return rc;
   }
   MapArgs ma;
