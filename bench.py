@@ -58,7 +58,7 @@ def load_traffic():
         return json.load(f).get("bytes_per_launch")
 
 
-def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=4):
+def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=30):
     """Times the oracle's dense-masked fp32 attention (kron mask -> masked_fill -> softmax ->
     matmul, block_sparse_attn_kernel.py:326-334) on `n_heads_sample` (b, h) heads on the host
     and scales to the full call."""
@@ -81,7 +81,7 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=4):
         "cores": threads,
         "kind": "port",
         "sample": f"{len(heads)} of {B * H} (b,h) heads of the C2 call, fp32 dense-masked, "
-                  f"{dt:.1f} s, scaled x{scale:.0f}",
+                  f"{dt:.1f} s, scaled x{scale:g}",
         "cpu": _cpu_model(),
     }
 
