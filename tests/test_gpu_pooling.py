@@ -58,6 +58,19 @@ def test_pooled_attention_short_sequences(dev, L, bs, causal):
     assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7)
 
 
+@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pooled_attention_several_column_chunks(dev, bs, causal):
+    # L = 2200: Po rows of 35 (bs 64) or 69 (bs 32) columns, so the attention kernel's Po
+    # epilogue runs over two or three 32-column chunks, including a partial last one.
+    case(f"attn_with_pooling L=2200 bs={bs} causal={causal}")
+    q, k, v = _qkv(2200 + bs + causal, 1, 1, 1, 2200)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, 0.125, bs)
+    want_o, want_po = pooled_attention(q, k, v, causal, 0.125, bs)
+    assert (o.cpu().double() - want_o).abs().max().item() <= 2e-2
+    assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7), (po.cpu().double() - want_po).abs().max()
+
+
 def test_pooled_attention_large_scores(dev):
     # scores of several hundred: the kernel's safe pass; Po must not depend on it
     case("attn_with_pooling large scores")
