@@ -166,6 +166,27 @@ def test_fused_gram_matches_written_probabilities(dev):
     assert torch.allclose(fused, written, rtol=2e-5, atol=1e-9), (fused - written).abs().max()
 
 
+@pytest.mark.parametrize("frames,sample_num", [(5, 13), (12, 9)])
+def test_similarity_judge_other_frame_counts(dev, frames, sample_num):
+    # The similarity kernel gives each sampled position a 12-column slot of its query
+    # groups: 5 frames use 5 of 12 columns, 12 frames all of them; 13 and 9 samples leave
+    # a partial last chunk of 8 positions.
+    case(f"judge_similarity frames={frames} samples={sample_num}")
+    geo = pa.PatternGeometry(frames=frames, height=4, width=6, text_length=8, sample_num=sample_num)
+    g = torch.Generator().manual_seed(frames)
+    q = torch.randn(1, 3, geo.L, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 3, geo.L, 64, generator=g).to(torch.bfloat16)
+    qd, kd = q.to(dev), k.to(dev)
+    _, ik = pa.get_indexs(geo)
+    sim, col = pa.judge_similarity(qd, kd, geo, index_k=ik, return_sim=True)
+    p = ik[geo.text_length: geo.text_length + geo.sample_num] - geo.text_length
+    w_sim, w_col = opat.judge_similarity(q, k, p, geo.frames, geo.S, geo.text_length)
+    assert torch.allclose(col.cpu().double(), w_col, rtol=1e-4, atol=1e-5), (col.cpu().double() - w_col).abs().max()
+    fused = pa._similarity_gram(qd, kd, geo, ik)
+    written = pa._similarity_gram_via_probs(qd, kd, geo, ik)
+    assert torch.allclose(fused, written, rtol=2e-5, atol=1e-9), (fused - written).abs().max()
+
+
 def test_combined_attn_head_routing(dev):
     # Heads routed by unified_judge: pattern heads equal the pattern attention on those heads,
     # the others equal SparseGen_Plus's block-sparse attention on the remaining heads.
