@@ -14,7 +14,8 @@
 // Three kernels:
 //   sample_gather_kernel   one wave per (tensor, b*h, block): ranks the 64 draws, writes the
 //                          token ids and copies the sampled rows to a compact bf16 buffer.
-//   sampled_pool_kernel    one wave per (b*h, 32 sampled query rows): S^T = K Q^T with
+//   sampled_pool_kernel    one wave per (b*h, 32 sampled query rows), four waves of one head per
+//                          workgroup sharing each LDS-staged key tile: S^T = K Q^T with
 //                          v_mfma_f32_32x32x16_bf16 over all sampled keys, twice (row max and
 //                          sum, then probabilities), summing each num_keep x num_keep cell.
 //   energy_list_kernel     one wave per score row: rank, sorted prefix sums, the kept count,
@@ -95,13 +96,18 @@ struct PoolSArgs {
   const uint16_t* sk;  // [BH][ns_pad][64]
   float* pooled;       // [BH][nb][nb]
   int nb, ns, ns_pad, ng;
-  int64_t total;       // BH * ng waves
+  int wg_per_bh;       // ceil(ng / 4): workgroups per head
 };
 
-__device__ inline sa_f32x16 tile_scores(const uint16_t* kp, const sa_bf16x8 (&qf)[4]) {
+// Sampled-key tiles in LDS: 32 keys x 8 chunks of 16 bytes, chunk c of key r at slot
+// r * 8 + (c ^ ((r >> 1) & 7)). Any 16 consecutive lanes of an operand read (keys 2k, 2k+1
+// for 8 k, one chunk) or of a tile store then touch 16 distinct 16-byte bank groups.
+__device__ inline int kslot(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+
+__device__ inline sa_f32x16 tile_scores(const est_u32x4* kt, int col, int hh, const sa_bf16x8 (&qf)[4]) {
   est_u32x4 kop[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) kop[s] = *reinterpret_cast<const est_u32x4*>(kp + 16 * s);
+  for (int s = 0; s < 4; ++s) kop[s] = kt[kslot(col, 2 * s + hh)];
   sa_f32x16 t = {};
 #pragma unroll
   for (int s = 0; s < 4; ++s)
@@ -109,30 +115,44 @@ __device__ inline sa_f32x16 tile_scores(const uint16_t* kp, const sa_bf16x8 (&qf
   return t;
 }
 
-// One wave: sampled query rows 32g .. 32g+31 of head bh (lane column = query 32g + lane%32).
-// C element i of a 32-key tile is key 32kt + 8(i/4) + 4(lane/32) + i%4.
+// Workgroup: the 4 query groups 4w .. 4w + 3 of head bh, one per wave; wave v takes sampled
+// query rows 32g .. 32g+31 (lane column = query 32g + lane%32), g = 4w + v. C element i of a
+// 32-key tile is key 32kt + 8(i/4) + 4(lane/32) + i%4. The four waves read the same keys:
+// each 32-key tile is loaded once per workgroup (one coalesced 16-byte load per thread, the
+// next tile's in flight while this one is scored) into one of two LDS buffers; one barrier
+// per tile orders the store before the reads, and the reads of a buffer before its
+// rewrite two tiles later. Waves past ng take part in the loads and barriers only.
 template <int S>
 __global__ __launch_bounds__(256) void sampled_pool_kernel(PoolSArgs a) {
+  __shared__ est_u32x4 kt_lds[2][32 * 8];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
-  if (wid >= a.total) return;  // no workgroup barriers below
-  const int64_t bh = wid / a.ng;
-  const int g = (int)(wid - bh * a.ng);
+  const int64_t bh = blockIdx.x / a.wg_per_bh;
+  const int g = (int)(blockIdx.x - bh * a.wg_per_bh) * 4 + wave;
+  const bool active = g < a.ng;  // wave-uniform
   const int col = lane & 31, hh = lane >> 5;
   sa_bf16x8 qf[4];
   {
-    const uint16_t* qp = a.sq + (bh * a.ns_pad + 32 * g + col) * kD + 8 * hh;
+    const uint16_t* qp = a.sq + (bh * a.ns_pad + 32 * min(g, a.ng - 1) + col) * kD + 8 * hh;
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = __builtin_bit_cast(sa_bf16x8, *reinterpret_cast<const est_u32x4*>(qp + 16 * s));
   }
-  const uint16_t* kbase = a.sk + (bh * a.ns_pad + col) * kD + 8 * hh;
   const int nkt = a.ns_pad / 32;
+  // This thread's share of every tile: key r = tid / 8, chunk c = tid % 8.
+  const int ld_r = threadIdx.x >> 3, ld_c = threadIdx.x & 7;
+  const est_u32x4* ksrc = reinterpret_cast<const est_u32x4*>(a.sk + (bh * a.ns_pad + ld_r) * kD) + ld_c;
+  const int ld_slot = kslot(ld_r, ld_c);
+  constexpr int kTileU4 = 32 * kD / 8;  // 16-byte units per tile
 
   // Pass 1: row max and row sum of exp2 (online, per lane over its keys).
   float m = -INFINITY, l = 0.f;
+  est_u32x4 pre = ksrc[0];
   for (int kt = 0; kt < nkt; ++kt) {
-    const sa_f32x16 t = tile_scores(kbase + (int64_t)kt * 32 * kD, qf);
+    kt_lds[kt & 1][ld_slot] = pre;
+    __syncthreads();
+    if (kt + 1 < nkt) pre = ksrc[(int64_t)(kt + 1) * kTileU4];
+    if (!active) continue;
+    const sa_f32x16 t = tile_scores(kt_lds[kt & 1], col, hh, qf);
     float x[16];
     float tmax = -INFINITY;
 #pragma unroll
@@ -160,13 +180,21 @@ __global__ __launch_bounds__(256) void sampled_pool_kernel(PoolSArgs a) {
   }
   const float inv = 1.f / l;
 
-  // Pass 2: probabilities, summed per (query block, key block) cell.
+  // Pass 2: probabilities, summed per (query block, key block) cell. Its tiles continue pass
+  // 1's buffer alternation (step nkt + kt), so every store still goes to the buffer read two
+  // steps earlier, which the barrier of the step in between has released.
   constexpr int kBlocks = 32 / S;  // key blocks per 32-key tile
   const int qblk = (32 * g + col) / S;
-  const bool writer = hh == 0 && (col % S) == 0 && qblk < a.nb;
+  const bool writer = active && hh == 0 && (col % S) == 0 && qblk < a.nb;
   float* prow = a.pooled + (bh * a.nb + (writer ? qblk : 0)) * a.nb;
+  pre = ksrc[0];
   for (int kt = 0; kt < nkt; ++kt) {
-    const sa_f32x16 t = tile_scores(kbase + (int64_t)kt * 32 * kD, qf);
+    const int buf = (nkt + kt) & 1;
+    kt_lds[buf][ld_slot] = pre;
+    __syncthreads();
+    if (kt + 1 < nkt) pre = ksrc[(int64_t)(kt + 1) * kTileU4];
+    if (!active) continue;
+    const sa_f32x16 t = tile_scores(kt_lds[buf], col, hh, qf);
     float bs[kBlocks];
 #pragma unroll
     for (int j = 0; j < kBlocks; ++j) bs[j] = 0.f;
@@ -345,8 +373,8 @@ extern "C" int sa_sampled_block_scores(const uint16_t* q_sampled, const uint16_t
   PoolSArgs a;
   a.sq = q_sampled; a.sk = k_sampled; a.pooled = pooled;
   a.nb = nb; a.ns = nb * num_keep; a.ns_pad = ns_pad; a.ng = ns_pad / 32;
-  a.total = (int64_t)BH * a.ng;
-  const int64_t grid = (a.total + 3) / 4;
+  a.wg_per_bh = (a.ng + 3) / 4;
+  const int64_t grid = (int64_t)BH * a.wg_per_bh;
   SA_REQUIRE(grid < (1LL << 31), "sa_sampled_block_scores: grid too large");
   hipStream_t s = sa::as_stream(stream);
   if (num_keep == 8) {
