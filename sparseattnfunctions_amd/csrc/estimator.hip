@@ -237,7 +237,7 @@ struct EnergyArgs {
 template <int NCH>
 __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   constexpr int NPAD = 64 * NCH;
-  __shared__ uint32_t key_lds[4][NPAD];
+  __shared__ __attribute__((aligned(16))) uint64_t key_lds[4][NPAD];
   __shared__ float cum_lds[4][NPAD];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -245,24 +245,30 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   if (row >= a.rows) return;  // no workgroup barriers below
   const int n = a.nkb;
   const float* src = a.scores + row * n;
+  // Composite keys (order_key << 32 | ~column): larger = earlier in (score descending,
+  // column ascending), and all distinct, so a rank is one unsigned compare per other entry.
+  // Entries past n hold 0, below every valid key.
   float v[NCH];
-  uint32_t key[NCH];
+  uint64_t key[NCH];
 #pragma unroll
   for (int e = 0; e < NCH; ++e) {
     const int c = 64 * e + lane;
     v[e] = c < n ? src[c] : 0.f;
-    key[e] = c < n ? order_key(v[e]) : 0u;
+    key[e] = c < n ? ((uint64_t)order_key(v[e]) << 32) | (uint32_t)~c : 0ull;
     key_lds[wave][c] = key[e];
   }
   __builtin_amdgcn_wave_barrier();
-  // Rank in (score descending, column ascending); the value goes to its sorted slot.
+  // Rank = the number of larger keys; the value goes to its sorted slot.
   int rank[NCH];
 #pragma unroll
   for (int e = 0; e < NCH; ++e) rank[e] = 0;
-  for (int j = 0; j < n; ++j) {
-    const uint32_t kj = key_lds[wave][j];
+  for (int j0 = 0; j0 < n; j0 += 2) {  // two keys per 16-byte broadcast read
+    const uint4 k2 = *reinterpret_cast<const uint4*>(&key_lds[wave][j0]);
+    const uint64_t kq[2] = {((uint64_t)k2.y << 32) | k2.x, ((uint64_t)k2.w << 32) | k2.z};
 #pragma unroll
-    for (int e = 0; e < NCH; ++e) rank[e] += (kj > key[e]) || (kj == key[e] && j < 64 * e + lane);
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < NCH; ++e) rank[e] += kq[t] > key[e];
   }
 #pragma unroll
   for (int e = 0; e < NCH; ++e)
