@@ -294,24 +294,26 @@ __global__ void combine_kernel(MapArgs a) {
 }
 
 // rank[s] = #{s' : node_max[s'] ranks before node_max[s]} (descending value, then position).
+// Composite keys (order_bits << 32 | ~position) are distinct and larger exactly when earlier
+// in that order, so each comparison is one unsigned 64-bit compare; padding keys are 0.
 __global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, int splits) {
-  __shared__ uint32_t keys[kRankTile];
+  __shared__ __attribute__((aligned(16))) uint64_t keys[kRankTile];
   const int g = blockIdx.y;
   const int s = blockIdx.x * 256 + threadIdx.x;
   const float* nm = m.node_max + (int64_t)g * m.n_src;
-  const uint32_t mine = s < m.n_src ? order_bits(nm[s]) : 0u;
+  const uint64_t mine = s < m.n_src ? ((uint64_t)order_bits(nm[s]) << 32) | (uint32_t)~s : ~0ull;
   const int per = (m.n_src + splits - 1) / splits;
   const int j_lo = blockIdx.z * per, j_hi = min(m.n_src, j_lo + per);
   int count = 0;
   for (int t0 = j_lo; t0 < j_hi; t0 += kRankTile) {
     __syncthreads();
-    for (int e = threadIdx.x; e < kRankTile; e += 256) keys[e] = t0 + e < j_hi ? order_bits(nm[t0 + e]) : 0u;
+    for (int e = threadIdx.x; e < kRankTile; e += 256) {
+      const int j = t0 + e;
+      keys[e] = j < j_hi ? ((uint64_t)order_bits(nm[j]) << 32) | (uint32_t)~j : 0ull;
+    }
     __syncthreads();
     const int n = min(kRankTile, j_hi - t0);
-    for (int e = 0; e < n; ++e) {
-      const uint32_t o = keys[e];
-      count += (o > mine) || (o == mine && t0 + e < s);
-    }
+    for (int e = 0; e < n; e += 2) count += (keys[e] > mine) + (keys[e + 1] > mine);
   }
   if (s < m.n_src && count) atomicAdd(&m.rank[(int64_t)g * m.n_src + s], count);
 }
