@@ -34,6 +34,9 @@ constexpr float kLog2eOver8 = 0.18033688011112042f;  // log2(e) / 8: the referen
 
 typedef unsigned est_u32x4 __attribute__((ext_vector_type(4)));
 
+__device__ inline float from_order_key(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
 __device__ inline uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -237,8 +240,16 @@ struct EnergyArgs {
 template <int NCH>
 __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   constexpr int NPAD = 64 * NCH;
-  __shared__ __attribute__((aligned(16))) uint64_t key_lds[4][NPAD];
+  // Sort width: the row padded to a power of two; E keys per lane.
+  constexpr int NSORT = NCH <= 4 ? 256 : NCH <= 8 ? 512 : 1024;
+  constexpr int E = NSORT / 64;
+  static_assert(NPAD <= NSORT, "sort width");
+  // Rows of more than 320 blocks are sorted (O(n log^2 n)); shorter rows rank every entry
+  // against every other (O(n^2), faster there: 0.105 against 0.115 ms at 278 blocks).
+  constexpr bool kSort = NCH >= 8;
+  __shared__ __attribute__((aligned(16))) uint64_t key_lds[4][kSort ? 2 : NPAD];
   __shared__ float cum_lds[4][NPAD];
+  __shared__ uint8_t keep_lds[4][NPAD];  // 1: the column is among the first k of the order
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -246,33 +257,77 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   const int n = a.nkb;
   const float* src = a.scores + row * n;
   // Composite keys (order_key << 32 | ~column): larger = earlier in (score descending,
-  // column ascending), and all distinct, so a rank is one unsigned compare per other entry.
-  // Entries past n hold 0, below every valid key.
-  float v[NCH];
-  uint64_t key[NCH];
+  // column ascending), and all distinct; entries past n hold 0, below every valid key.
+  uint64_t key[E];
 #pragma unroll
-  for (int e = 0; e < NCH; ++e) {
+  for (int e = 0; e < E; ++e) {
     const int c = 64 * e + lane;
-    v[e] = c < n ? src[c] : 0.f;
-    key[e] = c < n ? ((uint64_t)order_key(v[e]) << 32) | (uint32_t)~c : 0ull;
-    key_lds[wave][c] = key[e];
+    key[e] = (e < NCH && c < n) ? ((uint64_t)order_key(src[c]) << 32) | (uint32_t)~c : 0ull;
+    if (e < NCH) keep_lds[wave][c] = 0;
   }
-  __builtin_amdgcn_wave_barrier();
-  // Rank = the number of larger keys; the value goes to its sorted slot.
-  int rank[NCH];
+  int rank[NCH];  // rank path: position of this lane's entry e in the order
+  if constexpr (kSort) {
+    // Bitonic network, descending. Element i = 64 e + lane of the padded row sits in
+    // register e of lane `lane`: partners in the same lane (i ^ j, j >= 64) are exchanged
+    // in registers, partners in other lanes (j < 64) through shuffles. Sorted position p
+    // then holds the p-th key, and the key gives back its value and column.
 #pragma unroll
-  for (int e = 0; e < NCH; ++e) rank[e] = 0;
-  for (int j0 = 0; j0 < n; j0 += 2) {  // two keys per 16-byte broadcast read
-    const uint4 k2 = *reinterpret_cast<const uint4*>(&key_lds[wave][j0]);
-    const uint64_t kq[2] = {((uint64_t)k2.y << 32) | k2.x, ((uint64_t)k2.w << 32) | k2.z};
+    for (int k = 2; k <= NSORT; k <<= 1) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        if (j >= 64) {
+          const int je = j >> 6;
 #pragma unroll
-      for (int e = 0; e < NCH; ++e) rank[e] += kq[t] > key[e];
+          for (int e = 0; e < E; ++e) {
+            if (e & je) continue;
+            // pair (i, i + j) in one lane; descending block when (i & k) == 0 (k > 64 here)
+            const bool desc = ((64 * e) & k) == 0;
+            const uint64_t x = key[e], y = key[e | je];
+            const bool first_x = (x > y) == desc;
+            key[e] = first_x ? x : y;
+            key[e | je] = first_x ? y : x;
+          }
+        } else {
+          const bool lower = (lane & j) == 0;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const bool desc = (((64 * e) | lane) & k) == 0;
+            const uint64_t x = key[e];
+            const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, j);
+            const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j);
+            const uint64_t y = ((uint64_t)yhi << 32) | ylo;
+            // the lower index of a descending pair (or the upper of an ascending one) takes
+            // the larger key
+            key[e] = (lower == desc) == (x > y) ? x : y;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int p = 64 * e + lane;
+      if (p < n) cum_lds[wave][p] = from_order_key((uint32_t)(key[e] >> 32));
+    }
+  } else {
+    // Rank = the number of larger keys; the value goes to its sorted slot.
+#pragma unroll
+    for (int e = 0; e < NCH; ++e) {
+      key_lds[wave][64 * e + lane] = key[e];
+      rank[e] = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int j0 = 0; j0 < n; j0 += 2) {  // two keys per 16-byte broadcast read
+      const uint4 k2 = *reinterpret_cast<const uint4*>(&key_lds[wave][j0]);
+      const uint64_t kq[2] = {((uint64_t)k2.y << 32) | k2.x, ((uint64_t)k2.w << 32) | k2.z};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < NCH; ++e) rank[e] += kq[t] > key[e];
+    }
+#pragma unroll
+    for (int e = 0; e < NCH; ++e)
+      if (64 * e + lane < n) cum_lds[wave][rank[e]] = from_order_key((uint32_t)(key[e] >> 32));
   }
-#pragma unroll
-  for (int e = 0; e < NCH; ++e)
-    if (64 * e + lane < n) cum_lds[wave][rank[e]] = v[e];
   __builtin_amdgcn_wave_barrier();
   // Sequential prefix sums in rank order (the fixed order the oracle repeats).
   if (lane == 0) {
@@ -309,6 +364,19 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
     if (!met60 && k0 < n) k = min(k * 3, n);
     if (!met90 && k0 < n) k = min(k / 3 * 2, n);
   }
+  // The first k of the order, by column.
+  if constexpr (kSort) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int p = 64 * e + lane;
+      if (p < n && p < k) keep_lds[wave][~(uint32_t)key[e]] = 1;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < NCH; ++e)
+      if (64 * e + lane < n && rank[e] < k) keep_lds[wave][64 * e + lane] = 1;
+  }
+  __builtin_amdgcn_wave_barrier();
   const int r = (int)(row % a.nqb);
   const bool text_row = r < a.n_text;
   int32_t* out = a.kv_idx + row * a.max_cnt;
@@ -317,7 +385,7 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   for (int e = 0; e < NCH; ++e) {
     const int c = 64 * e + lane;
     const bool valid = c < n;
-    const bool on = valid && (rank[e] < k || text_row || c < a.n_text);
+    const bool on = valid && (keep_lds[wave][c] != 0 || text_row || c < a.n_text);
     if (a.mask_out && valid) a.mask_out[row * n + c] = on ? 1 : 0;
     const uint64_t bal = __ballot(on);
     const int pre = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));

@@ -93,7 +93,7 @@ def test_sampled_block_scores_cogvideox_shape(dev):
 
 
 @pytest.mark.parametrize("mode", ["energy", "topk"])
-@pytest.mark.parametrize("nkb", [5, 64, 65, 278, 700])
+@pytest.mark.parametrize("nkb", [5, 64, 65, 278, 400, 700, 1024])
 def test_energy_lists_bit_exact(dev, mode, nkb):
     case(f"energy_kv_list mode={mode} nkb={nkb}")
     B, H, nqb = 2, 3, 9
