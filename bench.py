@@ -36,17 +36,21 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_fn(fn, iters=10, warmup=2):
+def time_fn(fn, iters=20, warmup=5):
+    """Median ms per call over `iters` back-to-back calls after `warmup` untimed ones; each
+    call is bracketed by its own HIP events on the current stream."""
     for _ in range(warmup):
         fn()
+    ev = [_events() for _ in range(iters)]
     torch.cuda.synchronize()
-    e0, e1 = _events()
-    e0.record()
-    for _ in range(iters):
+    for e0, e1 in ev:
+        e0.record()
         fn()
-    e1.record()
+        e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+    times = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    mid = len(times) // 2
+    return times[mid] if len(times) % 2 else 0.5 * (times[mid - 1] + times[mid])
 
 
 def load_traffic():
@@ -64,7 +68,9 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=30):
     and scales to the full call."""
     from oracle.attention import masked_attention
 
-    threads = torch.get_num_threads()
+    threads = _cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
     mask = kv.to_mask().cpu()
     B, H = q.shape[:2]
     heads = [(i % B, (7 * i) % H) for i in range(n_heads_sample)]
@@ -72,6 +78,7 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=30):
     t0 = time.perf_counter()
     masked_attention(qc, kc, vc, mask, sm_scale, dtype=torch.float32, heads=heads, row_chunk=1024)
     dt = time.perf_counter() - t0
+    torch.set_num_threads(prev)
     scale = (B * H) / len(heads)
     ms_full = dt * 1e3 * scale
     return {
@@ -79,6 +86,8 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=30):
         "unit": "TFLOP/s",
         "ms_per_call": round(ms_full, 1),
         "cores": threads,
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)),
         "kind": "port",
         "sample": f"{len(heads)} of {B * H} (b,h) heads of the C2 call, fp32 dense-masked, "
                   f"{dt:.1f} s, scaled x{scale:g}",
@@ -93,6 +102,7 @@ def _tflops(flops, ms):
 def other_configs(q, k, v, dev):
     """The other BASELINE configurations, each timed with HIP events (reported, not `value`)."""
     from sparseattnfunctions_amd import _tome
+    from sparseattnfunctions_amd._kv import kv_list_from_mask
     from sparseattnfunctions_amd.combined_attn import CombinedAttn
     from sparseattnfunctions_amd.MergeAttention import MergeAttention
     from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention, block_sparse_triton_fn
@@ -104,18 +114,18 @@ def other_configs(q, k, v, dev):
     # C1: the reference's CPU-runnable case (B=1, H=2, L=2048, random block mask), in bf16.
     q1, k1, v1, m1, s1 = config1_inputs()
     q1, k1, v1, m1 = (t.to(dev) for t in (q1.bfloat16(), k1.bfloat16(), v1.bfloat16(), m1))
-    ms = time_fn(lambda: block_sparse_triton_fn(q1, k1, v1, m1, s1), iters=20)
-    from oracle.attention import flops_of_mask
-    out["c1"] = {"ms": round(ms, 4), "tflops": _tflops(flops_of_mask(m1.cpu(), 2048, 2048), ms),
-                 "block_density": round(m1.float().mean().item(), 4)}
+    ms = time_fn(lambda: block_sparse_triton_fn(q1, k1, v1, m1, s1))
+    f1 = 4 * 64 * kv_list_from_mask(m1, 1, 2, 32, 32).computed_pairs(2048, 2048)
+    out["c1"] = {"ms": round(ms, 4), "tflops": _tflops(f1, ms), "block_density": round(m1.float().mean().item(), 4),
+                 "dtype": "bf16 (the fp32 inputs of the configuration rounded to bf16: the kernel takes bf16)"}
 
     # C3: combined mask (local window U global top-10% U text) + attention.
     proc = CombinedAttn(warmup_epoch=0)
     proc(q, k, v)
     kv3 = proc.last_kv
     f3 = 4 * D * kv3.computed_pairs(L, L)
-    ms3 = time_fn(lambda: proc(q, k, v), iters=10)
-    ms3_attn = time_fn(lambda: block_sparse_attention(q, k, v, kv3, 0.125, n_text_blocks=4), iters=10)
+    ms3 = time_fn(lambda: proc(q, k, v))
+    ms3_attn = time_fn(lambda: block_sparse_attention(q, k, v, kv3, 0.125, n_text_blocks=4))
     out["c3"] = {"ms": round(ms3, 4), "tflops": _tflops(f3, ms3), "attn_ms": round(ms3_attn, 4),
                  "attn_tflops": _tflops(f3, ms3_attn), "sparsity": round(proc.sparsity(), 4),
                  "effective_tflop_per_call": round(f3 / 1e12, 4)}
@@ -131,13 +141,13 @@ def other_configs(q, k, v, dev):
     kvs = sg.mask[0]
     thr = float(sg.energy_threshold_list[10])
     fs = 4 * D * kvs.computed_pairs(L, L)
-    ms_est = time_fn(lambda: calc_attn_block_sum_efficient(q, k, num_keep=8), iters=10)
+    ms_est = time_fn(lambda: calc_attn_block_sum_efficient(q, k, num_keep=8))
     pooled = calc_attn_block_sum_efficient(q, k, num_keep=8)
     ms_sel = time_fn(lambda: sgp.transfer_attn_to_kv_list(pooled, "energy", max_retain_ratio=sg.max_retain_ratio_list[10],
                                                           min_retain_ratio=sg.min_retain_ratio_list[10],
-                                                          energy_threshold=thr), iters=10)
-    ms_attn = time_fn(lambda: block_sparse_attention(q, k, v, kvs, 0.125, n_text_blocks=4), iters=10)
-    ms_sg = time_fn(lambda: sg.forward(q, k, v), iters=10)
+                                                          energy_threshold=thr))
+    ms_attn = time_fn(lambda: block_sparse_attention(q, k, v, kvs, 0.125, n_text_blocks=4))
+    ms_sg = time_fn(lambda: sg.forward(q, k, v))
     out["sparsegen_plus"] = {"ms": round(ms_sg, 4), "tflops": _tflops(fs, ms_sg), "estimator_ms": round(ms_est, 4),
                              "energy_lists_ms": round(ms_sel, 4), "attn_ms": round(ms_attn, 4),
                              "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
@@ -151,10 +161,10 @@ def other_configs(q, k, v, dev):
 
     nb = math.ceil(L / 64)
     f_dense = 4 * D * B * H * L * L
-    ms_pool = time_fn(lambda: attn_with_pooling(q, k, v, False, 0.125, 64), iters=5)
-    ms_pool_causal = time_fn(lambda: attn_with_pooling(q, k, v, True, 0.125, 64), iters=5)
+    ms_pool = time_fn(lambda: attn_with_pooling(q, k, v, False, 0.125, 64))
+    ms_pool_causal = time_fn(lambda: attn_with_pooling(q, k, v, True, 0.125, 64))
     kv_all = dense_kv_list(B, H, nb, nb, q.device)
-    ms_dense = time_fn(lambda: block_sparse_attention(q, k, v, kv_all, 0.125), iters=5)
+    ms_dense = time_fn(lambda: block_sparse_attention(q, k, v, kv_all, 0.125, n_text_blocks=4))
     out["attn_pooling"] = {"ms": round(ms_pool, 4), "tflops": _tflops(f_dense, ms_pool),
                            "dense_attention_ms": round(ms_dense, 4), "causal_ms": round(ms_pool_causal, 4),
                            "block_size": 64}
@@ -169,9 +179,9 @@ def other_configs(q, k, v, dev):
     q6, k6, v6 = (torch.randn(2, 48, g.L, 64, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3))
     pat = pa.ParternAttentionColVersion_V2()
     _, idx6 = pa.get_indexs(g)
-    ms_pat = time_fn(lambda: pat(q6, k6, v6, index_k=idx6), iters=3, warmup=1)
+    ms_pat = time_fn(lambda: pat(q6, k6, v6, index_k=idx6))
     draws = (torch.randperm(g.S)[: g.sample_num], pa.get_indexs(g)[1], pa.get_indexs(g)[1])
-    ms_judge = time_fn(lambda: pa.unified_judge(q6, k6, g, draws=draws), iters=3, warmup=1)
+    ms_judge = time_fn(lambda: pa.unified_judge(q6, k6, g, draws=draws))
     T, S, F = g.text_length, g.S, g.frames
     f_pat = 2 * 48 * 4 * 64 * (T * g.L + S * g.L + F * S * T + F * g.sample_num * (T + F * g.sample_num) + F * S * S)
     # The routed CombinedAttn body (combined_attn.py:42-101) on the same geometry. The frames of
@@ -185,7 +195,7 @@ def other_configs(q, k, v, dev):
     routed = CombinedAttn(warmup_epoch=0, head_routing=True)
     routed(q6, k6, v6)
     n_pattern_heads = int(routed.last_routing.sum().item())
-    ms_routed = time_fn(lambda: routed(q6, k6, v6), iters=3, warmup=1)
+    ms_routed = time_fn(lambda: routed(q6, k6, v6))
     out["pattern_1_5b"] = {"pattern_ms": round(ms_pat, 3), "pattern_tflops": _tflops(f_pat, ms_pat),
                            "unified_judge_ms": round(ms_judge, 3), "heads": 96, "L": g.L,
                            "routed_call_ms": round(ms_routed, 3), "routed_pattern_heads": n_pattern_heads}
@@ -200,8 +210,8 @@ def other_configs(q, k, v, dev):
     sta(q, k, v)
     lay = sta.block_mask
     f_sta = 4 * D * B * H * KVList(lay.kv_idx, lay.kv_cnt, 1, 1, lay.nb, lay.nb).computed_pairs(L, L)
-    ms_sta = time_fn(lambda: sta(q, k, v), iters=10)
-    ms_sta_copies = time_fn(lambda: sta.process_out_back(sta.attention(*sta.preprocess(q, k, v))), iters=10)
+    ms_sta = time_fn(lambda: sta(q, k, v))
+    ms_sta_copies = time_fn(lambda: sta.process_out_back(sta.attention(*sta.preprocess(q, k, v))))
     out["sta"] = {"ms": round(ms_sta, 4), "tflops": _tflops(f_sta, ms_sta), "copies_ms": round(ms_sta_copies, 4),
                   "block_density": round(lay.density(), 4), "block_tflop_per_call": round(f_sta / 1e12, 4)}
 
@@ -212,16 +222,18 @@ def other_configs(q, k, v, dev):
     maps = mp.maps
     Lm = maps.Lm
     f4 = 4 * B * H * Lm * Lm * D
-    ms4 = time_fn(lambda: mp(q4, k4, v4), iters=10)
-    ms_match = time_fn(lambda: mp.build_maps(k4, v4), iters=10)
-    ms_merge = time_fn(lambda: [_tome.merge(x, maps, H) for x in (q4, k4, v4)], iters=10)
+    ms4 = time_fn(lambda: mp(q4, k4, v4))
+    ms_match = time_fn(lambda: mp.build_maps(k4, v4))
+    ms_merge = time_fn(lambda: _tome.merge_many((q4, k4, v4), maps, H))
+    ms_merge3 = time_fn(lambda: [_tome.merge(x, maps, H) for x in (q4, k4, v4)])
     qm = _tome.merge(q4, maps, H)
-    ms_unmerge = time_fn(lambda: _tome.unmerge(qm, maps, H), iters=10)
+    ms_unmerge = time_fn(lambda: _tome.unmerge(qm, maps, H))
     row = D * 2
     merge_bytes = 3 * (B * H * L * row + B * H * Lm * row)
     unmerge_bytes = B * H * Lm * row + B * H * L * row
     out["c4"] = {"ms": round(ms4, 4), "tflops": _tflops(f4, ms4), "merged_tokens": Lm,
                  "match_ms": round(ms_match, 4), "merge_qkv_ms": round(ms_merge, 4),
+                 "merge_qkv_three_launches_ms": round(ms_merge3, 4),
                  "merge_gbs": round(merge_bytes / (ms_merge * 1e-3) / 1e9, 1),
                  "unmerge_ms": round(ms_unmerge, 4),
                  "unmerge_gbs": round(unmerge_bytes / (ms_unmerge * 1e-3) / 1e9, 1),
@@ -229,8 +241,12 @@ def other_configs(q, k, v, dev):
     del q4, k4, v4, qm
 
     # C5: one denoising step = 30 layers of config-3 attention, each with its own inputs
-    # (seed = layer index, drawn on the GPU generator).
-    layers = [cogvideox_qkv(i, device=str(dev)) for i in range(30)]
+    # drawn as config 2 with seed = layer index (CPU generator; drawn in a thread pool and
+    # moved to the GPU before the timed region).
+    from concurrent.futures import ThreadPoolExecutor
+
+    with ThreadPoolExecutor(max(1, min(8, _cpu_threads()))) as ex:
+        layers = list(ex.map(lambda i: tuple(t.to(dev) for t in cogvideox_qkv(i)), range(30)))
     procs = [CombinedAttn(warmup_epoch=0) for _ in range(30)]
     for p, (a, b_, c) in zip(procs, layers):
         p(a, b_, c)
@@ -240,22 +256,37 @@ def other_configs(q, k, v, dev):
         for p, (a, b_, c) in zip(procs, layers):
             p(a, b_, c)
 
-    ms5 = time_fn(step, iters=3, warmup=1)
+    ms5 = time_fn(step)
     out["c5"] = {"ms_per_step": round(ms5, 3), "tflops": _tflops(f5, ms5),
                  "effective_tflop_per_step": round(f5 / 1e12, 3)}
     del layers
     return out
 
 
+def _cpu_threads():
+    """CPUs this process may run on (os.sched_getaffinity), capped by OMP_NUM_THREADS when
+    the environment sets it (the GPU box's CPU share)."""
+    n = len(os.sched_getaffinity(0)) or os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(omp))) if omp.isdigit() and int(omp) > 0 else n
+
+
 def _cpu_model():
+    """Model name plus family/model/stepping from /proc/cpuinfo (some hosts report only the
+    brand in the model name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break
+                key, _, val = line.partition(":")
+                info[key.strip()] = val.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    detail = ", ".join(f"{k} {info[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in info)
+    return f"{name} ({detail})" if detail else name
 
 
 def main():
@@ -327,6 +358,24 @@ def main():
     ms = g0.elapsed_time(g1) / args.steps
     attn_kernel_ms = sum(a.elapsed_time(b) for a, b in attn_ms) / len(attn_ms)
 
+    # Dense comparators, right after the timed steps (same warm GPU): torch SDPA and this
+    # kernel over a prebuilt all-blocks list.
+    dense = None
+    if not args.no_extra:
+        from sparseattnfunctions_amd.block_mask_attn import dense_kv_list
+
+        kv_all = dense_kv_list(B, H, geom.nb, geom.nb, dev)
+        dense_hip_ms = time_fn(lambda: block_sparse_attention(q, k, v, kv_all, proc.sm_scale,
+                                                              n_text_blocks=geom.n_text_blocks))
+        dense_sdpa_ms = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v))
+        dense = {
+            "torch_sdpa_ms": round(dense_sdpa_ms, 3),
+            "hip_all_blocks_ms": round(dense_hip_ms, 3),
+            "speedup_vs_torch_sdpa": round(dense_sdpa_ms / ms, 3),
+            "speedup_vs_hip_dense": round(dense_hip_ms / ms, 3),
+        }
+        del kv_all
+
     result = {
         "metric": METRIC,
         "value": round(eff_flops / (ms * 1e-3) / 1e12, 3),
@@ -368,16 +417,10 @@ def main():
         torch.cuda.synchronize()
         result["copy_calibration_bytes"] = src.numel() * src.element_size()
         del src, dst
+    if dense is not None:
+        result["dense"] = dense
     if not args.no_extra:
         result["other_configs"] = other_configs(q, k, v, dev)
-        dense_sdpa_ms = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v), iters=5)
-        dense_hip_ms = time_fn(lambda: proc.forward_dense(q, k, v), iters=3)
-        result["dense"] = {
-            "torch_sdpa_ms": round(dense_sdpa_ms, 3),
-            "hip_all_blocks_ms": round(dense_hip_ms, 3),
-            "speedup_vs_torch_sdpa": round(dense_sdpa_ms / ms, 3),
-            "speedup_vs_hip_dense": round(dense_hip_ms / ms, 3),
-        }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q, k, v, kv, proc.sm_scale, eff_flops)
     print(json.dumps(result), flush=True)

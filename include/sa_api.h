@@ -36,7 +36,7 @@ extern "C" {
 #define SA_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim != 64) */
 #define SA_ERR_HIP (-3)         /* a HIP runtime call failed (launch, device query) */
 
-#define SA_ABI_VERSION 1
+#define SA_ABI_VERSION 2
 
 /* Version of this ABI (SA_ABI_VERSION). */
 int sa_abi_version(void);
@@ -234,6 +234,12 @@ int sa_sampled_block_scores(const uint16_t* q_sampled, const uint16_t* k_sampled
  *             (:57-73: the crossing column itself is not kept before clamping);
  *   mode 1 ("topk"): k = init_k; if cum[init_k-1] < 0.6*total and init_k < n, k = min(3k, n);
  *             then if cum[init_k-1] < 0.9*total and init_k < n, k = min(k/3*2, n) (:31-46);
+ *   mode 2 ("inclusive"): k = 1 + the first j with cum[j] >= threshold*total (k = n when
+ *             none), then clamped to [min_keep, max_keep]: the frame-scope and row-scope
+ *             energy cuts of generate_attention_mask_frame_scope / get_inner_frame_mask
+ *             (utils/mask_related.py:224-232, 366-376: crossing column kept, last forced);
+ *   mode 3 ("cumulative <="): the ranks j with cum[j] <= threshold*total, plus rank n-1
+ *             (the head-scope cut of get_inner_frame_mask, utils/mask_related.py:378-391);
  * united with columns < n_text_blocks and every column of rows < n_text_blocks (:81-82).
  *   scores    fp32 [BH][nqb][nkb], nkb <= 1024; kv_idx int32 [BH*nqb][max_cnt >= nkb],
  *             kv_cnt int32 [BH*nqb]; mask_out nullable uint8 [BH][nqb][nkb].
@@ -412,6 +418,8 @@ typedef struct sa_tome_maps {
   int32_t* members;      /* [G][r] edge positions grouped by dst, ascending */
   int32_t* row_of_token; /* [G][L] merged row holding each token (the unmerge map, :137-154) */
   float* key_bias;       /* [G][Lm] log(size) rounded to bf16, 0 for text/unm (MergeAttention.py:163-167) */
+  int32_t* merged_src;   /* [G][Lm] token row that merged row j starts from: text j, unm its token, dst the dst token */
+  int32_t* member_rows;  /* [G][r] token row of each entry of members (the flat gather list of the dst means) */
 } sa_tome_maps;
 
 /*
@@ -461,6 +469,16 @@ int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspac
 int sa_tome_merge(const uint16_t* x, const int64_t x_strides[3], int B, int H, int D,
                   int heads_per_group, const sa_tome_maps* maps, uint16_t* out,
                   const int64_t out_strides[3], void* stream);
+
+/*
+ * The merge closure applied to n (1..3) tensors of the same [B,H,L,64] shape in one launch,
+ * as MergeAttention merges q, k and v with one set of maps (MergeAttention.py:33-38; the
+ * merges of merge_unmerge.py:119-128): out[i] = merge(x[i]), each exactly as sa_tome_merge.
+ * x_strides / out_strides hold n consecutive {stride_b, stride_h, stride_l} triples.
+ */
+int sa_tome_merge_multi(int n, const uint16_t* const* x, const int64_t* x_strides, int B, int H, int D,
+                        int heads_per_group, const sa_tome_maps* maps, uint16_t* const* out,
+                        const int64_t* out_strides, void* stream);
 
 /* unmerge closure (merge_unmerge.py:137-154): out[b,h,t] = xm[b,h,row_of_token[t]]. */
 int sa_tome_unmerge(const uint16_t* xm, const int64_t xm_strides[3], int B, int H, int D,

@@ -25,7 +25,7 @@ def expand_block_mask(block_mask: torch.Tensor, Lq: int, Lk: int, block: int = 6
 
 
 def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 64,
-                     dtype=torch.float64, row_chunk: int = 2048, heads=None, token_mask=None):
+                     dtype=torch.float64, row_chunk: int = 2048, heads=None, token_mask=None, rows=None):
     """Dense-masked attention on CPU tensors; returns [B, H, Lq, D] in `dtype`.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] (any float dtype; converted to `dtype`);
@@ -34,6 +34,8 @@ def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 
     computation to a list of (b, h) pairs (the rest of the output stays zero).
     `token_mask(rows)` optionally returns a bool [len(rows), Lk] token-level mask that is
     intersected with the block mask (flex_attention's mask_mod semantics).
+    `rows` (int64 [n], ascending query indices) computes only those query rows and returns
+    [B, H, n, D]; every row is computed as in the full call.
     """
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
@@ -41,7 +43,8 @@ def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 
     nkb = -(-Lk // block)
     bm = block_mask.to(torch.bool)
     bm = bm.expand(B, H, bm.shape[-2], bm.shape[-1])[..., :nqb, :nkb]
-    out = torch.zeros(B, H, Lq, D, dtype=dtype)
+    sel = torch.arange(Lq) if rows is None else rows.to(torch.int64)
+    out = torch.zeros(B, H, sel.numel(), D, dtype=dtype)
     pairs = heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]
     for b, h in pairs:
         kk = k[b, h].to(dtype)
@@ -49,16 +52,16 @@ def masked_attention(q, k, v, block_mask, sm_scale, key_bias=None, block: int = 
         bias = None
         if key_bias is not None:
             bias = key_bias.expand(B, H, Lk)[b, h].to(dtype)
-        for r0 in range(0, Lq, row_chunk):
-            r1 = min(Lq, r0 + row_chunk)
-            qq = q[b, h, r0:r1].to(dtype)
+        for r0 in range(0, sel.numel(), row_chunk):
+            r1 = min(sel.numel(), r0 + row_chunk)
+            ridx = sel[r0:r1]
+            qq = q[b, h, ridx].to(dtype)
             s = (qq @ kk.T) * sm_scale
             if bias is not None:
                 s = s + bias[None, :]
-            rows = torch.arange(r0, r1) // block
-            allowed = bm[b, h][rows].repeat_interleave(block, dim=-1)[:, :Lk]
+            allowed = bm[b, h][ridx // block].repeat_interleave(block, dim=-1)[:, :Lk]
             if token_mask is not None:
-                allowed = allowed & token_mask(torch.arange(r0, r1))
+                allowed = allowed & token_mask(ridx)
             s = s.masked_fill(~allowed, float("-inf"))
             empty = ~allowed.any(dim=-1)
             s[empty] = 0.0

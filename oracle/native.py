@@ -181,6 +181,27 @@ def tome_argmax(metric, a_subset, b_idx):
     return idx, mx
 
 
+def tome_argmax_all(metric, a_idx, b_idx, threads: int = 0):
+    """(node_idx, node_max) [G, n_src] for every src: `oracle_tome_argmax` on contiguous
+    slices of the srcs in a thread pool (ctypes releases the GIL during the call; every src
+    is computed independently, so the result does not depend on the split)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    lib()  # load once, before the threads call it
+    G = metric.shape[0]
+    n = a_idx.numel()
+    metric = metric.contiguous()
+    b_idx = b_idx.contiguous()
+    nt = max(1, min(threads or (os.cpu_count() or 1), 32))
+    bounds = [n * i // nt for i in range(nt + 1)]
+    parts = [(bounds[i], bounds[i + 1]) for i in range(nt) if bounds[i + 1] > bounds[i]]
+    with ThreadPoolExecutor(len(parts)) as ex:
+        res = list(ex.map(lambda p: tome_argmax(metric, a_idx[p[0]:p[1]].contiguous(), b_idx), parts))
+    idx = torch.cat([r[0] for r in res], dim=1) if res else torch.empty(G, 0, dtype=torch.int32)
+    mx = torch.cat([r[1] for r in res], dim=1) if res else torch.empty(G, 0)
+    return idx, mx
+
+
 def tome_maps(node_max, node_idx, N, a_idx, b_idx, r: int, text_len: int):
     """Maps from given node_max/node_idx [G, n_src] (same dict as tome_match)."""
     G = node_max.shape[0]

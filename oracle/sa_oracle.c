@@ -119,6 +119,11 @@ void oracle_block_topk(const float* qp, const float* kp, const float* scores_in,
  *          clamped to [min_keep, max_keep]; keep the first k sorted columns;
  *   mode 1 "topk" (:28-50): k0 = init_k, e = cum[k0-1]; if e < 0.6*total and k0 < n:
  *          k = min(3*k0, n); if e < 0.9*total and k0 < n: k = min(k/3*2, n);
+ *   mode 2 "inclusive" (mask_related.py:224-232, 366-376): j = first position with
+ *          cum[j] >= thr*total (n-1 if none: the last position is forced on), keep the first
+ *          j+1 sorted columns, then clamped to [min_keep, max_keep];
+ *   mode 3 "cumulative <=" (mask_related.py:378-391): keep every sorted position j with
+ *          cum[j] <= thr*total, and the last sorted position;
  * then text rows/columns (< n_text) forced on (:81-82); ascending kv lists and 0/1 mask.
  */
 void oracle_energy_list(const float* scores, int BH, int nqb, int nkb, int mode, float thr, int min_keep,
@@ -153,6 +158,21 @@ void oracle_energy_list(const float* scores, int BH, int nqb, int nkb, int mode,
       k = total < target ? n : first;
       if (k < min_keep) k = min_keep;
       if (k > max_keep) k = max_keep;
+    } else if (mode == 2) {
+      const float target = thr * total;
+      int first = n - 1;
+      for (int j = 0; j < n; ++j)
+        if (cum[j] >= target) {
+          first = j;
+          break;
+        }
+      k = first + 1;
+      if (k < min_keep) k = min_keep;
+      if (k > max_keep) k = max_keep;
+    } else if (mode == 3) {
+      const float target = thr * total;
+      k = 0;
+      while (k < n && cum[k] <= target) ++k;
     } else {
       const int k0 = init_k;
       const float e = cum[k0 - 1];
@@ -162,6 +182,7 @@ void oracle_energy_list(const float* scores, int BH, int nqb, int nkb, int mode,
     }
     memset(keep, 0, (size_t)n);
     for (int j = 0; j < k && j < n; ++j) keep[keys[j].idx] = 1;
+    if (mode == 3) keep[keys[n - 1].idx] = 1;
     const int r = (int)(row % nqb);
     int cnt = 0;
     for (int c = 0; c < n; ++c) {

@@ -84,13 +84,12 @@ class MergeAttention:
         bias = maps.key_bias.reshape(B, H // hpg, maps.Lm).expand(B, H, maps.Lm) if hpg == H else \
             maps.key_bias.reshape(B, H, maps.Lm)
         scale = self.sm_scale if self.sm_scale is not None else 1.0 / math.sqrt(D)
-        km = _tome.merge(k, maps, hpg)
-        vm = _tome.merge(v, maps, hpg)
         if self.full_merge:
-            qm = _tome.merge(q, maps, hpg)
+            qm, km, vm = _tome.merge_many((q, k, v), maps, hpg)
             om = block_sparse_attention(qm, km, vm, self._dense(B, H, maps.Lm, maps.Lm, q.device), scale,
                                         key_bias=bias)
             return _tome.unmerge(om, maps, hpg)
+        km, vm = _tome.merge_many((k, v), maps, hpg)
         return block_sparse_attention(q, km, vm, self._dense(B, H, L, maps.Lm, q.device), scale, key_bias=bias)
 
     def __call__(self, *args, **kwds):

@@ -21,7 +21,7 @@ class _MapsStruct(ctypes.Structure):
     _fields_ = [(n, _I) for n in ("G", "N", "text_len", "n_src", "n_dst", "r", "L", "Lm")] + [
         (n, _P)
         for n in ("a_idx", "b_idx", "node_idx", "node_max", "rank", "edge", "dst_idx", "dst_cnt", "dst_cursor",
-                  "dst_ptr", "members", "row_of_token", "key_bias")
+                  "dst_ptr", "members", "row_of_token", "key_bias", "merged_src", "member_rows")
     ]
 
 
@@ -107,10 +107,12 @@ class TomeMaps:
         self.members = torch.empty(G, max(r, 1), **i32)
         self.row_of_token = torch.empty(G, L, **i32)
         self.key_bias = torch.empty(G, L - r, dtype=torch.float32, device=device)
+        self.merged_src = torch.empty(G, L - r, **i32)
+        self.member_rows = torch.empty(G, max(r, 1), **i32)
         self.struct = _MapsStruct(G, N, text_len, ns, nd, r, L, L - r, *[
             t.data_ptr() for t in (a_idx, b_idx, self.node_idx, self.node_max, self.rank, self.edge, self.dst_idx,
                                    self.dst_cnt, self.dst_cursor, self.dst_ptr, self.members, self.row_of_token,
-                                   self.key_bias)])
+                                   self.key_bias, self.merged_src, self.member_rows)])
 
     @property
     def sizes(self) -> torch.Tensor:
@@ -157,6 +159,32 @@ def merge(x: torch.Tensor, maps: TomeMaps, heads_per_group: int, out=None) -> to
     if x.shape[2] != maps.L:
         raise ValueError(f"merge: tensor has {x.shape[2]} tokens, maps expect {maps.L}")
     return _apply("sa_tome_merge", x, maps, heads_per_group, maps.Lm, out)
+
+
+def merge_many(xs, maps: TomeMaps, heads_per_group: int):
+    """merge() of up to three [B, H, L, 64] tensors with one set of maps in one launch
+    (`sa_tome_merge_multi`); returns the merged tensors in order."""
+    xs = [_bf16(x) for x in xs]
+    if not 1 <= len(xs) <= 3:
+        raise ValueError("merge_many takes 1 to 3 tensors")
+    _lib.require_gpu(*xs)
+    B, H, L, D = xs[0].shape
+    for x in xs:
+        if tuple(x.shape) != (B, H, L, D) or x.device != xs[0].device:
+            raise ValueError("merge_many: tensors must share shape and device")
+    if L != maps.L:
+        raise ValueError(f"merge: tensor has {L} tokens, maps expect {maps.L}")
+    outs = [torch.empty(B, H, maps.Lm, D, dtype=x.dtype, device=x.device) for x in xs]
+    n = len(xs)
+    xp = (ctypes.c_void_p * n)(*[x.data_ptr() for x in xs])
+    op = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    xst = _lib.i64(*[s for x in xs for s in x.stride()[:3]])
+    ost = _lib.i64(*[s for o in outs for s in o.stride()[:3]])
+    with torch.cuda.device(xs[0].device):
+        rc = _lib.load().sa_tome_merge_multi(n, xp, xst, B, H, D, heads_per_group, ctypes.byref(maps.struct), op, ost,
+                                             _lib.stream_of(xs[0]))
+    _lib.check(rc, "sa_tome_merge_multi")
+    return outs
 
 
 def unmerge(xm: torch.Tensor, maps: TomeMaps, heads_per_group: int, out=None) -> torch.Tensor:

@@ -353,6 +353,27 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
     }
     k = total < target ? n : first;
     k = min(max(k, a.min_keep), a.max_keep);
+  } else if (a.mode == 2 || a.mode == 3) {
+    // "inclusive" (2): through the first position whose cumulative energy reaches
+    // threshold * total (the last position when none does), then [min, max].
+    // "cumulative <=" (3): the positions whose cumulative energy stays <= threshold * total
+    // (a prefix: the sums do not decrease), plus the last position (added below).
+    const float target = a.threshold * total;
+    int first = n;
+#pragma unroll
+    for (int e = NCH - 1; e >= 0; --e) {
+      const int c = 64 * e + lane;
+      const float cv = c < n ? cum_lds[wave][c] : 0.f;
+      const bool hit_c = c < n && (a.mode == 2 ? cv >= target : !(cv <= target));
+      const uint64_t hit = __ballot(hit_c);
+      if (hit) first = 64 * e + __builtin_ctzll(hit);
+    }
+    if (a.mode == 2) {
+      k = (first < n ? first : n - 1) + 1;
+      k = min(max(k, a.min_keep), a.max_keep);
+    } else {
+      k = first;
+    }
   } else {
     // "topk": start from init_k; below 60 % of the energy triple it, then (below 90 %)
     // take two thirds of the result, both capped at n.
@@ -369,12 +390,12 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int p = 64 * e + lane;
-      if (p < n && p < k) keep_lds[wave][~(uint32_t)key[e]] = 1;
+      if (p < n && (p < k || (a.mode == 3 && p == n - 1))) keep_lds[wave][~(uint32_t)key[e]] = 1;
     }
   } else {
 #pragma unroll
     for (int e = 0; e < NCH; ++e)
-      if (64 * e + lane < n && rank[e] < k) keep_lds[wave][64 * e + lane] = 1;
+      if (64 * e + lane < n && (rank[e] < k || (a.mode == 3 && rank[e] == n - 1))) keep_lds[wave][64 * e + lane] = 1;
   }
   __builtin_amdgcn_wave_barrier();
   const int r = (int)(row % a.nqb);
@@ -464,7 +485,8 @@ extern "C" int sa_energy_kv_list(const float* scores, int BH, int nqb, int nkb, 
                                  int max_cnt, int32_t* kv_cnt, uint8_t* mask_out, void* stream) {
   SA_REQUIRE(scores && kv_idx && kv_cnt, "sa_energy_kv_list: null pointer");
   SA_REQUIRE(BH > 0 && nqb > 0 && nkb > 0, "sa_energy_kv_list: bad shape BH=%d nqb=%d nkb=%d", BH, nqb, nkb);
-  SA_REQUIRE(mode == 0 || mode == 1, "sa_energy_kv_list: mode %d (0 = energy, 1 = topk)", mode);
+  SA_REQUIRE(mode >= 0 && mode <= 3, "sa_energy_kv_list: mode %d (0 energy, 1 topk, 2 inclusive, 3 cumulative <=)",
+             mode);
   SA_REQUIRE(n_text_blocks >= 0, "sa_energy_kv_list: negative n_text_blocks");
   SA_REQUIRE(max_cnt >= nkb, "sa_energy_kv_list: max_cnt=%d < nkb=%d", max_cnt, nkb);
   if (mode == 1) SA_REQUIRE(init_k >= 1 && init_k <= nkb, "sa_energy_kv_list: init_k=%d outside [1, %d]", init_k, nkb);

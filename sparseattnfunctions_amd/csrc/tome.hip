@@ -326,7 +326,8 @@ __global__ void edge_kernel(sa_tome_maps m) {
   m.edge[g * m.n_src + m.rank[i]] = (int32_t)(i - g * m.n_src);
 }
 
-// dst_idx, dst counts and the unmerge map for every token.
+// dst_idx, dst counts, the unmerge map for every token and the source row of every
+// merged row (merged_src).
 __global__ void assign_kernel(sa_tome_maps m) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)m.G * m.L) return;
@@ -334,8 +335,10 @@ __global__ void assign_kernel(sa_tome_maps m) {
   const int t = (int)(i - g * m.L);
   const int T = m.text_len, U = m.n_src - m.r;
   int32_t* rot = m.row_of_token + g * m.L;
+  int32_t* msrc = m.merged_src + g * m.Lm;
   if (t < T) {
     rot[t] = t;
+    msrc[t] = t;
   } else if (t < T + m.n_src) {  // edge position e = t - T
     const int e = t - T;
     const int s = m.edge[g * m.n_src + e];
@@ -347,10 +350,12 @@ __global__ void assign_kernel(sa_tome_maps m) {
       rot[tok] = T + U + d;
     } else {
       rot[tok] = T + (e - m.r);
+      msrc[T + (e - m.r)] = tok;
     }
   } else if (t < T + m.n_src + m.n_dst) {
     const int d = t - T - m.n_src;
     rot[T + m.b_idx[d]] = T + U + d;
+    msrc[T + U + d] = T + m.b_idx[d];
   }
 }
 
@@ -399,7 +404,8 @@ __global__ void fill_kernel(sa_tome_maps m) {
   m.members[g * m.r + m.dst_ptr[g * (m.n_dst + 1) + d] + p] = e;
 }
 
-// Members of each dst in ascending edge order (insertion sort of its short segment).
+// Members of each dst in ascending edge order (insertion sort of its short segment), then
+// the token row of each member (member_rows): the merge reads one index per member.
 __global__ void sort_kernel(sa_tome_maps m) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)m.G * m.n_dst) return;
@@ -417,20 +423,35 @@ __global__ void sort_kernel(sa_tome_maps m) {
     }
     mem[y + 1] = v;
   }
+  const int32_t* edge = m.edge + g * m.n_src;
+  int32_t* rows = m.member_rows + g * m.r;
+  for (int x = lo; x < hi; ++x) rows[x] = m.text_len + m.a_idx[edge[mem[x]]];
 }
 
 // ---------------------------------------------------------------------------------------
-// Merge: out[b, h, j] = mean of the tokens of merged row j. 8 lanes per row (16 B each).
+// Merge: out[b, h, j] = mean of the tokens of merged row j, for up to three tensors that
+// share the maps (q, k, v). 8 lanes per row (16 B each). Row j reads merged_src[j]; a dst
+// row with merged srcs then reads its member rows from the flat member_rows list, four
+// members' loads in flight at a time, and adds them in edge order after the dst token.
+constexpr int kMergeMax = 3;
+
 struct MergeArgs {
   sa_tome_maps m;
-  const uint16_t* x;
-  int64_t x_sb, x_sh, x_sl;
-  uint16_t* out;
-  int64_t o_sb, o_sh, o_sl;
+  const uint16_t* x[kMergeMax];
+  int64_t x_sb[kMergeMax], x_sh[kMergeMax], x_sl[kMergeMax];
+  uint16_t* out[kMergeMax];
+  int64_t o_sb[kMergeMax], o_sh[kMergeMax], o_sl[kMergeMax];
   int B, H, heads_per_group;
 };
 
+__device__ inline void add_u4(float* s, uint4 w) {
+  s[0] += bf16lo(w.x); s[1] += bf16hi(w.x); s[2] += bf16lo(w.y); s[3] += bf16hi(w.y);
+  s[4] += bf16lo(w.z); s[5] += bf16hi(w.z); s[6] += bf16lo(w.w); s[7] += bf16hi(w.w);
+}
+
+template <int kN>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  constexpr int kU = 4;  // member loads in flight
   const sa_tome_maps& m = a.m;
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
   const int c8 = threadIdx.x & 7;
@@ -439,41 +460,66 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int j = (int)(row - bh * m.Lm);
   const int64_t b = bh / a.H, h = bh - b * a.H;
   const int64_t g = bh / a.heads_per_group;
-  const int T = m.text_len, U = m.n_src - m.r;
-  const uint16_t* xb = a.x + b * a.x_sb + h * a.x_sh + 8 * c8;
-  uint4 res;
-  if (j < T + U) {
-    const int tok = j < T ? j : T + m.a_idx[m.edge[g * m.n_src + m.r + (j - T)]];
-    res = *reinterpret_cast<const uint4*>(xb + (int64_t)tok * a.x_sl);
+  const int d0 = m.text_len + m.n_src - m.r;  // first dst row
+  const int src = m.merged_src[g * m.Lm + j];
+  int lo = 0, hi = 0;
+  if (j >= d0) {
+    const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1) + (j - d0);
+    lo = ptr[0];
+    hi = ptr[1];
+  }
+  const uint16_t* xb[kN];
+  uint4 w0[kN];
+#pragma unroll
+  for (int t = 0; t < kN; ++t) {
+    xb[t] = a.x[t] + b * a.x_sb[t] + h * a.x_sh[t] + 8 * c8;
+    w0[t] = *reinterpret_cast<const uint4*>(xb[t] + (int64_t)src * a.x_sl[t]);
+  }
+  uint4 res[kN];
+  if (lo == hi) {
+#pragma unroll
+    for (int t = 0; t < kN; ++t) res[t] = w0[t];
   } else {
-    const int d = j - T - U;
-    const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1);
-    const int lo = ptr[d], hi = ptr[d + 1];
-    const uint4 w0 = *reinterpret_cast<const uint4*>(xb + (int64_t)(T + m.b_idx[d]) * a.x_sl);
-    if (lo == hi) {
-      res = w0;
-    } else {
-      float s[8] = {bf16lo(w0.x), bf16hi(w0.x), bf16lo(w0.y), bf16hi(w0.y),
-                    bf16lo(w0.z), bf16hi(w0.z), bf16lo(w0.w), bf16hi(w0.w)};
-      for (int p = lo; p < hi; ++p) {
-        const int e = m.members[g * m.r + p];
-        const int tok = T + m.a_idx[m.edge[g * m.n_src + e]];
-        const uint4 w = *reinterpret_cast<const uint4*>(xb + (int64_t)tok * a.x_sl);
-        s[0] += bf16lo(w.x); s[1] += bf16hi(w.x); s[2] += bf16lo(w.y); s[3] += bf16hi(w.y);
-        s[4] += bf16lo(w.z); s[5] += bf16hi(w.z); s[6] += bf16lo(w.w); s[7] += bf16hi(w.w);
-      }
-      const float n = (float)(1 + hi - lo);
+    float s[kN][8];
+#pragma unroll
+    for (int t = 0; t < kN; ++t) {
+      const uint4 w = w0[t];
+      s[t][0] = bf16lo(w.x); s[t][1] = bf16hi(w.x); s[t][2] = bf16lo(w.y); s[t][3] = bf16hi(w.y);
+      s[t][4] = bf16lo(w.z); s[t][5] = bf16hi(w.z); s[t][6] = bf16lo(w.w); s[t][7] = bf16hi(w.w);
+    }
+    const int32_t* mr = m.member_rows + g * m.r;
+    for (int p = lo; p < hi; p += kU) {
+      int rr[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) rr[u] = mr[min(p + u, hi - 1)];  // clamped: always a member
+      uint4 w[kU][kN];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int t = 0; t < kN; ++t) w[u][t] = *reinterpret_cast<const uint4*>(xb[t] + (int64_t)rr[u] * a.x_sl[t]);
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (p + u < hi) {
+#pragma unroll
+          for (int t = 0; t < kN; ++t) add_u4(s[t], w[u][t]);
+        }
+    }
+    const float n = (float)(1 + hi - lo);
+#pragma unroll
+    for (int t = 0; t < kN; ++t) {
       uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t lo16 = __float_as_uint(round_bf16(s[2 * q] / n)) >> 16;
-        const uint32_t hi16 = __float_as_uint(round_bf16(s[2 * q + 1] / n)) & 0xffff0000u;
+        const uint32_t lo16 = __float_as_uint(round_bf16(s[t][2 * q] / n)) >> 16;
+        const uint32_t hi16 = __float_as_uint(round_bf16(s[t][2 * q + 1] / n)) & 0xffff0000u;
         o[q] = lo16 | hi16;
       }
-      res = make_uint4(o[0], o[1], o[2], o[3]);
+      res[t] = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
-  *reinterpret_cast<uint4*>(a.out + b * a.o_sb + h * a.o_sh + (int64_t)j * a.o_sl + 8 * c8) = res;
+#pragma unroll
+  for (int t = 0; t < kN; ++t)
+    *reinterpret_cast<uint4*>(a.out[t] + b * a.o_sb[t] + h * a.o_sh[t] + (int64_t)j * a.o_sl[t] + 8 * c8) = res[t];
 }
 
 // Unmerge: out[b, h, t] = xm[b, h, row_of_token[t]].
@@ -487,8 +533,9 @@ __global__ __launch_bounds__(256) void unmerge_kernel(MergeArgs a) {
   const int64_t b = bh / a.H, h = bh - b * a.H;
   const int64_t g = bh / a.heads_per_group;
   const int src_row = m.row_of_token[g * m.L + t];
-  const uint4 w = *reinterpret_cast<const uint4*>(a.x + b * a.x_sb + h * a.x_sh + (int64_t)src_row * a.x_sl + 8 * c8);
-  *reinterpret_cast<uint4*>(a.out + b * a.o_sb + h * a.o_sh + (int64_t)t * a.o_sl + 8 * c8) = w;
+  const uint4 w =
+      *reinterpret_cast<const uint4*>(a.x[0] + b * a.x_sb[0] + h * a.x_sh[0] + (int64_t)src_row * a.x_sl[0] + 8 * c8);
+  *reinterpret_cast<uint4*>(a.out[0] + b * a.o_sb[0] + h * a.o_sh[0] + (int64_t)t * a.o_sl[0] + 8 * c8) = w;
 }
 
 int check_maps(const sa_tome_maps* m, const char* fn) {
@@ -498,7 +545,8 @@ int check_maps(const sa_tome_maps* m, const char* fn) {
                  m->Lm == m->L - m->r,
              "%s: inconsistent map sizes", fn);
   SA_REQUIRE(m->a_idx && m->b_idx && m->node_idx && m->node_max && m->rank && m->edge && m->dst_cnt &&
-                 m->dst_cursor && m->dst_ptr && m->row_of_token && m->key_bias && (m->r == 0 || (m->dst_idx && m->members)),
+                 m->dst_cursor && m->dst_ptr && m->row_of_token && m->key_bias && m->merged_src &&
+                 (m->r == 0 || (m->dst_idx && m->members && m->member_rows)),
              "%s: null map buffer", fn);
   return SA_OK;
 }
@@ -620,43 +668,61 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
 }
 
 namespace {
-int launch_merge(bool unmerge, const uint16_t* x, const int64_t xs[3], int B, int H, int D, int heads_per_group,
-                 const sa_tome_maps* maps, uint16_t* out, const int64_t os[3], void* stream) {
-  const char* fn = unmerge ? "sa_tome_unmerge" : "sa_tome_merge";
+int launch_merge(bool unmerge, int n, const uint16_t* const* x, const int64_t* xs, int B, int H, int D,
+                 int heads_per_group, const sa_tome_maps* maps, uint16_t* const* out, const int64_t* os,
+                 void* stream, const char* fn) {
   int rc = check_maps(maps, fn);
   if (rc) return rc;
+  SA_REQUIRE(n >= 1 && n <= (unmerge ? 1 : kMergeMax), "%s: %d tensors (1..%d)", fn, n, unmerge ? 1 : kMergeMax);
   SA_REQUIRE(x && xs && out && os, "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && heads_per_group > 0 && H % heads_per_group == 0, "%s: bad B/H/heads_per_group", fn);
   SA_REQUIRE((int64_t)B * H / heads_per_group == maps->G, "%s: B*H/heads_per_group != maps->G", fn);
   if (D != kD) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (only 64)", fn, D);
-  const void* ptrs[2] = {x, out};
-  for (const void* p : ptrs)
-    if (reinterpret_cast<uintptr_t>(p) % 16) return sa::fail(SA_ERR_UNSUPPORTED, "%s: base not 16-byte aligned", fn);
-  for (int i = 0; i < 3; ++i)
-    if (xs[i] % 8 || os[i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "%s: strides must be multiples of 8", fn);
   MergeArgs a;
-  a.m = *maps; a.x = x; a.x_sb = xs[0]; a.x_sh = xs[1]; a.x_sl = xs[2];
-  a.out = out; a.o_sb = os[0]; a.o_sh = os[1]; a.o_sl = os[2];
+  a.m = *maps;
+  for (int t = 0; t < n; ++t) {
+    SA_REQUIRE(x[t] && out[t], "%s: null tensor %d", fn, t);
+    if (reinterpret_cast<uintptr_t>(x[t]) % 16 || reinterpret_cast<uintptr_t>(out[t]) % 16)
+      return sa::fail(SA_ERR_UNSUPPORTED, "%s: base not 16-byte aligned", fn);
+    for (int i = 0; i < 3; ++i)
+      if (xs[3 * t + i] % 8 || os[3 * t + i] % 8)
+        return sa::fail(SA_ERR_UNSUPPORTED, "%s: strides must be multiples of 8", fn);
+    a.x[t] = x[t]; a.x_sb[t] = xs[3 * t]; a.x_sh[t] = xs[3 * t + 1]; a.x_sl[t] = xs[3 * t + 2];
+    a.out[t] = out[t]; a.o_sb[t] = os[3 * t]; a.o_sh[t] = os[3 * t + 1]; a.o_sl[t] = os[3 * t + 2];
+  }
   a.B = B; a.H = H; a.heads_per_group = heads_per_group;
   const int64_t rows = (int64_t)B * H * (unmerge ? maps->L : maps->Lm);
+  SA_REQUIRE(rows * 8 / 256 < (1LL << 31), "%s: grid too large", fn);
   hipStream_t s = sa::as_stream(stream);
-  if (unmerge)
-    hipLaunchKernelGGL(unmerge_kernel, dim3(grid256(rows * 8)), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(merge_kernel, dim3(grid256(rows * 8)), dim3(256), 0, s, a);
+  const dim3 grid(grid256(rows * 8)), blk(256);
+  if (unmerge) hipLaunchKernelGGL(unmerge_kernel, grid, blk, 0, s, a);
+  else if (n == 1) hipLaunchKernelGGL(merge_kernel<1>, grid, blk, 0, s, a);
+  else if (n == 2) hipLaunchKernelGGL(merge_kernel<2>, grid, blk, 0, s, a);
+  else hipLaunchKernelGGL(merge_kernel<3>, grid, blk, 0, s, a);
   return sa::check_launch(fn);
 }
 }  // namespace
 
 extern "C" int sa_tome_merge(const uint16_t* x, const int64_t x_strides[3], int B, int H, int D, int heads_per_group,
                              const sa_tome_maps* maps, uint16_t* out, const int64_t out_strides[3], void* stream) {
-  return launch_merge(false, x, x_strides, B, H, D, heads_per_group, maps, out, out_strides, stream);
+  SA_REQUIRE(x_strides && out_strides, "sa_tome_merge: null strides");
+  return launch_merge(false, 1, &x, x_strides, B, H, D, heads_per_group, maps, &out, out_strides, stream,
+                      "sa_tome_merge");
+}
+
+extern "C" int sa_tome_merge_multi(int n, const uint16_t* const* x, const int64_t* x_strides, int B, int H, int D,
+                                   int heads_per_group, const sa_tome_maps* maps, uint16_t* const* out,
+                                   const int64_t* out_strides, void* stream) {
+  return launch_merge(false, n, x, x_strides, B, H, D, heads_per_group, maps, out, out_strides, stream,
+                      "sa_tome_merge_multi");
 }
 
 extern "C" int sa_tome_unmerge(const uint16_t* xm, const int64_t xm_strides[3], int B, int H, int D,
                                int heads_per_group, const sa_tome_maps* maps, uint16_t* out,
                                const int64_t out_strides[3], void* stream) {
-  return launch_merge(true, xm, xm_strides, B, H, D, heads_per_group, maps, out, out_strides, stream);
+  SA_REQUIRE(xm_strides && out_strides, "sa_tome_unmerge: null strides");
+  return launch_merge(true, 1, &xm, xm_strides, B, H, D, heads_per_group, maps, &out, out_strides, stream,
+                      "sa_tome_unmerge");
 }
 
 // ---------------------------------------------------------------------------------------

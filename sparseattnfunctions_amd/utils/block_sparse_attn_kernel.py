@@ -171,6 +171,41 @@ def sparse_attention_factory(BLOCK_M=64, BLOCK_N=64, **kwargs):
 block_sparse_triton_fn = _sparse_attention.apply
 
 
+def get_sparse_attn_mask_from_topk(x, topk, use_dense_for_last_block=False):
+    """Per-row top-k block mask (reference :31-39: `torch.topk` over the last axis, then
+    `scatter_` into a bool [bsz, heads, n, n] mask; with `use_dense_for_last_block` the last
+    two rows are set dense).
+
+    The selection runs in `topk_kernel` (`sa_block_topk_kv_list` in its `scores_in` mode, no
+    text blocks, no local window): the kept set of each row is the first `topk` columns in
+    (score descending, column ascending) order. Scores are compared in fp32; bf16/fp16 inputs
+    convert exactly, so the order is the input's. torch leaves the order of tied scores
+    unspecified; here the lowest column wins. `x` is [bsz, heads, n, m] with m <= n and
+    m <= 1024; columns m..n-1 of the mask stay False, as the reference's scatter leaves them.
+    """
+    from ..block_masks import topk_kv_list
+
+    if x.dim() != 4:
+        raise ValueError(f"get_sparse_attn_mask_from_topk: x must be 4-D, got {tuple(x.shape)}")
+    bsz, num_head, n, m = x.shape
+    topk = int(topk)
+    if topk < 0 or topk > m:
+        raise RuntimeError(f"selected index k out of range (topk={topk}, {m} columns)")
+    if m > n:
+        raise ValueError(f"get_sparse_attn_mask_from_topk: {m} columns > {n} rows (the mask is [n, n])")
+    _lib.require_gpu(x)
+    if not x.is_floating_point():
+        raise TypeError(f"get_sparse_attn_mask_from_topk: floating-point scores expected, got {x.dtype}")
+    dense_mask = torch.zeros(bsz, num_head, n, n, dtype=torch.bool, device=x.device)
+    if topk > 0 and n > 0:
+        _, sel = topk_kv_list(None, None, bsz, num_head, topk, 0,
+                              scores_in=x.to(torch.float32).reshape(bsz * num_head, n, m), return_mask=True)
+        dense_mask[..., :m] = sel
+    if use_dense_for_last_block:
+        dense_mask[:, :, -2:, :] = True
+    return dense_mask
+
+
 def get_sparse_attn_mask_from_threshold(x, threshold, use_dense_for_last_block=False):
     """Threshold block mask with lower-triangular restriction (reference :42-47)."""
     dense_mask = x > threshold

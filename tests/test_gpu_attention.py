@@ -224,7 +224,7 @@ def test_factory_and_backward(dev):
 
 def test_cogvideox_shape_subset_of_heads(dev):
     # Full CogVideoX-2B shape (B=2, H=30, L=17776) with a random ~20% mask; the oracle checks
-    # 3 of the 60 heads (the kernel computes all of them).
+    # 3 of the 60 heads in full and 40 sampled rows (text, random, the last) of every head.
     case("CogVideoX shape random 20% mask")
     B, H, L = 2, 30, 17776
     nb = math.ceil(L / 64)
@@ -238,3 +238,9 @@ def test_cogvideox_shape_subset_of_heads(dev):
     want = masked_attention(q, k, v, mask, 0.125, heads=heads)
     for b, h in heads:
         _check(out[b, h], want[b, h])
+    for b in range(B):
+        for h in range(H):
+            rows = torch.unique(torch.cat([torch.randint(0, 256, (8,), generator=g),
+                                           torch.randint(256, L, (31,), generator=g), torch.tensor([L - 1])]))
+            w = masked_attention(q, k, v, mask, 0.125, heads=[(b, h)], rows=rows)[b, h]
+            _check(out[b, h, rows], w)

@@ -82,3 +82,47 @@ def test_config2_mask_bit_exact(dev):
     c = kv.cnt.cpu().reshape(60, geom.nb)
     assert torch.all(c[:, :4] == geom.nb)
     assert torch.all((c[:, 4:] >= topk) & (c[:, 4:] <= topk + 4))
+
+
+def _torch_topk_mask(x, topk, dense_last):
+    """The reference's own recipe (block_sparse_attn_kernel.py:31-39) with torch CPU ops."""
+    bsz, nh, n, _ = x.shape
+    idx = torch.topk(x, topk, dim=-1).indices
+    m = torch.zeros(bsz, nh, n, n, dtype=torch.bool)
+    m.scatter_(-1, idx, True)
+    if dense_last:
+        m[:, :, -2:, :] = True
+    return m
+
+
+@pytest.mark.parametrize("n,topk,dense_last,dtype", [(32, 8, False, torch.float32), (278, 55, True, torch.float32),
+                                                      (100, 100, False, torch.float32), (64, 1, True, torch.bfloat16)])
+def test_mask_from_topk_matches_torch(dev, n, topk, dense_last, dtype):
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import get_sparse_attn_mask_from_topk
+
+    case(f"get_sparse_attn_mask_from_topk n={n} topk={topk} dense_last={dense_last} {dtype}")
+    g = torch.Generator().manual_seed(n + topk)
+    # Tie-free rows: a random permutation of distinct values per row (exact in bf16 up to 256).
+    x = torch.argsort(torch.rand(2, 3, n, n, generator=g), dim=-1).to(torch.float32) - n / 2
+    x = x.to(dtype)
+    got = get_sparse_attn_mask_from_topk(x.to(dev), topk, use_dense_for_last_block=dense_last)
+    assert got.dtype == torch.bool and got.shape == (2, 3, n, n)
+    assert torch.equal(got.cpu(), _torch_topk_mask(x.float(), topk, dense_last))
+
+
+def test_mask_from_topk_ties_vs_oracle(dev):
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import get_sparse_attn_mask_from_topk
+
+    case("get_sparse_attn_mask_from_topk ties")
+    g = torch.Generator().manual_seed(11)
+    x = torch.randint(0, 3, (1, 4, 50, 50), generator=g).float()
+    x[0, 0, 0, :4] = torch.tensor([float("nan"), float("inf"), -0.0, 0.0])
+    got = get_sparse_attn_mask_from_topk(x.to(dev), 7, use_dense_for_last_block=True)
+    _, _, omask, _ = native.block_topk(None, None, 7, 0, scores_in=x.reshape(4, 50, 50))
+    want = omask.bool().reshape(1, 4, 50, 50).clone()
+    want[:, :, -2:, :] = True
+    assert torch.equal(got.cpu(), want)
+    # Exactly topk entries in every row above the dense tail.
+    assert torch.all(got[:, :, :-2].sum(-1).cpu() == 7)
+    with pytest.raises(RuntimeError):
+        get_sparse_attn_mask_from_topk(x.to(dev), 51)

@@ -1,6 +1,7 @@
-"""GPU parity of the processor classes at the CogVideoX-2B shape (configs 2 and 3) and small
-shapes: kv lists bit-exact against the C oracle, outputs within the bf16 tolerances
-(max-abs <= 2e-2, mean-abs <= 2e-3) against the fp64 oracle on a subset of heads."""
+"""GPU parity of the processor classes at the CogVideoX-2B shape (configs 2, 3 and layers of
+config 5) and small shapes: kv lists bit-exact against the C oracle, outputs within the bf16
+tolerances (max-abs <= 2e-2, mean-abs <= 2e-3) against the fp64 oracle -- in full on a few
+heads, and on sampled rows of every head (all text rows, 32 random video rows, the last row)."""
 import math
 
 import pytest
@@ -25,6 +26,19 @@ def _check(got, want):
     assert err.mean().item() <= 2e-3, err.mean().item()
 
 
+def _check_all_heads(out, q, k, v, mask, seed, n_rand=32, text_len=226):
+    """Every (b, h): its text rows, n_rand random video rows and the last row (the partial
+    query block) against the fp64 oracle."""
+    g = torch.Generator().manual_seed(seed)
+    B, H, L, _ = q.shape
+    for b in range(B):
+        for h in range(H):
+            rnd = torch.randint(text_len, L, (n_rand,), generator=g)
+            rows = torch.unique(torch.cat([torch.arange(text_len), rnd, torch.tensor([L - 1])]))
+            want = masked_attention(q, k, v, mask, 1 / 8, heads=[(b, h)], rows=rows)[b, h]
+            _check(out[b, h, rows], want)
+
+
 def _oracle_mask(q, k, topk, n_text, local=None):
     nb = math.ceil(q.shape[2] / 64)
     _, _, m, _ = native.block_topk(native.block_pool(q), native.block_pool(k), topk, n_text, local=local)
@@ -47,6 +61,7 @@ def test_block_mask_attn_config2(dev, c2_inputs):
     want = masked_attention(q, k, v, mask, 1 / 8, heads=HEADS)
     for b, h in HEADS:
         _check(out[b, h], want[b, h])
+    _check_all_heads(out, q, k, v, mask, seed=2)
 
 
 def test_combined_attn_config3(dev, c2_inputs):
@@ -62,6 +77,34 @@ def test_combined_attn_config3(dev, c2_inputs):
     want = masked_attention(q, k, v, mask, 1 / 8, heads=HEADS)
     for b, h in HEADS:
         _check(out[b, h], want[b, h])
+    _check_all_heads(out, q, k, v, mask, seed=3)
+
+
+@pytest.fixture(scope="module")
+def c5_processor():
+    # One denoising step's processor: every layer recomputes its combined mask.
+    return CombinedAttn(warmup_epoch=0, layer_num=30)
+
+
+@pytest.mark.parametrize("layer", [1, 14, 29])
+def test_config5_layers(dev, c5_processor, layer):
+    # Config 5: layer `layer` of the 30-layer step, its q/k/v drawn as config 2 with
+    # seed = layer index (CPU generator), the config-3 mask recomputed for the layer.
+    case(f"config 5 layer {layer}")
+    q, k, v = cogvideox_qkv(layer)
+    out = c5_processor(q.to(dev), k.to(dev), v.to(dev)).cpu()
+    nb = COGVIDEOX_2B.nb
+    local = native.local_window(COGVIDEOX_2B, 1, 8, 8)
+    idx, cnt, m, _ = native.block_topk(native.block_pool(q), native.block_pool(k), topk_count(0.1, nb), 4,
+                                       local=local)
+    kv = c5_processor.last_kv
+    gi, gc = kv.idx.cpu(), kv.cnt.cpu()
+    assert torch.equal(gc, cnt)
+    for r in range(cnt.numel()):
+        assert torch.equal(gi[r, : cnt[r]], idx[r, : cnt[r]]), r
+    mask = m.reshape(2, 30, nb, nb).bool()
+    assert 0.80 < c5_processor.sparsity() < 0.88
+    _check_all_heads(out, q, k, v, mask, seed=100 + layer)
 
 
 def test_combined_attn_warmup_is_dense(dev):

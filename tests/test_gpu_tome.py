@@ -66,38 +66,51 @@ def test_small_pipeline_bit_exact(dev, mode):
             assert torch.equal(_tome.unmerge(xm, maps, hpg).cpu(), native.tome_unmerge(xm.cpu(), want, hpg))
 
 
-def test_config4_maps_bit_exact(dev):
-    case("tome config 4 full shape maps")
+@pytest.fixture(scope="module")
+def c4_oracle():
+    """Config 4 inputs (seed 3) and every matching map computed by the C oracle alone: the
+    metric, the partition, the argmax of all 12 240 srcs of both groups (no GPU output is
+    involved), then the edge order and the merge/unmerge maps from that argmax."""
     q, k, v = cogvideox_qkv(3)
-    metric = _tome.metric_from_qkv(k.to(dev), None, 226, 0)
     om = native.tome_metric(k, None, 226, 0)
-    assert torch.equal(metric.cpu(), om)
+    oa, ob = native.tome_partition(13, 30, 45, 2, 2, 1)
+    idx, mx = native.tome_argmax_all(om, oa, ob)
+    want = native.tome_maps(mx, idx, 17550, oa, ob, 4000, 226)
+    return dict(q=q, k=k, v=v, metric=om, a=oa, b=ob, maps=want)
+
+
+def test_config4_maps_bit_exact(dev, c4_oracle):
+    case("tome config 4 full shape maps")
+    o = c4_oracle
+    metric = _tome.metric_from_qkv(o["k"].to(dev), None, 226, 0)
+    assert torch.equal(metric.cpu(), o["metric"])
     a, b = _tome.partition(13, 30, 45, 2, 2, 1, dev)
     assert (a.numel(), b.numel()) == (12240, 5310)
+    assert torch.equal(a.cpu(), o["a"]) and torch.equal(b.cpu(), o["b"])
     maps = _tome.match(metric, a, b, 4000, 226)
-    oa, ob = a.cpu(), b.cpu()
-    # argmax spot check on 256 srcs per group (each src's argmax is independent)
-    sub = torch.arange(0, 12240, 48, dtype=torch.int32)
-    idx, mx = native.tome_argmax(om, oa[sub.long()], ob)
-    assert torch.equal(maps.node_idx.cpu()[:, sub.long()], idx)
-    assert torch.equal(maps.node_max.cpu()[:, sub.long()], mx)
-    # every other map from the GPU's (spot-checked) node_max / node_idx
-    want = native.tome_maps(maps.node_max.cpu(), maps.node_idx.cpu(), 17550, oa, ob, 4000, 226)
-    _maps_equal(maps, want, ("edge", "dst_idx", "dst_cnt", "row_of_token", "key_bias"))
+    _maps_equal(maps, o["maps"])
     _check_members(maps)
     assert maps.Lm == 13776 and int(maps.sizes.sum(1)[0]) == 5310 + 4000
+    # Merged q, k, v of every head bit-exact against the oracle's merge from its own maps.
+    merged = _tome.merge_many([o[n].to(dev) for n in "qkv"], maps, 30)
+    for n, xm in zip("qkv", merged):
+        want = native.tome_merge(o[n], o["maps"], o["a"], o["b"], 4000, 226, 30)
+        assert torch.equal(xm.cpu(), want), n
+        assert torch.equal(_tome.merge(o[n].to(dev), maps, 30).cpu(), want), n
+    back = _tome.unmerge(merged[2], maps, 30).cpu()
+    assert torch.equal(back, native.tome_unmerge(merged[2].cpu(), o["maps"], 30))
 
 
-def test_merge_attention_config4(dev):
+def test_merge_attention_config4(dev, c4_oracle):
     case("MergeAttention config 4 end to end")
-    q, k, v = cogvideox_qkv(3)
+    o = c4_oracle
+    q, k, v = o["q"], o["k"], o["v"]
     proc = MergeAttention()
     out = proc(q.to(dev), k.to(dev), v.to(dev)).cpu()
-    maps = proc.maps
-    want_maps = {f: getattr(maps, f).cpu() for f in ("edge", "row_of_token", "key_bias")}
-    want_maps["dst_idx"] = maps.dst_idx.cpu()[:, :4000]
-    a, b = maps.a_idx.cpu(), maps.b_idx.cpu()
-    heads = [(0, 0), (1, 21)]
+    want_maps = o["maps"]
+    _maps_equal(proc.maps, want_maps)
+    a, b = o["a"], o["b"]
+    heads = [(0, 0), (0, 17), (1, 8), (1, 29)]
     for bb, hh in heads:
         sel = lambda x: x[bb:bb + 1, hh:hh + 1]
         sub = {f: t[bb:bb + 1] for f, t in want_maps.items()}

@@ -96,3 +96,21 @@ def test_partial_last_block_masks_tail(L):
     got = masked_attention(q, k, v, m, 0.125)
     want = torch.nn.functional.scaled_dot_product_attention(q, k, v, scale=0.125)
     assert torch.allclose(got, want, atol=1e-12)
+
+
+def test_row_subset_equals_full_rows():
+    # `rows=` computes the selected query rows as the full call does (to fp64 rounding: the
+    # matmul's summation order depends on the chunk shape), including rows of different
+    # blocks, an empty block row, a key bias and a token mask.
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(1, 2, 300, 64, generator=g) for _ in range(3))
+    bm = torch.rand(1, 2, 5, 5, generator=g) < 0.5
+    bm[0, 1, 2] = False
+    bias = torch.randn(1, 2, 300, generator=g)
+    tm = lambda r: (r[:, None] + torch.arange(300)[None, :]) % 3 != 0
+    rows = torch.tensor([0, 1, 63, 64, 130, 150, 255, 299])
+    full = masked_attention(q, k, v, bm, 0.125, key_bias=bias, token_mask=tm)
+    part = masked_attention(q, k, v, bm, 0.125, key_bias=bias, token_mask=tm, rows=rows, row_chunk=3)
+    assert part.shape == (1, 2, rows.numel(), 64)
+    assert torch.allclose(part, full[:, :, rows], rtol=0, atol=1e-12)
+    assert torch.all(part[0, 1, 4:6] == 0)  # rows 130 and 150 sit in the empty block row

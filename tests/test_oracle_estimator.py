@@ -84,6 +84,21 @@ def _reference_ops(scores, mode, thr, min_keep, max_keep, init_k, n_text=4):
         uns = (cum[..., -1:] < thr * total).squeeze(-1)
         kk = torch.where(uns, torch.full_like(kk, n), kk)
         kk = torch.clamp(torch.clamp(kk, max=n), min=min_keep, max=max_keep)
+    elif mode == 2:
+        # generate_attention_mask_frame_scope / get_inner_frame_mask "row" (mask_related.py
+        # :224-232, 366-376): cum >= threshold, last forced, argmax, ranks <= k.
+        over = cum >= thr * total
+        over[..., -1] = True
+        kk = torch.argmax(over.int(), dim=-1) + 1
+        kk = torch.clamp(kk, min=min_keep, max=max_keep)
+    elif mode == 3:
+        # get_inner_frame_mask "head" (mask_related.py:378-391): cum <= threshold, last forced.
+        sel = cum <= thr * total
+        sel[..., -1] = True
+        mask = torch.zeros_like(sel).scatter_(-1, ind, sel)
+        mask[:, :n_text] = True
+        mask[:, :, :n_text] = True
+        return mask
     else:
         cur_k = torch.full((BH, nqb), init_k, dtype=torch.int64)
         cur = cum.gather(-1, (cur_k - 1)[..., None]).squeeze(-1)
@@ -99,7 +114,7 @@ def _reference_ops(scores, mode, thr, min_keep, max_keep, init_k, n_text=4):
     return mask
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
 @pytest.mark.parametrize("n,seed", [(5, 0), (64, 1), (65, 2), (278, 3), (700, 4)])
 def test_energy_oracle_matches_reference_ops(mode, n, seed):
     BH, nqb = 3, 7
@@ -139,6 +154,28 @@ def test_energy_hand_cases():
     _, cnt, m = native.energy_list(s, 0, 0.5, 1, 6, 1, 2)
     m = m.reshape(3, 6)
     assert m[0].all() and m[1].all() and m[2].tolist() == [1, 1, 0, 0, 0, 1]
+
+
+def test_energy_inclusive_and_cumulative_hand_cases():
+    # Equal scores, cum[j] = j + 1, total 10. Mode 2 keeps through the crossing: 0.95 -> j = 9
+    # (all 10); 0.5 -> j = 4 (5 kept). Mode 3 keeps cum <= target plus the last rank:
+    # 0.5 -> ranks 0..4 and rank 9 (ties: ranks follow the column order).
+    s = torch.ones(1, 1, 10)
+    assert native.energy_list(s, 2, 0.95, 0, 10, 1, 0)[1].item() == 10
+    _, cnt, m = native.energy_list(s, 2, 0.5, 0, 10, 1, 0)
+    assert cnt.item() == 5 and m[0].tolist() == [1] * 5 + [0] * 5
+    _, cnt, m = native.energy_list(s, 3, 0.5, 0, 10, 1, 0)
+    assert m[0].tolist() == [1] * 5 + [0] * 4 + [1]
+    # Threshold 1 (the reference's get_inner_frame_mask default): mode 2 keeps every column
+    # up to the last one that still raises the sum; a zero tail is dropped.
+    s = torch.tensor([[[0.0, 3.0, 0.5, 0.0, 1.5]]])
+    _, cnt, m = native.energy_list(s, 2, 1.0, 0, 5, 1, 0)
+    assert m[0].tolist() == [0, 1, 1, 0, 1]
+    # A dominant column alone crosses 0.5: mode 2 keeps it; mode 3 keeps nothing below the
+    # target but the forced last rank (the smallest score).
+    s = torch.tensor([[[0.1, 5.0, 0.2, 0.05]]])
+    assert native.energy_list(s, 2, 0.5, 0, 4, 1, 0)[2][0].tolist() == [0, 1, 0, 0]
+    assert native.energy_list(s, 3, 0.5, 0, 4, 1, 0)[2][0].tolist() == [0, 0, 0, 1]
 
 
 def test_energy_prefix_property():
