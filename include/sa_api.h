@@ -10,7 +10,8 @@
  *    strides {stride_b, stride_h, stride_l}; the D axis must be contiguous (stride 1).
  *    Element type is bf16 (uint16_t bit patterns) unless stated otherwise.
  *  - Device buffers are owned by the caller (PyTorch's caching allocator in the Python
- *    package). The library allocates no device memory.
+ *    package). The library allocates no device memory; its one device-resident buffer is
+ *    the fixed scratch array of sa_tome_match_noalloc, part of the loaded code object.
  *  - `stream` is a hipStream_t passed as void*; NULL means the default stream. All GPU
  *    work is enqueued asynchronously on it; no entry point synchronises the device.
  *  - Entry points documented as "host" run on the CPU only and touch no GPU state.
@@ -459,6 +460,18 @@ int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes);
  */
 int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspace,
                   int64_t workspace_bytes, void* stream);
+
+/*
+ * sa_tome_match without a workspace argument and without any allocation. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops). The split partials live in a device array inside the library
+ * (one 16 MiB copy per GPU, held until the process ends); calls whose partials,
+ * G * splits * max(n_src, 1) * 8 bytes with splits <= 16 (sa_tome_match_workspace), exceed it
+ * fail with SA_ERR_INVALID. Every call on one GPU shares that array: calls that overlap on
+ * one GPU (on different streams or host threads) race and must be serialised by the caller.
+ * Results are identical to sa_tome_match's.
+ */
+int sa_tome_match_noalloc(const float* metric, int C, sa_tome_maps* maps, void* stream);
 
 /*
  * merge closure for a 4-D [B,H,L,64] tensor (merge_unmerge.py:119-128): out [B,H,Lm,64] =

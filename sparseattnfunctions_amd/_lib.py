@@ -77,6 +77,7 @@ _PROTOTYPES = {
     "sa_tome_normalize": (_I, [_P, ctypes.c_int64, _I, _P, _P]),
     "sa_tome_match_workspace": (_I, [_I, _I, _I, _I64P]),
     "sa_tome_match": (_I, [_P, _I, _P, _P, ctypes.c_int64, _P]),
+    "sa_tome_match_noalloc": (_I, [_P, _I, _P, _P]),
     "sa_tome_merge": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _I64P, _P]),
     "sa_tome_merge_multi": (_I, [_I, _P, _I64P, _I, _I, _I, _I, _P, _P, _I64P, _P]),
     "sa_tome_unmerge": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _I64P, _P]),

@@ -140,6 +140,22 @@ def match(metric: torch.Tensor, a_idx: torch.Tensor, b_idx: torch.Tensor, r: int
     return maps
 
 
+def match_noalloc(metric: torch.Tensor, a_idx: torch.Tensor, b_idx: torch.Tensor, r: int, text_len: int) -> TomeMaps:
+    """match() through `sa_tome_match_noalloc`: the library allocates nothing and no workspace
+    is passed (its partials live in a fixed 16 MiB device array per GPU; larger problems raise
+    ValueError). The maps themselves are caller buffers, allocated here."""
+    _lib.require_gpu(metric, a_idx, b_idx)
+    G, N, C = metric.shape
+    r = max(0, min(int(r), a_idx.numel()))
+    maps = TomeMaps(G, N, text_len, a_idx, b_idx, r, metric.device)
+    metric = metric.contiguous()
+    with torch.cuda.device(metric.device):
+        rc = _lib.load().sa_tome_match_noalloc(metric.data_ptr(), C, ctypes.byref(maps.struct),
+                                               _lib.stream_of(metric))
+    _lib.check(rc, "sa_tome_match_noalloc")
+    return maps
+
+
 def _apply(fn_name, x, maps: TomeMaps, heads_per_group: int, rows_out: int, out: Optional[torch.Tensor]):
     _lib.require_gpu(x)
     x = _bf16(x)

@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <vector>
 
 #include "sa_common.h"
@@ -619,26 +620,15 @@ extern "C" int sa_tome_normalize(const float* metric, int64_t rows, int C, float
   return sa::check_launch("sa_tome_normalize");
 }
 
-extern "C" int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes) {
-  SA_REQUIRE(bytes && G > 0 && n_src >= 0 && n_dst > 0, "sa_tome_match_workspace: bad arguments");
-  const int splits = match_splits(n_dst);
-  *bytes = (int64_t)G * splits * std::max(n_src, 1) * 8;
-  return sa::ok();
-}
-
-extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspace, int64_t ws_bytes,
-                             void* stream) {
-  int rc = check_maps(maps, "sa_tome_match");
-  if (rc) return rc;
-  SA_REQUIRE(metric && workspace, "sa_tome_match: null metric/workspace");
-  SA_REQUIRE(C > 0 && C <= kMaxC, "sa_tome_match: C=%d outside [1, %d]", C, kMaxC);
-  const sa_tome_maps& m = *maps;
-  int64_t need = 0;
-  sa_tome_match_workspace(m.G, m.n_src, m.n_dst, &need);
-  SA_REQUIRE(ws_bytes >= need, "sa_tome_match: workspace %lld < %lld bytes", (long long)ws_bytes, (long long)need);
-  hipStream_t s = sa::as_stream(stream);
+namespace {
+// Matching and map construction with the split partials (G * splits * max(n_src, 1) floats
+// of maxima, then as many int32 positions) at `partials`: every entry the combine step reads
+// is written by match_kernel first, so the buffer needs no clearing.
+int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* partials, hipStream_t s,
+                    const char* fn) {
+  int rc;
   const int splits = match_splits(m.n_dst);
-  float* part_max = reinterpret_cast<float*>(workspace);
+  float* part_max = reinterpret_cast<float*>(partials);
   int32_t* part_idx = reinterpret_cast<int32_t*>(part_max + (int64_t)m.G * splits * std::max(m.n_src, 1));
   if (m.n_src > 0) {
     MatchArgs a;
@@ -647,7 +637,7 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
     a.dst_per_split = match_tiles_per_split(m.n_dst) * kMTile;
     a.part_max = part_max; a.part_idx = part_idx;
     hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kMTile - 1) / kMTile, m.G, splits), dim3(256), 0, s, a);
-    if ((rc = sa::check_launch("sa_tome_match/match"))) return rc;
+    if ((rc = sa::check_launch(fn))) return rc;
   }
   MapArgs ma;
   ma.m = m; ma.part_max = part_max; ma.part_idx = part_idx; ma.splits = splits;
@@ -664,7 +654,76 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
     hipLaunchKernelGGL(fill_kernel, dim3(grid256((int64_t)m.G * m.r)), dim3(256), 0, s, m);
     hipLaunchKernelGGL(sort_kernel, dim3(grid256((int64_t)m.G * m.n_dst)), dim3(256), 0, s, m);
   }
-  return sa::check_launch("sa_tome_match");
+  return sa::check_launch(fn);
+}
+
+int64_t match_partial_bytes(int G, int n_src, int n_dst) {
+  return (int64_t)G * match_splits(n_dst) * std::max(n_src, 1) * 8;
+}
+
+// ---- allocation-free matching ---------------------------------------------------------
+// The split partials of sa_tome_match_noalloc live in this file-scope device array (one copy
+// per GPU, held for the life of the process). Host code never passes `scratch` itself to a
+// kernel: the name is a host-side stand-in; its device address on the current GPU comes from
+// hipGetSymbolAddress on that GPU's first call and is kept per device.
+constexpr int64_t kNoAllocScratchBytes = 16ll << 20;
+static __device__ __attribute__((aligned(256))) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices];
+
+int scratch_address(void** out, const char* fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return sa::fail(SA_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return sa::fail(SA_ERR_UNSUPPORTED, "%s: device %d >= %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return sa::fail(SA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return SA_OK;
+}
+}  // namespace
+
+extern "C" int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes) {
+  SA_REQUIRE(bytes && G > 0 && n_src >= 0 && n_dst > 0, "sa_tome_match_workspace: bad arguments");
+  *bytes = match_partial_bytes(G, n_src, n_dst);
+  return sa::ok();
+}
+
+extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspace, int64_t ws_bytes,
+                             void* stream) {
+  int rc = check_maps(maps, "sa_tome_match");
+  if (rc) return rc;
+  SA_REQUIRE(metric && workspace, "sa_tome_match: null metric/workspace");
+  SA_REQUIRE(C > 0 && C <= kMaxC, "sa_tome_match: C=%d outside [1, %d]", C, kMaxC);
+  const sa_tome_maps& m = *maps;
+  const int64_t need = match_partial_bytes(m.G, m.n_src, m.n_dst);
+  SA_REQUIRE(ws_bytes >= need, "sa_tome_match: workspace %lld < %lld bytes", (long long)ws_bytes, (long long)need);
+  return tome_match_impl(metric, C, m, workspace, sa::as_stream(stream), "sa_tome_match");
+}
+
+extern "C" int sa_tome_match_noalloc(const float* metric, int C, sa_tome_maps* maps, void* stream) {
+  const char* fn = "sa_tome_match_noalloc";
+  int rc = check_maps(maps, fn);
+  if (rc) return rc;
+  SA_REQUIRE(metric, "%s: null metric", fn);
+  SA_REQUIRE(C > 0 && C <= kMaxC, "%s: C=%d outside [1, %d]", fn, C, kMaxC);
+  const sa_tome_maps& m = *maps;
+  const int64_t need = match_partial_bytes(m.G, m.n_src, m.n_dst);
+  SA_REQUIRE(need <= kNoAllocScratchBytes,
+             "%s: G=%d, n_src=%d, n_dst=%d need %lld bytes of partials, above the %lld-byte device scratch "
+             "(use sa_tome_match with a workspace)",
+             fn, m.G, m.n_src, m.n_dst, (long long)need, (long long)kNoAllocScratchBytes);
+  void* partials = nullptr;
+  if ((rc = scratch_address(&partials, fn))) return rc;
+  return tome_match_impl(metric, C, m, partials, sa::as_stream(stream), fn);
 }
 
 namespace {
