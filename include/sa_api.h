@@ -355,6 +355,26 @@ int sa_pattern_judge_finish(const float* share, const float* G1, const float* G2
                             void* stream);
 
 /*
+ * Row-group sums: out[b*H + h][g][c] = sum over rows r in [g*R, min(L, g*R + R)) of
+ * x[b, h, r, col0 + c] (fp32, rows ascending), c < ncols, col0 + ncols <= 64, g < ceil(L/R).
+ * With x the key-block masses of a frame's attention (the attention of the frame's queries
+ * over its keys with a 0/1 key-block indicator as v), these are the 64 x 64 cell sums of
+ * get_inner_frame_mask (utils/mask_related.py:352-361: calc_attn, then the (s1 s2) sum).
+ */
+int sa_row_group_sums(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L,
+                      int rows_per_group, int col0, int ncols, float* out, void* stream);
+
+/*
+ * Kronecker fusion of get_block_mask (utils/mask_related.py:397-404): for each of BH heads,
+ * out[i][j] (fp32 0/1, [F*Ri + pad][F*Ci + pad]) = frame_mask[i / Ri][j / Ci] &&
+ * inner_mask[i % Ri][j % Ci] for i < F*Ri and j < F*Ci, and 1 on the `pad` trailing (text)
+ * rows and columns, as the reference's pad(value=1). frame_mask uint8 [BH][F][F],
+ * inner_mask uint8 [BH][Ri][Ci].
+ */
+int sa_kron_block_mask(const uint8_t* frame_mask, const uint8_t* inner_mask, int BH, int F, int Ri,
+                       int Ci, int pad, float* out, void* stream);
+
+/*
  * (host) Static local 3-D window of the combined mask, one byte per (query block, key
  * block): 1 iff both blocks are video blocks and their centre tokens (index
  * block*qb + block/2, clamped to L-1) lie within +-dt latent frames, +-dh patch rows and

@@ -65,6 +65,8 @@ _PROTOTYPES = {
     "sa_pattern_plan": (_I, [_P, _I64P, _P, _I, _I, _I, _I, _I, _F, _F, _F, _F, _F, _P, _P, _P, _P, _P, _P]),
     "sa_pattern_combine": (_I, [_P, _I64P, _P, _I64P, _P, _I64P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                 _F, _F, _F, _F, _P, _I64P, _P]),
+    "sa_row_group_sums": (_I, [_P, _I64P, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "sa_kron_block_mask": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "sa_sta_permutation": (_I, [_I, _I, _I, _I, _P, _P]),
     "sa_sta_block_masks": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "sa_gather_tokens": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _I64P, _P]),

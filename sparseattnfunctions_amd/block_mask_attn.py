@@ -11,8 +11,11 @@ Differences from the reference, by design:
   * `__call__` returns the output (the reference computes it and returns None, :26-29);
   * `forward` is the block-sparse path (the reference's `forward` is dense SDPA on a padded
     layout, :21-25); `forward_dense` runs the same kernel with every block kept;
-  * `forward_backup` (frame-scope sampled estimator + per-frame pad/truncate layout,
-    :11-20) depends on torch RNG draws and is not provided.
+  * `forward_backup` (:11-20) is the reference's frame-factored path: the frame-level mask
+    of generate_attention_mask_frame_scope, the per-frame pad/truncate layout of
+    preprocess_qkv, the first frame's inner block mask, their Kronecker fusion with dense text
+    blocks, block-sparse attention and the inverse layout -- each a HIP kernel here (see
+    utils/mask_related.py); it draws the same torch random numbers in the same order.
 """
 from __future__ import annotations
 
@@ -20,7 +23,7 @@ import math
 
 import torch
 
-from ._kv import KVList
+from ._kv import KVList, kv_list_from_mask
 from .block_masks import meanpool_topk_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
 from .workloads import COGVIDEOX_2B, Geometry, topk_count
@@ -63,10 +66,25 @@ class BlockSparseAttention:
         return block_sparse_attention(q, k, v, dense_kv_list(B, H, nb, math.ceil(k.shape[2] / 64), q.device),
                                       self.sm_scale)
 
-    def forward_backup(self, q, k, v):
-        raise NotImplementedError(
-            "forward_backup (frame-scope sampled estimator, block_mask_attn.py:11-20) is not part of "
-            "the MI355X build; forward() is the block-sparse path")
+    def forward_backup(self, q, k, v, frame_draws=None, starts=None):
+        """block_mask_attn.py:11-20: frame-level mask (generate_attention_mask_frame_scope),
+        per-frame pad/truncate layout (preprocess_qkv), inner-frame mask of the first frame
+        (get_inner_frame_mask, threshold 1), their fusion (get_block_mask), block-sparse
+        attention on the processed layout and reverse_process_out. `frame_draws` / `starts`
+        replace the two torch.randint draws (CPU: 60 first-frame positions; GPU: the (B, 13)
+        truncation offsets) when given."""
+        from .utils.mask_related import (generate_attention_mask_frame_scope, get_block_mask, get_inner_frame_mask,
+                                         preprocess_qkv, reverse_process_out)
+
+        outer = generate_attention_mask_frame_scope(q, k, draws=frame_draws)
+        qp, kp, vp = preprocess_qkv(q, k, v, starts=starts)
+        inner = get_inner_frame_mask(qp, kp)
+        all_mask = get_block_mask(inner, outer)
+        B, H = q.shape[:2]
+        kv = kv_list_from_mask(all_mask, B, H, math.ceil(qp.shape[2] / 64), math.ceil(kp.shape[2] / 64))
+        self.last_kv = kv
+        out = block_sparse_attention(qp, kp, vp, kv, self.sm_scale)
+        return reverse_process_out(out)
 
     def sparsity(self) -> float:
         """Fraction of skipped blocks in the last call."""

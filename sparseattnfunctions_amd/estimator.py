@@ -19,6 +19,10 @@ from .block_masks import _prep
 
 BLOCK = 64
 MODES = {"energy": 0, "topk": 1}
+# Selection rules of the backup block mask (utils/mask_related.py:224-232, 366-391): "inclusive"
+# keeps the sorted prefix through the first position reaching the threshold (the last one when
+# none does); "cumulative" keeps the positions whose cumulative sum stays within it, plus the last.
+CUT_MODES = {"inclusive": 2, "cumulative": 3}
 
 
 def _ns_pad(nb: int, num_keep: int) -> int:
@@ -130,3 +134,25 @@ def energy_kv_list(scores: torch.Tensor, mode: str = "energy", init_k=None, max_
             _lib.stream_of(s))
     _lib.check(rc, "sa_energy_kv_list")
     return (kv, mask.bool()) if return_mask else kv
+
+
+def energy_mask(scores: torch.Tensor, mode: str, threshold: float) -> torch.Tensor:
+    """Energy cut of every row of fp32 scores [G, rows, n] (n <= 1024) on the GPU with the
+    rules of CUT_MODES (`sa_energy_kv_list` modes 2 and 3, no clamping, no text blocks):
+    bool [G, rows, n]. Ranks order (score descending, column ascending); the cumulative sums
+    are sequential fp32 additions in rank order and the total is their last value."""
+    _lib.require_gpu(scores)
+    if scores.dim() != 3:
+        raise ValueError(f"scores must be [G, rows, n], got {tuple(scores.shape)}")
+    if mode not in CUT_MODES:
+        raise ValueError(f"Unsupported mode: {mode}")
+    G, rows, n = scores.shape
+    s = scores.to(torch.float32).contiguous()
+    kv = KVList.empty(G, 1, rows, n, s.device)
+    mask = torch.empty(G, rows, n, dtype=torch.uint8, device=s.device)
+    with torch.cuda.device(s.device):
+        rc = _lib.load().sa_energy_kv_list(
+            s.data_ptr(), G, rows, n, CUT_MODES[mode], float(threshold), 0, n, 1, 0, kv.idx.data_ptr(), kv.max_cnt,
+            kv.cnt.data_ptr(), mask.data_ptr(), _lib.stream_of(s))
+    _lib.check(rc, "sa_energy_kv_list")
+    return mask.bool()

@@ -125,7 +125,7 @@ class ParternAttentionColVersion_V2:
             raise ValueError(f"expected q, k, v of shape [B, H, {g.L}, 64], got {tuple(q.shape)}")
         return _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
 
-    def sampled_masses(self, q, k, index_k):
+    def sampled_masses(self, q, k, index_k, sm_scale: float = scale_factor):
         """Segment masses of the sampled attention (get_weight_for_patch, :321-358): for every
         sampled video row, the softmax mass (with log(ns/S) added to text keys) on the text
         keys (column 0) and on each frame's samples (column 1 + f). bf16 [B, H, F*ns, 64]."""
@@ -137,7 +137,7 @@ class ParternAttentionColVersion_V2:
         bias = _cached(("bias", g, str(q.device)), lambda: torch.where(
             torch.arange(nk, device=q.device) < g.text_length, composition(g), 0.0).float())
         return block_sparse_attention(qs[:, :, g.text_length:], ks, _bcast(_sample_indicator(g, q.device), B, H),
-                                      _dense(B, H, g.frames * g.sample_num, nk, q.device), scale_factor,
+                                      _dense(B, H, g.frames * g.sample_num, nk, q.device), sm_scale,
                                       key_bias=_bcast(bias, B, H))
 
     def forward(self, q, k, v, index_k=None):
@@ -205,12 +205,12 @@ class ParternAttentionColVersion_V2:
                                                    _lib.stream_of(mass)), "sa_pattern_maps")
         return i2i, i2t
 
-    def get_weight_for_patch(self, q, k, index_k=None):
+    def get_weight_for_patch(self, q, k, index_k=None, sm_scale: float = scale_factor):
         """(img2img_map [B,H,F,F], img2text_map [B,H,F,1]) fp32."""
         q, k, _ = self._check(q, k, k)
         if index_k is None:
             _, index_k = get_indexs(self.geometry)
-        return self._maps(self.sampled_masses(q, k, index_k))
+        return self._maps(self.sampled_masses(q, k, index_k, sm_scale))
 
     def __call__(self, *args, **kwds):
         return self.forward(*args, **kwds)
@@ -235,11 +235,11 @@ def _compact(x, idx, n_pad):
     return gather_tokens(x, full.to(x.device)).reshape(B * H, n_pad, 64)
 
 
-def _probs(qs, ks, rows, keys, n_bias, bias, c_lo, c_hi, P):
+def _probs(qs, ks, rows, keys, n_bias, bias, c_lo, c_hi, P, sm_scale: float = scale_factor):
     BH = qs.shape[0]
     with torch.cuda.device(qs.device):
         _lib.check(_lib.load().sa_sampled_probs(
-            qs.data_ptr(), ks.data_ptr(), BH, rows, qs.shape[1], keys, ks.shape[1], scale_factor, n_bias, bias,
+            qs.data_ptr(), ks.data_ptr(), BH, rows, qs.shape[1], keys, ks.shape[1], sm_scale, n_bias, bias,
             c_lo, c_hi, P.data_ptr(), P.stride(0), P.stride(1), _lib.stream_of(qs)), "sa_sampled_probs")
 
 

@@ -63,3 +63,9 @@ class _attention_pooling(torch.autograd.Function):
 
 
 attn_with_pooling = _attention_pooling.apply
+
+
+def is_hip() -> bool:
+    """The reference's backend probe (Triton's active target is "hip" on ROCm): this build runs
+    on HIP only."""
+    return True

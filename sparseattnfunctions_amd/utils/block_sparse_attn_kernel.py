@@ -213,3 +213,9 @@ def get_sparse_attn_mask_from_threshold(x, threshold, use_dense_for_last_block=F
         dense_mask[:, :, -2:, :] = True
     dense_mask.tril_()
     return dense_mask
+
+
+def is_hip() -> bool:
+    """The reference's backend probe (Triton's active target is "hip" on ROCm): this build runs
+    on HIP only."""
+    return True

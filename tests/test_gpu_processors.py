@@ -139,5 +139,3 @@ def test_block_mask_attn_small_and_dense(dev):
     _check(out, masked_attention(q, k, v, mask, 1 / 8))
     dense = proc.forward_dense(q.to(dev), k.to(dev), v.to(dev))
     _check(dense, masked_attention(q, k, v, torch.ones(1, 1, nb, nb, dtype=torch.bool), 1 / 8))
-    with pytest.raises(NotImplementedError):
-        proc.forward_backup(q, k, v)
