@@ -95,6 +95,11 @@ def cpu_baseline(q, k, v, kv, sm_scale, eff_flops_total, n_heads_sample=30):
     }
 
 
+def _progress(msg):
+    """One progress line per finished configuration on stderr (stdout carries only the JSON)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def _tflops(flops, ms):
     return round(flops / (ms * 1e-3) / 1e12, 2)
 
@@ -119,6 +124,8 @@ def other_configs(q, k, v, dev):
     out["c1"] = {"ms": round(ms, 4), "tflops": _tflops(f1, ms), "block_density": round(m1.float().mean().item(), 4),
                  "dtype": "bf16 (the fp32 inputs of the configuration rounded to bf16: the kernel takes bf16)"}
 
+    _progress("c1 done")
+
     # C3: combined mask (local window U global top-10% U text) + attention.
     proc = CombinedAttn(warmup_epoch=0)
     proc(q, k, v)
@@ -130,6 +137,8 @@ def other_configs(q, k, v, dev):
                  "attn_tflops": _tflops(f3, ms3_attn), "sparsity": round(proc.sparsity(), 4),
                  "effective_tflop_per_call": round(f3 / 1e12, 4)}
 
+    _progress("c3 done")
+
     # SparseGen_Plus on the C2 inputs (a sparse step after warm-up, schedule step 10):
     # sampled block scores (num_keep 8) -> energy kv lists -> block-sparse attention.
     from sparseattnfunctions_amd import SparseGen_Plus as sgp
@@ -138,7 +147,7 @@ def other_configs(q, k, v, dev):
     sg = sgp.BlockSparseAttention(warmup_epoch=0, verbose=False)
     sg.counter = 10 * sg.layernum
     sg.forward(q, k, v)
-    kvs = sg.mask[0]
+    kvs = sg.mask.kv(0)
     thr = float(sg.energy_threshold_list[10])
     fs = 4 * D * kvs.computed_pairs(L, L)
     ms_est = time_fn(lambda: calc_attn_block_sum_efficient(q, k, num_keep=8))
@@ -152,6 +161,8 @@ def other_configs(q, k, v, dev):
                              "energy_lists_ms": round(ms_sel, 4), "attn_ms": round(ms_attn, 4),
                              "attn_tflops": _tflops(fs, ms_attn), "sparsity": round(sg._calculate_sparsity(kvs), 4),
                              "effective_tflop_per_call": round(fs / 1e12, 4)}
+
+    _progress("sparsegen_plus done")
 
     # Pooled-attention map (attn_with_pooling, block_size 64) on the C2 inputs: dense attention
     # that also returns the normalised 2-D max-pooled probabilities, against the same kernel
@@ -169,6 +180,8 @@ def other_configs(q, k, v, dev):
                            "dense_attention_ms": round(ms_dense, 4), "causal_ms": round(ms_pool_causal, 4),
                            "block_size": 64}
     del kv_all
+
+    _progress("attn_pooling done")
 
     # 1.5-5B geometry (B=2, H=48, L=45104): unified_judge and the frame-pattern attention on
     # every head (synthetic inputs drawn on the GPU).
@@ -201,6 +214,8 @@ def other_configs(q, k, v, dev):
                            "routed_call_ms": round(ms_routed, 3), "routed_pattern_heads": n_pattern_heads}
     del q6, k6, v6, routed
 
+    _progress("pattern_1_5b done")
+
     # Sliding-tile attention (default config) on the C2 inputs: the fused call (query and
     # output permutations inside the kernel) against permute-copies + attention + copy back.
     from sparseattnfunctions_amd._kv import KVList
@@ -214,6 +229,8 @@ def other_configs(q, k, v, dev):
     ms_sta_copies = time_fn(lambda: sta.process_out_back(sta.attention(*sta.preprocess(q, k, v))))
     out["sta"] = {"ms": round(ms_sta, 4), "tflops": _tflops(f_sta, ms_sta), "copies_ms": round(ms_sta_copies, 4),
                   "block_density": round(lay.density(), 4), "block_tflop_per_call": round(f_sta / 1e12, 4)}
+
+    _progress("sta done")
 
     # C4: token merging (seed 3), r = 4000 -> 13776 tokens, biased dense attention, unmerge.
     q4, k4, v4 = (t.to(dev) for t in cogvideox_qkv(3))
@@ -240,6 +257,8 @@ def other_configs(q, k, v, dev):
                  "attention_tflop_per_call": round(f4 / 1e12, 4)}
     del q4, k4, v4, qm
 
+    _progress("c4 done")
+
     # C5: one denoising step = 30 layers of config-3 attention, each with its own inputs
     # drawn as config 2 with seed = layer index (CPU generator; drawn in a thread pool and
     # moved to the GPU before the timed region).
@@ -260,6 +279,7 @@ def other_configs(q, k, v, dev):
     out["c5"] = {"ms_per_step": round(ms5, 3), "tflops": _tflops(f5, ms5),
                  "effective_tflop_per_step": round(f5 / 1e12, 3)}
     del layers
+    _progress("c5 done")
     return out
 
 

@@ -16,7 +16,7 @@ by design:
   * the warm-up steps run dense attention through the same kernel (every block kept) instead
     of SageAttention's quantized kernel, which this build does not ship;
   * block scores are fp32 (see utils/mask_related.py of this package);
-  * `mask` entries are kv lists (KVList); `KVList.to_mask()` gives the dense mask.
+  * `mask[layer]` gives the bool block mask built from the cached kv lists (`mask.kv(layer)`).
 """
 from __future__ import annotations
 
@@ -27,7 +27,7 @@ import os
 import numpy as np
 import torch
 
-from ._kv import KVList
+from ._kv import KVList, kv_list_from_mask
 from .block_mask_attn import dense_kv_list
 from .estimator import energy_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
@@ -75,6 +75,37 @@ class _RngGuard:
         return False
 
 
+class LayerMasks:
+    """Per-layer cache of the last sparse step's block masks (the reference's `self.mask`
+    list, SparseGen_Plus.py:117, 165-172). Item access returns the reference's bool
+    [B, H, nqb, nkb] block mask (None before the layer's first sparse step), formed from the
+    kv lists the kernel uses; `kv(layer)` returns those lists. A bool/0-1 mask assigned to
+    an item is converted to kv lists."""
+
+    def __init__(self, n: int):
+        self._kv = [None] * n
+
+    def __len__(self):
+        return len(self._kv)
+
+    def __getitem__(self, layer):
+        kv = self._kv[layer]
+        return None if kv is None else kv.to_mask()
+
+    def __setitem__(self, layer, value):
+        if value is None or isinstance(value, KVList):
+            self._kv[layer] = value
+            return
+        B, H, nqb, nkb = value.shape
+        self._kv[layer] = kv_list_from_mask(value, B, H, nqb, nkb)
+
+    def __iter__(self):
+        return (self[i] for i in range(len(self)))
+
+    def kv(self, layer):
+        return self._kv[layer]
+
+
 class BlockSparseAttention:
     def __init__(self, block_size=64, layernum=42, timestep=50, num_samples=1, warmup_epoch=5,
                  verbose=True, record_dir="."):
@@ -89,7 +120,7 @@ class BlockSparseAttention:
         self.sparsity_records = [self._init_sparsity_dict() for _ in range(num_samples)]
         self.update_list = []
         self.warmup_epoch = warmup_epoch
-        self.mask = [None] * layernum
+        self.mask = LayerMasks(layernum)
         self.k_list = [0.3, 0.2, 0.15, 0.1]
         self.max_retain_ratio_list = concentrated_interpolation(0.8, 1, 50, concentration=0.5)
         self.min_retain_ratio_list = concentrated_interpolation(0.1, 0.12, 50, concentration=0.5)
@@ -156,7 +187,7 @@ class BlockSparseAttention:
             out = self.forward(q, k, v)
         self.counter += 1
         if self.need_update(self.counter):
-            self.mask = [None] * self.layernum
+            self.mask = LayerMasks(self.layernum)
         if self.counter % (self.layernum * self.timestep) == 0:
             sample_idx = self.counter // (self.layernum * self.timestep) - 1
             self._save_sparsity_records(sample_idx)

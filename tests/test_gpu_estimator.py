@@ -146,9 +146,11 @@ def test_sparsegen_processor_end_to_end(dev, tmp_path):
         if call < 2:  # timestep 0 < warmup_epoch: dense
             want = masked_attention(q, k, v, full, 1 / 8)
         else:
-            kv = proc.mask[call % 2]
-            want = masked_attention(q, k, v, kv.to_mask().cpu(), 1 / 8)
-            m = kv.to_mask().cpu()
+            kv = proc.mask.kv(call % 2)
+            m = proc.mask[call % 2].cpu()  # the reference's bool [B, H, nb, nb] view
+            assert m.dtype == torch.bool and m.shape == (1, 2, nb, nb)
+            assert torch.equal(m, kv.to_mask().cpu())
+            want = masked_attention(q, k, v, m, 1 / 8)
             assert m[:, :, :4].all() and m[:, :, :, :4].all()
         err = (out.float().cpu().double() - want).abs()
         assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
