@@ -67,7 +67,8 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
  * block (:87-89), fp32 online softmax, P rounded to bf16 before P.V (:107), no causal
  * mask, query-block m uses mask row m (:155). A query block with an empty list writes 0
  * (the reference divides by l=0 and writes NaN, :201-203).
- *   q [B,H,Lq,64], k/v [B,H,Lk,64], out [B,H,Lq,64]: bf16, strides as above.
+ *   q [B,H,Lq,D], k/v [B,H,Lk,D], out [B,H,Lq,D]: bf16, strides as above; D = 64 or 128,
+ *             the head dims the reference accepts (:231).
  *   kv_idx/kv_cnt: lists for B*H*ceil(Lq/64) rows (row = (b*H + h)*nqb + m); entries
  *             outside [0, ceil(Lk/64)) are skipped, counts are clamped to [0, max_cnt].
  *   key_bias  nullable fp32, element [b*bias_strides[0] + h*bias_strides[1] + key]:
@@ -85,8 +86,21 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         const int32_t* work_order, int64_t n_slots, void* stream);
 
 /*
- * Block-sparse attention with token-level masks inside cut blocks: as sa_block_sparse_fwd,
- * plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
+ * sa_block_sparse_fwd for fp16 q, k, v and out (the reference kernel runs on either 16-bit
+ * type: P is rounded to v's dtype, :107): same arguments and contract, D = 64 or 128, with the
+ * fp16 MFMA and P rounded to fp16. Every item runs with the running row maximum (fp16 P has
+ * too little exponent range for the unshifted exp2 that bf16 launches try first).
+ */
+int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                            const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                            uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                            int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                            const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                            const int32_t* work_order, int64_t n_slots, void* stream);
+
+/*
+ * Block-sparse attention with token-level masks inside cut blocks: as sa_block_sparse_fwd
+ * (bf16, head dim 64), plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
  * bitmask in tile_masks (uint64 [slots][64]: bit c of word r = query r of the block may
  * attend key c). Replaces flex_attention with a BlockMask built from a mask_mod
  * (SildingTileAttention.py:88-106, 146), which also masks element-wise inside partial blocks.

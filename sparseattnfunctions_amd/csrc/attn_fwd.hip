@@ -124,6 +124,38 @@ __device__ inline float dot2_bf16_ones(uint32_t pair, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(sa_bf16x2, pair), ones, acc, false);
 }
 
+typedef _Float16 sa_f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 sa_f16x8 __attribute__((ext_vector_type(8)));
+
+// Operand element type of a launch: the MFMA, the rounding of P (and of the output) to the
+// element type (round to nearest even), and the row-sum dot of a packed pair with ones.
+template <typename T>
+struct Elem;
+template <>
+struct Elem<__bf16> {
+  typedef sa_bf16x8 v8;
+  __device__ static inline v8 as8(sa_u32x4v x) { return as_bf16x8(x); }
+  __device__ static inline sa_f32x16 mfma(v8 a, v8 b, sa_f32x16 c) { return mfma32(a, b, c); }
+  __device__ static inline uint32_t pack(float a, float b) { return cvt_pk_bf16(a, b); }
+  __device__ static inline float dot2_ones(uint32_t pair, float acc) { return dot2_bf16_ones(pair, acc); }
+};
+template <>
+struct Elem<_Float16> {
+  typedef sa_f16x8 v8;
+  __device__ static inline v8 as8(sa_u32x4v x) { return __builtin_bit_cast(sa_f16x8, x); }
+  __device__ static inline sa_f32x16 mfma(v8 a, v8 b, sa_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack(float a, float b) {  // v_cvt_pk_f16_f32
+    const sa_f16x2 r = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ static inline float dot2_ones(uint32_t pair, float acc) {
+    const sa_f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(sa_f16x2, pair), ones, acc, false);
+  }
+};
+
 // max / sum of x over lanes l and l ^ 32 (v_permlane32_swap: no LDS traffic).
 __device__ inline float xhalf_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -195,18 +227,29 @@ __device__ __forceinline__ void lgkm_wait_pair(int n, sa_u32x2v& a, sa_u32x2v& b
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 constexpr int kWaitLgkm0 = 0xC07F;
 
-template <bool kBias, bool kMask, int kPool>
-__global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
+// T: bf16 or fp16 operands (and output). kD: head dim 64 or 128. A 128-dim row is staged as
+// two 128-byte half rows in two half tiles with the 64-dim layout, so every read pattern of
+// the 64-dim kernel applies per half; at 128 dims a wave holds ~420 registers, so one
+// workgroup (one wave per SIMD) runs per CU.
+template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64>
+__global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs a) {
   static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
+  static_assert(kD == 64 || kD == 128, "head dim 64 or 128");
+  static_assert((kD == 64 && std::is_same<T, __bf16>::value) || (!kMask && kPool == 0),
+                "tile masks and pooling: bf16, head dim 64");
+  typedef Elem<T> E;
+  constexpr int kDS = kD / 16;     // 16-wide d steps of S = K Q^T
+  constexpr int kDC = kD / 32;     // 32-row d chunks of O^T
+  constexpr int kHalves = kD / 64;  // 128-byte half rows per token
   // Separate LDS objects for K, V and bias so that the compiler's own wait analysis can
   // tell a copy into one from a read of another.
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kWaves * kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes * kHalves];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kWaves * kTileBytes * kHalves];
   __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * kBlock : 4];
-  // Vector-memory operations per tile, in issue order: group K = [mask rows (2)] [K (8)],
-  // group V = [bias (1)] [V (8)]. The waits below count them.
-  constexpr int kGroupK = 8 + (kMask ? 2 : 0);
-  constexpr int kGroupV = 8 + (kBias ? 1 : 0);
+  // Vector-memory operations per tile, in issue order: group K = [mask rows (2)] [K (8 per
+  // half)], group V = [bias (1)] [V (8 per half)]. The waits below count them.
+  constexpr int kGroupK = 8 * kHalves + (kMask ? 2 : 0);
+  constexpr int kGroupV = 8 * kHalves + (kBias ? 1 : 0);
 
   const int lane = threadIdx.x & 63;
   // Wave-uniform values are made provably uniform (readfirstlane) so that the list, slot
@@ -241,8 +284,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
   const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
   const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
-  lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes;
-  lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes;
+  lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes * kHalves;
+  lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes * kHalves;
   float* bl_lds = b_lds + (kBias ? wave * kBlock : 0);
 
   // Lane constants: copy offsets, K operand read offsets, V^T transposed read offsets.
@@ -280,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   // Q^T B operands: qf[g][s] = q[qb*64 + 32g + col][16s + 8hh .. +7] (rows clamped into Lq;
   // clamped rows are never stored). With a row map, query i reads q row q_rows[i] (zeros
   // when that is outside the tensor: padding rows of a remapped layout).
-  sa_bf16x8 qf[2][4];
+  typename E::v8 qf[2][kDS];
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     int row = min(qb * kBlock + 32 * g + col, a.Lq - 1);
@@ -292,13 +335,13 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     }
     const uint16_t* p = qbase + (int64_t)row * a.q_sl + 8 * hh;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kDS; ++s) {
       const uint4 w = *reinterpret_cast<const uint4*>(p + 16 * s);
-      qf[g][s] = as_bf16x8(zero ? make_uint4(0u, 0u, 0u, 0u) : w);
+      qf[g][s] = __builtin_bit_cast(typename E::v8, zero ? make_uint4(0u, 0u, 0u, 0u) : w);
     }
   }
 
-  sa_f32x16 acc[2][2];  // [dc][g]
+  sa_f32x16 acc[kDC][2];  // [dc][g]
   float m[2];
   float l[2];
 
@@ -316,7 +359,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       mw[0] = mrow[col];
       mw[1] = mrow[32 + col];
     }
-    dma_tile(khead, kbytes, kb0 * krow, krow, kgo, kl);
+#pragma unroll
+    for (int hf = 0; hf < kHalves; ++hf) dma_tile(khead + 64 * hf, kbytes, kb0 * krow, krow, kgo, kl + hf * kTileBytes);
   };
   // Group V of tile `kb`: bias copy (keys past Lk read as zero), V copy.
   auto issue_v = [&](int kb) {
@@ -326,7 +370,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
                                                                           a.Lk * 4, 0x00020000);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_u8*)bl_lds, 4, (kb0 + lane) * 4, 0, 0, 0);
     }
-    dma_tile(vhead, vbytes, kb0 * vrow, vrow, vgo, vl);
+#pragma unroll
+    for (int hf = 0; hf < kHalves; ++hf) dma_tile(vhead + 64 * hf, vbytes, kb0 * vrow, vrow, vgo, vl + hf * kTileBytes);
   };
 
   // One pass over the item's key blocks. Fast pass (kSafe = false): P = exp2(S) with no
@@ -337,7 +382,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
   auto run = [&](auto safe_tag) {
     constexpr bool kSafe = decltype(safe_tag)::value;
 #pragma unroll
-    for (int dc = 0; dc < 2; ++dc)
+    for (int dc = 0; dc < kDC; ++dc)
 #pragma unroll
       for (int g = 0; g < 2; ++g) acc[dc][g] = sa_f32x16{};
     m[0] = m[1] = -INFINITY;
@@ -359,11 +404,11 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
 
       // ---- K operands of this tile, then request the next tile's group K.
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupV));
-      sa_u32x4v kop[2][4];
+      sa_u32x4v kop[2][kDS];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kop[c][s] = lds_read_b128(kl + kro[s] + 4096 * c);
+        for (int s = 0; s < kDS; ++s) kop[c][s] = lds_read_b128(kl + (s >> 2) * kTileBytes + kro[s & 3] + 4096 * c);
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
       issue_k(kb_next, it_next);
 
@@ -376,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
         for (int g = 0; g < 2; ++g) {
           sa_f32x16 t = {};
 #pragma unroll
-          for (int s = 0; s < 4; ++s) t = mfma32(as_bf16x8(kop[c][s]), qf[g][s], t);
+          for (int s = 0; s < kDS; ++s) t = E::mfma(E::as8(kop[c][s]), qf[g][s], t);
           S[g][c] = t;
         }
       
@@ -469,7 +514,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
             m[g] = m_new;
             l[g] *= alpha;
 #pragma unroll
-            for (int dc = 0; dc < 2; ++dc) acc[dc][g] *= alpha;
+            for (int dc = 0; dc < kDC; ++dc) acc[dc][g] *= alpha;
           }
         }
 #pragma unroll
@@ -484,8 +529,8 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
           for (int e = 0; e < 16; e += 2) {
             const float p0 = fast_exp2(kSafe ? fmaf(S[g][c][e], sc, -mu[g]) : S[g][c][e] * sc);
             const float p1 = fast_exp2(kSafe ? fmaf(S[g][c][e + 1], sc, -mu[g]) : S[g][c][e + 1] * sc);
-            P[g][c][e >> 1] = cvt_pk_bf16(p0, p1);
-            l[g] = dot2_bf16_ones(P[g][c][e >> 1], l[g]);
+            P[g][c][e >> 1] = E::pack(p0, p1);
+            l[g] = E::dot2_ones(P[g][c][e >> 1], l[g]);
           }
 
       // ---- V^T operands of this tile, then request the next tile's V.
@@ -494,39 +539,43 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       // waits only for its own two reads (LDS reads return in order; the full wait first
       // leaves no scalar load outstanding, so the counts are exact). The next tile's V
       // copy overwrites this buffer, so it is requested after the last read has landed.
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      sa_u32x2v vr[2][2][2][2];  // [c][u][dc][t]
+      // At 128 dims each half tile (d chunks 2hp, 2hp + 1) is read and consumed in turn.
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int hp = 0; hp < kHalves; ++hp) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        sa_u32x2v vr[2][2][2][2];  // [c][u][dc][t]
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int dc = 0; dc < 2; ++dc)
+          for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const uint32_t base = (uint32_t)(uintptr_t)(vl + vro[dc][t]);
-              vr[c][u][dc][t] = (c == 0 ? (u == 0 ? lds_read_tr16_asm<0>(base) : lds_read_tr16_asm<2048>(base))
-                                        : (u == 0 ? lds_read_tr16_asm<4096>(base) : lds_read_tr16_asm<6144>(base)));
-            }
+            for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                const uint32_t base = (uint32_t)(uintptr_t)(vl + hp * kTileBytes + vro[dc][t]);
+                vr[c][u][dc][t] = (c == 0 ? (u == 0 ? lds_read_tr16_asm<0>(base) : lds_read_tr16_asm<2048>(base))
+                                          : (u == 0 ? lds_read_tr16_asm<4096>(base) : lds_read_tr16_asm<6144>(base)));
+              }
 
-      // ---- O^T += V^T P^T over the tile's four 16-key steps.
+        // ---- O^T += V^T P^T over the tile's four 16-key steps.
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+          for (int u = 0; u < 2; ++u)
 #pragma unroll
-          for (int dc = 0; dc < 2; ++dc) {
-            constexpr int kReads = 16;
-            const int done = 2 * ((c * 2 + u) * 2 + dc) + 2;  // reads this MFMA pair needs
-            lgkm_wait_pair(kReads - done, vr[c][u][dc][0], vr[c][u][dc][1]);
-            const sa_u32x4v vop = {vr[c][u][dc][0].x, vr[c][u][dc][0].y, vr[c][u][dc][1].x, vr[c][u][dc][1].y};
+            for (int dc = 0; dc < 2; ++dc) {
+              constexpr int kReads = 16;
+              const int done = 2 * ((c * 2 + u) * 2 + dc) + 2;  // reads this MFMA pair needs
+              lgkm_wait_pair(kReads - done, vr[c][u][dc][0], vr[c][u][dc][1]);
+              const sa_u32x4v vop = {vr[c][u][dc][0].x, vr[c][u][dc][0].y, vr[c][u][dc][1].x, vr[c][u][dc][1].y};
 #pragma unroll
-            for (int g = 0; g < 2; ++g)
-              acc[dc][g] = mfma32(as_bf16x8(vop),
-                                  as_bf16x8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
-                                                      P[g][c][4 * u + 3]}),
-                                  acc[dc][g]);
-          }
+              for (int g = 0; g < 2; ++g)
+                acc[2 * hp + dc][g] = E::mfma(E::as8(vop),
+                                              E::as8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
+                                                               P[g][c][4 * u + 3]}),
+                                              acc[2 * hp + dc][g]);
+            }
+      }
       issue_v(kb_next);
 
       it = it + 1;
@@ -537,10 +586,13 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
 
-  run(std::false_type{});
+  // fp16 P has a narrow exponent range: fp16 launches run the safe pass only.
+  constexpr bool kFast = std::is_same<T, __bf16>::value;
+  if (kFast) run(std::false_type{});
+  else run(std::true_type{});
   // The fast pass is exact unless a row's sum left [2^-90, 2^90] (scores far from 0, where
   // exp2 would lose range) or an accumulator overflowed; then redo the item safely.
-  if (cnt > 0) {
+  if (kFast && cnt > 0) {
     bool bad = false;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -548,7 +600,7 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
       bad |= !(l_tot >= 0x1p-90f && l_tot <= 0x1p90f);
       float amax = 0.f;
 #pragma unroll
-      for (int dc = 0; dc < 2; ++dc)
+      for (int dc = 0; dc < kDC; ++dc)
 #pragma unroll
         for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][g][e])), fabsf(acc[dc][g][e + 1]));
       bad |= !(amax <= 3.0e38f);
@@ -578,14 +630,13 @@ __global__ __launch_bounds__(256, 2) void bsa_fwd_kernel(FwdArgs a) {
     if (store) {
       uint16_t* orow = obase + (int64_t)row * a.o_sl;
 #pragma unroll
-      for (int dc = 0; dc < 2; ++dc) {
+      for (int dc = 0; dc < kDC; ++dc) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const sa_f32x16& A = acc[dc][g];
           // element 4q4 + j is d = 32dc + 8q4 + 4hh + j
           *reinterpret_cast<uint2*>(orow + 32 * dc + 8 * q4 + 4 * hh) =
-              make_uint2(cvt_pk_bf16(A[4 * q4] * inv, A[4 * q4 + 1] * inv),
-                         cvt_pk_bf16(A[4 * q4 + 2] * inv, A[4 * q4 + 3] * inv));
+              make_uint2(E::pack(A[4 * q4] * inv, A[4 * q4 + 1] * inv), E::pack(A[4 * q4 + 2] * inv, A[4 * q4 + 3] * inv));
         }
       }
     }
@@ -701,11 +752,13 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
                const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
-               float* pool_lse = nullptr, const PoolOut* pool_out = nullptr) {
+               float* pool_lse = nullptr, const PoolOut* pool_out = nullptr, bool fp16 = false) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
-  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (only 64)", fn, D);
+  if (D != 64 && D != 128) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", fn, D);
+  if ((D != 64 || fp16) && (kv_slot || pool_cols))
+    return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks and pooling need bf16 and head_dim 64", fn);
   SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f, "%s: sm_scale must be finite and > 0", fn);
   const int nqb = sa::cdiv(Lq, kBlock);
   const int nkb = sa::cdiv(Lk, kBlock);
@@ -734,7 +787,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   }
   // K/V tiles are copied through 32-bit buffer offsets relative to each head's first row.
   for (const int64_t* st : {k_strides, v_strides}) {
-    if ((int64_t)(Lk - 1) * st[2] * 2 + 2 * kHeadDim > INT_MAX)
+    if ((int64_t)(Lk - 1) * st[2] * 2 + 2 * D > INT_MAX)
       return sa::fail(SA_ERR_UNSUPPORTED, "%s: key rows of one head span more than 2 GiB", fn);
   }
   const int64_t grid = n_slots / kWaves;
@@ -781,6 +834,19 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
 
   hipStream_t s = sa::as_stream(stream);
   const dim3 g((unsigned)grid), blk(64 * kWaves);
+  if (fp16 || D == 128) {
+    if (fp16 && D == 64) {
+      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, _Float16, 64>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, _Float16, 64>), g, blk, 0, s, a);
+    } else if (fp16) {
+      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, _Float16, 128>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, _Float16, 128>), g, blk, 0, s, a);
+    } else {
+      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, __bf16, 128>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, __bf16, 128>), g, blk, 0, s, a);
+    }
+    return sa::check_launch(fn);
+  }
   if (kv_slot) {
     if (key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
     if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 32>), g, blk, 0, s, a);
@@ -808,6 +874,17 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
                     0, nullptr, 0, stream, "sa_block_sparse_fwd");
+}
+
+extern "C" int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                       const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                       uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                       int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                       const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                       const int32_t* work_order, int64_t n_slots, void* stream) {
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
+                    0, nullptr, 0, stream, "sa_block_sparse_fwd_f16", 1, 0, nullptr, nullptr, nullptr, true);
 }
 
 extern "C" int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,

@@ -9,8 +9,11 @@ Mirrors special_attentions/utils/block_sparse_attn_kernel.py of xiaolong-li1/Spa
 The name keeps "triton" for source compatibility; the work runs in the HIP kernels of
 libsa_hip.so (`sa_mask_to_kv_list` + `sa_block_sparse_fwd`), not Triton.
 
+Inputs are bf16 or fp16 (all three the same), head_dim 64 or 128 as the reference asserts
+(:231); P is rounded to the input dtype before P.V as the reference rounds it to v's (:107).
+
 Differences from the reference, by design:
-  * head_dim 64 only (the reference also accepts 128, :231) -> NotImplementedError;
+  * fp32 inputs are not accepted (the reference's tl.dot would take them): TypeError;
   * a query block whose mask row is empty yields 0 instead of NaN (:201-203);
   * sm_scale must be > 0.
 """
@@ -27,10 +30,11 @@ from .._kv import KVList, kv_list_from_mask
 BLOCK = 64
 
 
-def _prep_qkv(t: torch.Tensor) -> torch.Tensor:
-    """bf16, last dim contiguous, 16-byte aligned rows (the kernel's vector loads)."""
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"expected bfloat16 tensors, got {t.dtype}")
+def _prep_qkv(t: torch.Tensor, dtypes=(torch.bfloat16,)) -> torch.Tensor:
+    """bf16 (or another of `dtypes`), last dim contiguous, 16-byte aligned rows (the kernel's
+    vector loads)."""
+    if t.dtype not in dtypes:
+        raise TypeError(f"expected {' or '.join(str(d) for d in dtypes)} tensors, got {t.dtype}")
     if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
         t = t.contiguous()
     return t
@@ -69,9 +73,10 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                            n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
-    q [B,H,Lq,64], k/v [B,H,Lk,64] bf16 on the GPU; key_bias optional fp32 [B,H,Lk] (any
-    strides with a contiguous key axis, stride 0 to broadcast). `n_text_blocks` only
-    affects scheduling (those block rows are dispatched first).
+    q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128;
+    key_bias optional fp32 [B,H,Lk] (any strides with a contiguous key axis, stride 0 to
+    broadcast). `n_text_blocks` only affects scheduling (those block rows are dispatched
+    first). Row maps and tile masks need bf16 and D = 64.
 
     Layout remapping inside the kernel (no copies): with `q_rows` (int32 [n]) the attention
     runs over n logical query rows, row i reading q's row q_rows[i] (zeros outside q); with
@@ -80,7 +85,11 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     lists_shared) adds token-level masks inside cut blocks.
     """
     _lib.require_gpu(q, k, v)
-    q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
+    half = (torch.bfloat16, torch.float16)
+    q, k, v = _prep_qkv(q, half), _prep_qkv(k, half), _prep_qkv(v, half)
+    if not q.dtype == k.dtype == v.dtype:
+        raise TypeError(f"q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    fp16 = q.dtype == torch.float16
     B, H, Lsrc, D = q.shape
     q_rows, o_rows = _row_map(q_rows, q.device), _row_map(o_rows, q.device)
     Lq = q_rows.numel() if q_rows is not None else (o_rows.numel() if o_rows is not None else Lsrc)
@@ -108,6 +117,8 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
         bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
     order = work_order(B, H, math.ceil(Lq / BLOCK), n_text_blocks, q.device)
     lib = _lib.load()
+    if fp16 and (q_rows is not None or o_rows is not None or tile_masks is not None):
+        raise NotImplementedError("row maps and tile masks need bf16 inputs")
     if q_rows is not None or o_rows is not None or tile_masks is not None:
         kv_slot, masks = (tile_masks[0], tile_masks[1]) if tile_masks is not None else (None, None)
         with torch.cuda.device(q.device):
@@ -120,8 +131,9 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                 _lib.stream_of(q))
         _lib.check(rc, "sa_block_sparse_fwd_mapped")
         return out
+    fn = "sa_block_sparse_fwd_f16" if fp16 else "sa_block_sparse_fwd"
     with torch.cuda.device(q.device):
-        rc = lib.sa_block_sparse_fwd(
+        rc = getattr(lib, fn)(
             q.data_ptr(), _lib.i64(*q.stride()[:3]),
             k.data_ptr(), _lib.i64(*k.stride()[:3]),
             v.data_ptr(), _lib.i64(*v.stride()[:3]),
@@ -132,7 +144,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
             order.data_ptr(), order.numel(),
             _lib.stream_of(q),
         )
-    _lib.check(rc, "sa_block_sparse_fwd")
+    _lib.check(rc, fn)
     return out
 
 

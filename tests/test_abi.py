@@ -51,7 +51,7 @@ def test_bad_shapes_rejected(lib):
     dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     s3 = _lib.i64(0, 0, 0)
     args = [dummy, s3, dummy, s3, dummy, s3, dummy, s3]
-    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 128, dummy, dummy, 2, None, None, 0.125, None, 0, None)
+    rc = lib.sa_block_sparse_fwd(*args, 1, 1, 64, 64, 96, dummy, dummy, 2, None, None, 0.125, None, 0, None)
     assert rc == _lib.SA_ERR_UNSUPPORTED and b"head_dim" in lib.sa_last_error()
     rc = lib.sa_block_sparse_fwd(*args, 0, 1, 64, 64, 64, dummy, dummy, 2, None, None, 0.125, None, 0, None)
     assert rc == _lib.SA_ERR_INVALID

@@ -244,3 +244,56 @@ def test_cogvideox_shape_subset_of_heads(dev):
                                            torch.randint(256, L, (31,), generator=g), torch.tensor([L - 1])]))
             w = masked_attention(q, k, v, mask, 0.125, heads=[(b, h)], rows=rows)[b, h]
             _check(out[b, h, rows], w)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128), (torch.float16, 128)])
+def test_fp16_and_head_dim_128(dev, dtype, D):
+    # The reference accepts head_dim 64 or 128 (:231) and any 16-bit input type (P is rounded
+    # to v's dtype, :107). Partial last block, Lq < Lk, a random mask with an empty row.
+    case(f"dtype={dtype} D={D}")
+    for (Lq, Lk, seed) in [(257, 257, 1), (200, 385, 2)]:
+        q = _rand((2, 3, Lq, D), 100 + seed, dtype)
+        k = _rand((2, 3, Lk, D), 110 + seed, dtype)
+        v = _rand((2, 3, Lk, D), 120 + seed, dtype)
+        nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+        g = torch.Generator().manual_seed(seed)
+        mask = torch.rand(2, 3, nqb, nkb, generator=g) < 0.5
+        mask[:, :, :, 0] = True
+        mask[1, 2, 1] = False  # an empty row writes 0
+        scale = 1 / math.sqrt(D)
+        out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+        assert out.dtype == dtype and out.shape == q.shape
+        _check(out, masked_attention(q, k, v, mask, scale))
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128)])
+def test_fp16_and_head_dim_128_key_bias(dev, dtype, D):
+    case(f"key bias dtype={dtype} D={D}")
+    q, k, v = (_rand((1, 2, 300, D), 130 + i, dtype) for i in range(3))
+    bias = torch.log(torch.randint(1, 5, (1, 2, 300), generator=torch.Generator().manual_seed(3)).float())
+    nb = math.ceil(300 / 64)
+    kv = kv_list_from_mask(torch.ones(1, 1, nb, nb, dtype=torch.bool, device=dev), 1, 2, nb, nb)
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 1 / 8, key_bias=bias.to(dev))
+    _check(out, masked_attention(q, k, v, torch.ones(1, 1, nb, nb, dtype=torch.bool), 1 / 8, key_bias=bias.double()))
+
+
+def test_fp16_large_scores_use_running_max(dev):
+    # fp16 P cannot hold exp2 of raw scores of several hundred: fp16 launches always subtract
+    # the running row maximum (the bf16 fast pass would overflow fp16).
+    case("fp16 large scores")
+    q = (_rand((1, 1, 128, 64), 140) * 6).half()
+    k = (_rand((1, 1, 128, 64), 141) * 6).half()
+    v = _rand((1, 1, 128, 64), 142, torch.float16)
+    mask = torch.ones(1, 1, 2, 2, dtype=torch.bool)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 1 / 8)
+    _check(out, masked_attention(q, k, v, mask, 1 / 8))
+
+
+def test_mixed_or_fp32_dtypes_rejected(dev):
+    case("dtype errors")
+    q = _rand((1, 1, 64, 64), 150).to(dev)
+    m = torch.ones(1, 1, 1, 1, dtype=torch.bool, device=dev)
+    with pytest.raises(TypeError):
+        block_sparse_triton_fn(q, q.half(), q, m, 1 / 8)
+    with pytest.raises(TypeError):
+        block_sparse_triton_fn(q.float(), q.float(), q.float(), m, 1 / 8)
