@@ -107,7 +107,8 @@ def _tflops(flops, ms):
 def other_configs(q, k, v, dev):
     """The other BASELINE configurations, each timed with HIP events (reported, not `value`)."""
     from sparseattnfunctions_amd import _tome
-    from sparseattnfunctions_amd._kv import kv_list_from_mask
+    from sparseattnfunctions_amd._kv import KVList, kv_list_from_mask
+    from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention, dense_kv_list
     from sparseattnfunctions_amd.combined_attn import CombinedAttn
     from sparseattnfunctions_amd.MergeAttention import MergeAttention
     from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention, block_sparse_triton_fn
@@ -258,6 +259,48 @@ def other_configs(q, k, v, dev):
     del q4, k4, v4, qm
 
     _progress("c4 done")
+
+    # The reference's own performance test (block_sparse_attn_kernel.py:402-490,
+    # test_performance_no_mask): B=2, H=30, d=64, bf16, an all-ones block mask through the
+    # block-sparse kernel against flash attention (torch SDPA here), L from 2 560 to 40 960,
+    # with the max-abs difference of the two outputs.
+    sweep = []
+    for L_s in (2560, 5120, 10240, 20480, 40960):
+        gs = torch.Generator(device=dev).manual_seed(L_s)
+        qs_, ks_, vs_ = (torch.randn(2, 30, L_s, 64, device=dev, generator=gs).to(torch.bfloat16) for _ in range(3))
+        nb_s = math.ceil(L_s / 64)
+        kv_s = dense_kv_list(2, 30, nb_s, nb_s, dev)
+        ms_bs = time_fn(lambda: block_sparse_attention(qs_, ks_, vs_, kv_s, 1 / 8))
+        ms_fa = time_fn(lambda: torch.nn.functional.scaled_dot_product_attention(qs_, ks_, vs_))
+        diff = (block_sparse_attention(qs_, ks_, vs_, kv_s, 1 / 8).float()
+                - torch.nn.functional.scaled_dot_product_attention(qs_, ks_, vs_).float()).abs().max().item()
+        f_s = 4 * 64 * 60 * L_s * L_s
+        sweep.append({"seq_len": L_s, "blocksparse_ms": round(ms_bs, 4), "blocksparse_tflops": _tflops(f_s, ms_bs),
+                      "sdpa_ms": round(ms_fa, 4), "speedup_vs_sdpa": round(ms_fa / ms_bs, 3),
+                      "max_abs_diff_vs_sdpa": round(diff, 5)})
+        del qs_, ks_, vs_, kv_s
+    out["reference_perf_no_mask"] = sweep
+    _progress("reference_perf_no_mask done")
+
+    # The kernel's other input types on the C2 kv lists: fp16 q/k/v, and head dim 128 (15 heads
+    # of 128 = the same hidden size 1920, the lists of the first 15 heads of each batch item).
+    kvc = BlockSparseAttention(64, keep_ratio=0.2).build_kv_list(q, k)
+    f_c2 = 4 * D * kvc.computed_pairs(L, L)
+    q16, k16, v16 = q.half(), k.half(), v.half()
+    ms_f16 = time_fn(lambda: block_sparse_attention(q16, k16, v16, kvc, 0.125, n_text_blocks=4))
+    del q16, k16, v16
+    sel = (torch.arange(2)[:, None] * 30 + torch.arange(15)[None, :]).reshape(-1)
+    rows = (sel[:, None] * kvc.nqb + torch.arange(kvc.nqb)[None, :]).reshape(-1).to(dev)
+    kv128 = KVList(kvc.idx[rows].contiguous(), kvc.cnt[rows].contiguous(), 2, 15, kvc.nqb, kvc.nkb)
+    g128 = torch.Generator(device=dev).manual_seed(128)
+    q8, k8, v8 = (torch.randn(2, 15, L, 128, device=dev, generator=g128).to(torch.bfloat16) for _ in range(3))
+    f128 = 4 * 128 * kv128.computed_pairs(L, L)
+    ms_128 = time_fn(lambda: block_sparse_attention(q8, k8, v8, kv128, 1 / math.sqrt(128), n_text_blocks=4))
+    del q8, k8, v8
+    out["attention_variants"] = {"fp16_c2_ms": round(ms_f16, 4), "fp16_c2_tflops": _tflops(f_c2, ms_f16),
+                                 "head_dim_128_ms": round(ms_128, 4), "head_dim_128_tflops": _tflops(f128, ms_128),
+                                 "head_dim_128_shape": [2, 15, L, 128]}
+    _progress("attention_variants done")
 
     # C5: one denoising step = 30 layers of config-3 attention, each with its own inputs
     # drawn as config 2 with seed = layer index (CPU generator; drawn in a thread pool and

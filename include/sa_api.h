@@ -317,6 +317,16 @@ int sa_pattern_combine(const uint16_t* o_frames, const int64_t of_strides[3], co
                        float hi_frame, uint16_t* out, const int64_t out_strides[3], void* stream);
 
 /*
+ * constrained_mod_factor (partern_attention.py:262-315) of a factor tensor x fp32 [BH][L]
+ * (the reference's [B, H, L, 1]): unchanged when every head lies within [lo, hi]; otherwise each
+ * head (range >= 1e-6) is mapped affinely from [min, max] onto [max(min, lo), min(max, hi)],
+ * rescaled to its original sum, and every value is clamped to [lo, hi]. stats fp32 [BH][3]
+ * receives each head's sum, min and max (caller buffer). BH <= 4096.
+ */
+int sa_constrained_mod_factor(const float* x, int BH, int64_t L, float lo, float hi, float* stats,
+                              float* out, void* stream);
+
+/*
  * Softmax probabilities of sampled queries over sampled keys, for the head-routing judges
  * (judge_sparsity / judge_similarity, partern_attention.py:468-514):
  *   P[bh][r][c - c_lo] = softmax_c(q_rows[bh][r] . k_rows[bh][c] * sm_scale + (c < n_bias ? bias : 0))

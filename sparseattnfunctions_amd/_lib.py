@@ -61,6 +61,7 @@ _PROTOTYPES = {
     ),
     "sa_gather_tokens_heads": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _I64P, _P]),
     "sa_pattern_maps": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _P, _P]),
+    "sa_constrained_mod_factor": (_I, [_P, _I, ctypes.c_int64, _F, _F, _P, _P, _P]),
     "sa_sampled_probs": (_I, [_P, _P, _I, _I, _I, _I, _I, _F, _I, _F, _I, _I, _P, ctypes.c_int64, ctypes.c_int64,
                               _P]),
     "sa_topk_share": (_I, [_P, ctypes.c_int64, ctypes.c_int64, _I, _I, _I, _I, _P, _P]),

@@ -381,7 +381,99 @@ int check_bf16_rows(const void* p, const int64_t s[3], const char* fn) {
   return SA_OK;
 }
 
+
+// ---------------------------------------------------------------------------------------
+// constrained_mod_factor (partern_attention.py:262-315) on a standalone factor tensor
+// x [BH][L] fp32. modfac_stats_kernel: one workgroup per head, fixed-order sum (thread t adds
+// entries t, t + 256, ... in order, then a tree over the 256 partials), min and max.
+// modfac_apply_kernel: the "any head out of range" decision from every head's statistics,
+// then per element the affine map of [min, max] onto [max(min, lo), min(max, hi)], the
+// rescale to the original sum (the mapped sum in closed form, (sum - L min) / range *
+// (tmax - tmin) + L tmin), heads with range < 1e-6 unchanged, and the clamp to [lo, hi].
+struct ModStatsArgs {
+  const float* x;
+  int64_t L;
+  float* stats;  // [BH][3]: sum, min, max
+};
+
+__global__ __launch_bounds__(256) void modfac_stats_kernel(ModStatsArgs a) {
+  __shared__ float ps[256], pmn[256], pmx[256];
+  const int64_t bh = blockIdx.x;
+  const int t = threadIdx.x;
+  const float* x = a.x + bh * a.L;
+  float s = 0.f, mn = INFINITY, mx = -INFINITY;
+  for (int64_t i = t; i < a.L; i += 256) {
+    const float v = x[i];
+    s += v;
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  ps[t] = s; pmn[t] = mn; pmx[t] = mx;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (t < st) {
+      ps[t] += ps[t + st];
+      pmn[t] = fminf(pmn[t], pmn[t + st]);
+      pmx[t] = fmaxf(pmx[t], pmx[t + st]);
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    a.stats[bh * 3 + 0] = ps[0];
+    a.stats[bh * 3 + 1] = pmn[0];
+    a.stats[bh * 3 + 2] = pmx[0];
+  }
+}
+
+struct ModApplyArgs {
+  const float* x;
+  const float* stats;
+  int BH;
+  int64_t L;
+  float lo, hi;
+  float* out;
+};
+
+__global__ __launch_bounds__(256) void modfac_apply_kernel(ModApplyArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.BH * a.L) return;
+  bool need = false;
+  for (int h = 0; h < a.BH; ++h) need |= a.stats[h * 3 + 1] < a.lo || a.stats[h * 3 + 2] > a.hi;
+  const float v = a.x[i];
+  if (!need) {
+    a.out[i] = v;
+    return;
+  }
+  const int64_t bh = i / a.L;
+  const float sum = a.stats[bh * 3 + 0], cmin = a.stats[bh * 3 + 1], cmax = a.stats[bh * 3 + 2];
+  const float tmin = cmin < a.lo ? a.lo : cmin;
+  const float tmax = cmax > a.hi ? a.hi : cmax;
+  const bool flat = (cmax - cmin) < 1e-6f;
+  const float rng = flat ? 1.f : cmax - cmin;
+  const float n = (float)a.L;
+  const float new_sum = (sum - n * cmin) / rng * (tmax - tmin) + n * tmin;
+  const float scaled = (v - cmin) / rng * (tmax - tmin) + tmin;
+  const float f = flat ? v : scaled * (sum / new_sum);
+  a.out[i] = fminf(fmaxf(f, a.lo), a.hi);
+}
 }  // namespace
+
+extern "C" int sa_constrained_mod_factor(const float* x, int BH, int64_t L, float lo, float hi, float* stats,
+                                         float* out, void* stream) {
+  const char* fn = "sa_constrained_mod_factor";
+  SA_REQUIRE(x && stats && out, "%s: null pointer", fn);
+  SA_REQUIRE(BH > 0 && BH <= 4096 && L > 0, "%s: bad shape BH=%d L=%lld", fn, BH, (long long)L);
+  SA_REQUIRE(lo <= hi, "%s: lo %g > hi %g", fn, (double)lo, (double)hi);
+  hipStream_t s = sa::as_stream(stream);
+  ModStatsArgs sa_{x, L, stats};
+  hipLaunchKernelGGL(modfac_stats_kernel, dim3((unsigned)BH), dim3(256), 0, s, sa_);
+  if (int rc = sa::check_launch(fn)) return rc;
+  ModApplyArgs aa{x, stats, BH, L, lo, hi, out};
+  const int64_t n = (int64_t)BH * L;
+  SA_REQUIRE((n + 255) / 256 < (1LL << 31), "%s: grid too large", fn);
+  hipLaunchKernelGGL(modfac_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, aa);
+  return sa::check_launch(fn);
+}
 
 extern "C" int sa_gather_tokens_heads(const uint16_t* x, const int64_t x_strides[3], int B, int H, int L_in, int D,
                                       const int32_t* idx, int L_out, uint16_t* out, const int64_t out_strides[3],

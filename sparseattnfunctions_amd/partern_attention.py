@@ -55,6 +55,9 @@ class PatternGeometry:
 DEFAULT = PatternGeometry()
 f, width, height, text_length, sample_num, dim = 11, 85, 48, 224, 500, 64
 scale_factor = 1 / 8
+# The reference's module tensors (partern_attention.py:34-35).
+sample_rate = torch.tensor(sample_num / (width * height))
+composition = torch.log(sample_rate).view(1, 1, 1, 1)
 
 _CACHE = {}
 
@@ -93,7 +96,7 @@ def _sample_indicator(g: PatternGeometry, device):
     return _cached(("sind", g, str(device)), make)
 
 
-def composition(geometry: PatternGeometry = DEFAULT) -> float:
+def composition_bias(geometry: PatternGeometry = DEFAULT) -> float:
     """Bias of the sampled text keys: log(sample_num / S) in fp32, rounded to bf16 as the
     reference adds it (partern_attention.py:34-35, 343, 497: composition.to(q.dtype))."""
     g = geometry
@@ -135,7 +138,7 @@ class ParternAttentionColVersion_V2:
         qs, ks = gather_tokens(q, idx), gather_tokens(k, idx)
         nk = idx.numel()
         bias = _cached(("bias", g, str(q.device)), lambda: torch.where(
-            torch.arange(nk, device=q.device) < g.text_length, composition(g), 0.0).float())
+            torch.arange(nk, device=q.device) < g.text_length, composition_bias(g), 0.0).float())
         return block_sparse_attention(qs[:, :, g.text_length:], ks, _bcast(_sample_indicator(g, q.device), B, H),
                                       _dense(B, H, g.frames * g.sample_num, nk, q.device), sm_scale,
                                       key_bias=_bcast(bias, B, H))
@@ -216,6 +219,33 @@ class ParternAttentionColVersion_V2:
         return self.forward(*args, **kwds)
 
 
+def constrained_mod_factor(modify_factor, min_threshold=0.01, max_threshold=50.0):
+    """partern_attention.py:262-315 on the GPU (`sa_constrained_mod_factor`): modify_factor
+    [B, H, L, 1] fp32 (other float dtypes are converted); unchanged when every head lies within
+    [min_threshold, max_threshold], else each head is mapped affinely onto the clipped range,
+    rescaled to its original sum and clamped. Returns fp32 of the input's shape."""
+    _lib.require_gpu(modify_factor)
+    if modify_factor.dim() != 4 or modify_factor.shape[-1] != 1:
+        raise ValueError(f"modify_factor must be [B, H, L, 1], got {tuple(modify_factor.shape)}")
+    B, H, L, _ = modify_factor.shape
+    x = modify_factor.to(torch.float32).contiguous()
+    out = torch.empty_like(x)
+    stats = torch.empty(B * H, 3, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().sa_constrained_mod_factor(x.data_ptr(), B * H, L, float(min_threshold),
+                                                         float(max_threshold), stats.data_ptr(), out.data_ptr(),
+                                                         _lib.stream_of(x)), "sa_constrained_mod_factor")
+    return out
+
+
+def get_softmax(q, k):
+    """softmax(q k^T * scale_factor) over the keys (partern_attention.py:463-467): fp32
+    probabilities (`sa_sampled_probs`) in q's dtype."""
+    from .utils.mask_related import calc_attn
+
+    return calc_attn(q, k)
+
+
 # ---- head routing (partern_attention.py:463-521) ---------------------------------------------
 
 SPARSE_KEEP, SPARSE_THR, SIM_THR = 0.2, 0.9, 0.9
@@ -285,7 +315,7 @@ def _similarity_gram(q, k, g: PatternGeometry, index_k):
     with torch.cuda.device(q.device):
         _lib.check(_lib.load().sa_pattern_sim_gram(
             qs.data_ptr(), ks.data_ptr(), qs.shape[0], F, ns, T, qs.shape[1], ks.shape[1], scale_factor,
-            composition(g), G.data_ptr(), _lib.stream_of(q)), "sa_pattern_sim_gram")
+            composition_bias(g), G.data_ptr(), _lib.stream_of(q)), "sa_pattern_sim_gram")
     return G
 
 
@@ -297,7 +327,7 @@ def _similarity_gram_via_probs(q, k, g: PatternGeometry, index_k):
     BH = qs.shape[0]
     for h0, h1 in _chunks(BH, nv * _pad32(nv) * 4):
         P = torch.empty(h1 - h0, nv, _pad32(nv), dtype=torch.float32, device=q.device)
-        _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, composition(g), T, T + nv, P)
+        _probs(qs[h0:h1], ks[h0:h1], nv, T + nv, T, composition_bias(g), T, T + nv, P)
         with torch.cuda.device(q.device):
             _lib.check(_lib.load().sa_pattern_gram(P.data_ptr(), P.stride(0), P.stride(1), h1 - h0, F, ns,
                                                    G[h0:h1].data_ptr(), _lib.stream_of(q)), "sa_pattern_gram")

@@ -213,3 +213,35 @@ def test_combined_attn_head_routing(dev):
     got = out.reshape(4, G.L, 64)
     assert torch.equal(got[sel.to(dev)], pat[0])
     assert torch.equal(got[rest.to(dev)], other[0])
+
+
+def test_constrained_mod_factor_matches_oracle(dev):
+    from oracle import pattern as opat
+    from sparseattnfunctions_amd.partern_attention import constrained_mod_factor
+
+    case("constrained_mod_factor")
+    g = torch.Generator().manual_seed(21)
+    # every head in range: returned unchanged
+    x = torch.rand(2, 3, 500, 1, generator=g) + 0.5
+    assert torch.equal(constrained_mod_factor(x.to(dev), 0.01, 50.0).cpu(), x)
+    # one head out of range (above hi), a flat head and in-range heads: the decision covers
+    # every head, each remapped head keeps its sum (before the clamp)
+    x = torch.rand(2, 48, 4500, 1, generator=g) * 2
+    x[0, 5] *= 80
+    x[1, 7] = 0.5
+    got = constrained_mod_factor(x.to(dev), 0.05, 100.0).cpu().double()
+    want = opat.constrained_mod_factor(x.double(), 0.05, 100.0)
+    assert torch.allclose(got, want, rtol=2e-5, atol=1e-6), (got - want).abs().max()
+    assert torch.equal(got[1, 7], torch.full_like(got[1, 7], 0.5))
+
+
+def test_get_softmax_probabilities(dev):
+    from sparseattnfunctions_amd.partern_attention import get_softmax
+
+    case("get_softmax")
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, 2, 50, 64, generator=g).bfloat16()
+    k = torch.randn(1, 2, 300, 64, generator=g).bfloat16()
+    got = get_softmax(q.to(dev), k.to(dev)).cpu()
+    want = torch.softmax(q.double() @ k.double().transpose(-1, -2) / 8, dim=-1)
+    assert got.dtype == torch.bfloat16 and (got.double() - want).abs().max().item() <= 2 ** -8 * want.max().item()
