@@ -412,6 +412,17 @@ int sa_local_window_bitmap(int L, int block, int text_len, int T, int Hp, int Wp
                            int dw, uint8_t* bitmap);
 
 /*
+ * (host) The local window of sa_local_window_bitmap for a permuted token layout: position j
+ * holds natural token perm[j] (text first, then row-major (t, h, w)); block b's centre token is
+ * perm[min(b*block + block/2, L-1)], and two video centres are in the window as above. Every
+ * row and column of a block holding any text token is set (the layout may put the text
+ * anywhere, e.g. last in the 1.5-5B rearranger of combined_attn.py:17-31, so the top-k
+ * kernel's leading n_text_blocks cannot express it). bitmap uint8 [nb][nb].
+ */
+int sa_local_window_bitmap_perm(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh,
+                                int dw, const int32_t* perm, uint8_t* bitmap);
+
+/*
  * (host) Tile-major token order of sliding-tile attention (SildingTileAttention.py:111-131):
  * perm[j] = natural token at position j; text tokens stay first, video tokens are grouped
  * "(nt tt nh th nw tw) -> (nt nh nw tt th tw)" for tile = {tt, th, tw} dividing (T, Hp, Wp).

@@ -77,6 +77,7 @@ _PROTOTYPES = {
     "sa_sta_block_masks": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P]),
     "sa_gather_tokens": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _I64P, _P]),
     "sa_local_window_bitmap": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "sa_local_window_bitmap_perm": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "sa_sample_block_tokens": (_I, [_P, _P, _I64P, _P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
     "sa_sampled_block_scores": (_I, [_P, _P, _I, _I, _I, _I, _P, _P]),
     "sa_energy_kv_list": (_I, [_P, _I, _I, _I, _I, _F, _I, _I, _I, _I, _P, _I, _P, _P, _P]),

@@ -120,3 +120,25 @@ def local_window_bitmap(geom, window=(1, 8, 8), device=None) -> torch.Tensor:
         bm = host.to(device) if device is not None else host
         _LOCAL_CACHE[key] = bm
     return bm
+
+
+def local_window_bitmap_perm(geom, perm: torch.Tensor, window=(1, 8, 8), device=None) -> torch.Tensor:
+    """The local window for a permuted token layout (`sa_local_window_bitmap_perm`): uint8
+    [nb, nb] with position j holding natural token perm[j], blocks compared by the (t, h, w)
+    of their centre tokens, and every row/column of a block with a text token set. Built on
+    the host, cached per (geometry, permutation, window, device)."""
+    perm = perm.to(device="cpu", dtype=torch.int32).contiguous()
+    key = (geom, tuple(window), str(device), perm.numel(), hash(perm.numpy().tobytes()))
+    bm = _LOCAL_CACHE.get(key)
+    if bm is None:
+        nb = math.ceil(geom.L / geom.block)
+        if perm.numel() != geom.L:
+            raise ValueError(f"permutation of {perm.numel()} tokens for L={geom.L}")
+        host = torch.empty(nb, nb, dtype=torch.uint8)
+        dt, dh, dw = window
+        rc = _lib.load().sa_local_window_bitmap_perm(geom.L, geom.block, geom.text_len, geom.T, geom.Hp, geom.Wp,
+                                                     dt, dh, dw, perm.data_ptr(), host.data_ptr())
+        _lib.check(rc, "sa_local_window_bitmap_perm")
+        bm = host.to(device) if device is not None else host
+        _LOCAL_CACHE[key] = bm
+    return bm

@@ -20,8 +20,11 @@ attention, optionally through the 1.5-5B token permutation (`use_rearranger=True
 routing needs one host synchronisation per call (the count of pattern heads), as in the
 reference. Selected heads are copied with torch's index_select/index_copy_.
 `rearranger` / `recover` are the reference's 1.5-5B token permutations (combined_attn.py:
-17-41), as GPU gathers; without head routing `use_rearranger=True` is not supported, since
-the combined rule's local window is defined on the text-first (t, h, w) layout.
+17-41), as GPU gathers. Without head routing, `use_rearranger=True` (1.5-5B geometry) applies
+the combined rule in the rearranged layout, as the reference's block-sparse heads are
+estimated there: block means of the permuted q and k for the global top-k, the local window
+between the original (t, h, w) of the permuted blocks' centre tokens, the blocks holding text
+(last in that layout) dense; the output is recovered to the natural order.
 """
 from __future__ import annotations
 
@@ -31,7 +34,7 @@ import torch
 
 from ._gather import gather_tokens
 from .block_mask_attn import dense_kv_list
-from .block_masks import local_window_bitmap, meanpool_topk_kv_list
+from .block_masks import local_window_bitmap, local_window_bitmap_perm, meanpool_topk_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
 from .workloads import COGVIDEOX_2B, Geometry, topk_count
 
@@ -175,14 +178,28 @@ class CombinedAttn:
             print("counter:", self.counter, "now increment:", n_sel)
         return out.view(B, H, L, D)
 
+    def build_kv_list_rearranged(self, qr, kr):
+        """Combined-rule kv lists in the rearranged layout (qr, kr from `rearranger`)."""
+        g = self.geometry
+        if (g.text_len, g.T, g.Hp, g.Wp) != (_R_TEXT, _R_T, _R_H, _R_W):
+            raise ValueError("use_rearranger needs the 1.5-5B geometry (224 text + 11 x 48 x 85 video tokens)")
+        nb = math.ceil(qr.shape[2] / 64)
+        perm, _ = _perms("cpu")
+        local = local_window_bitmap_perm(g, perm, self.window, qr.device)
+        return meanpool_topk_kv_list(qr, kr, topk_count(self.global_ratio, nb), 0, local_bitmap=local)
+
     def __call__(self, q, k, v, use_rearranger: bool = False):
         if self.head_routing:
             return self._routed(q, k, v, use_rearranger)
-        if use_rearranger:
-            raise NotImplementedError(
-                "use_rearranger (the 1.5-5B token permutation, combined_attn.py:17-41) is not supported "
-                "with the combined local-window mask, which is defined on the text-first layout")
         warm = self.ct // self.layer_num < self.warmup_epoch
+        if use_rearranger:
+            self.ct += 1
+            qr, kr, vr = self.rearranger(q, k, v)
+            B, H, L, _ = q.shape
+            nb = math.ceil(L / 64)
+            kv = dense_kv_list(B, H, nb, nb, q.device) if warm else self.build_kv_list_rearranged(qr, kr)
+            self.last_kv = kv
+            return self.recover(block_sparse_attention(qr, kr, vr, kv, self._scale(q)))
         self.ct += 1
         if warm:
             B, H, L, _ = q.shape

@@ -50,6 +50,32 @@ extern "C" int sa_local_window_bitmap(int L, int block, int text_len, int T, int
   return sa::ok();
 }
 
+extern "C" int sa_local_window_bitmap_perm(int L, int block, int text_len, int T, int Hp, int Wp, int dt, int dh,
+                                           int dw, const int32_t* perm, uint8_t* bitmap) {
+  SA_REQUIRE(bitmap && perm, "sa_local_window_bitmap_perm: null pointer");
+  SA_REQUIRE(block > 0 && text_len >= 0 && T > 0 && Hp > 0 && Wp > 0 && dt >= 0 && dh >= 0 && dw >= 0,
+             "sa_local_window_bitmap_perm: bad geometry");
+  SA_REQUIRE(L == text_len + T * Hp * Wp, "sa_local_window_bitmap_perm: L=%d != text_len + T*Hp*Wp", L);
+  const int nb = sa::cdiv(L, block);
+  std::vector<VideoPos> centre(nb);
+  std::vector<uint8_t> has_text(nb, 0);
+  for (int j = 0; j < L; ++j) {
+    SA_REQUIRE(perm[j] >= 0 && perm[j] < L, "sa_local_window_bitmap_perm: perm[%d]=%d outside [0, %d)", j, perm[j], L);
+    if (perm[j] < text_len) has_text[j / block] = 1;
+  }
+  for (int b = 0; b < nb; ++b) centre[b] = token_pos(perm[std::min(b * block + block / 2, L - 1)], text_len, Hp, Wp);
+  for (int qb = 0; qb < nb; ++qb) {
+    for (int kb = 0; kb < nb; ++kb) {
+      const VideoPos& pq = centre[qb];
+      const VideoPos& pk = centre[kb];
+      const bool win = pq.video && pk.video && iabs(pq.t - pk.t) <= dt && iabs(pq.h - pk.h) <= dh &&
+                       iabs(pq.w - pk.w) <= dw;
+      bitmap[(int64_t)qb * nb + kb] = (win || has_text[qb] || has_text[kb]) ? 1 : 0;
+    }
+  }
+  return sa::ok();
+}
+
 // ---------------------------------------------------------------------------------------
 // Sliding-tile attention (SildingTileAttention.py:18-143): the tile-major token order and
 // the token-level 3-D tile window, expressed as 64x64 block lists with bitmasks for the

@@ -124,7 +124,7 @@ def test_combined_attn_warmup_is_dense(dev):
             assert torch.equal(proc.last_kv.to_mask().cpu(), mask)
             _check(out, masked_attention(q, k, v, mask, 1 / 8))
     assert proc.ct == 3
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError):  # the rearranger is the 1.5-5B permutation
         proc(q.to(dev), k.to(dev), v.to(dev), use_rearranger=True)
 
 
@@ -139,3 +139,35 @@ def test_block_mask_attn_small_and_dense(dev):
     _check(out, masked_attention(q, k, v, mask, 1 / 8))
     dense = proc.forward_dense(q.to(dev), k.to(dev), v.to(dev))
     _check(dense, masked_attention(q, k, v, torch.ones(1, 1, nb, nb, dtype=torch.bool), 1 / 8))
+
+
+def test_combined_attn_rearranged_config3(dev):
+    # use_rearranger=True without head routing (1.5-5B geometry): the combined rule applied in
+    # the rearranged layout -- block means of the permuted tokens for the global top-k, the
+    # local window between the permuted blocks' centre tokens, text blocks dense -- then the
+    # output recovered to the natural order.
+    from oracle import layout
+    from sparseattnfunctions_amd.combined_attn import rearranger_permutation
+    from sparseattnfunctions_amd.workloads import COGVIDEOX_15_5B as g
+
+    case("CombinedAttn config 3 with use_rearranger (1.5-5B)")
+    q, k, v = cogvideox_qkv(11, B=1, H=2, geom=g)
+    proc = CombinedAttn(warmup_epoch=0, geometry=g)
+    out = proc(q.to(dev), k.to(dev), v.to(dev), use_rearranger=True).cpu()
+    assert out.shape == q.shape
+    perm = rearranger_permutation().long()
+    qr, kr, vr = (x[:, :, perm].contiguous() for x in (q, k, v))
+    nb = math.ceil(g.L / 64)
+    local = layout.local_window_perm(perm, g.L, 64, g.text_len, g.T, g.Hp, g.Wp, 1, 8, 8)
+    _, _, m, _ = native.block_topk(native.block_pool(qr), native.block_pool(kr), topk_count(0.1, nb), 0, local=local)
+    mask = m.reshape(1, 2, nb, nb).bool()
+    assert torch.equal(proc.last_kv.to_mask().cpu(), mask)
+    inv = torch.argsort(perm)
+    gen = torch.Generator().manual_seed(12)
+    for h in range(2):
+        tok = torch.unique(torch.cat([torch.randint(0, g.text_len, (8,), generator=gen),
+                                      torch.randint(g.text_len, g.L, (48,), generator=gen), torch.tensor([g.L - 1])]))
+        pos = inv[tok]
+        order = torch.argsort(pos)
+        want = masked_attention(qr, kr, vr, mask, 1 / 8, heads=[(0, h)], rows=pos[order])[0, h]
+        _check(out[0, h, tok[order]], want)
