@@ -15,6 +15,8 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsa_hip.so")
 
+ABI_VERSION = 2  # SA_ABI_VERSION of include/sa_api.h these prototypes describe
+
 SA_OK = 0
 SA_ERR_INVALID = -1
 SA_ERR_UNSUPPORTED = -2
@@ -109,6 +111,11 @@ def load() -> ctypes.CDLL:
                 "(or __graft_entry__.build())"
             )
         lib = ctypes.CDLL(LIB_PATH)
+        lib.sa_abi_version.restype = _I
+        version = lib.sa_abi_version()
+        if version != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI version {version}, the bindings expect {ABI_VERSION}; rebuild it "
+                              "with `make -C sparseattnfunctions_amd/csrc`")
         for name, (res, args) in _PROTOTYPES.items():
             fn = getattr(lib, name)
             fn.restype = res

@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.sa_abi_version() == 2
+    assert lib.sa_abi_version() == 2 == _lib.ABI_VERSION
     assert lib.sa_last_error() is not None
 
 
