@@ -100,7 +100,7 @@ int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const
 
 /*
  * Block-sparse attention with token-level masks inside cut blocks: as sa_block_sparse_fwd
- * (bf16, head dim 64), plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
+ * (bf16, D = 64 or 128), plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
  * bitmask in tile_masks (uint64 [slots][64]: bit c of word r = query r of the block may
  * attend key c). Replaces flex_attention with a BlockMask built from a mask_mod
  * (SildingTileAttention.py:88-106, 146), which also masks element-wise inside partial blocks.
@@ -143,13 +143,29 @@ int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_strides[3], co
                                void* stream);
 
 /*
+ * sa_block_sparse_fwd_mapped for fp16 q, k, v and out: same arguments and contract, computed
+ * as sa_block_sparse_fwd_f16 (fp16 MFMA, P rounded to fp16, running row maximum).
+ */
+int sa_block_sparse_fwd_mapped_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                   const int64_t k_strides[3], const uint16_t* v,
+                                   const int64_t v_strides[3], uint16_t* out,
+                                   const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                                   const int32_t* kv_idx, const int32_t* kv_cnt, const int32_t* kv_slot,
+                                   int max_cnt, int lists_shared, const uint64_t* tile_masks,
+                                   const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                   const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                                   int o_dst_rows, const int32_t* work_order, int64_t n_slots,
+                                   void* stream);
+
+/*
  * Dense or causal attention that also returns the 2-D max-pooled attention map, a block-score
  * source (attn_with_pooling = _attention_pooling.forward, utils/attn_pooling_kernel.py:18-289):
- *   out[b,h,r] = softmax_c(q[b,h,r] . k[b,h/(H/H_kv),c] * sm_scale) v[...]     bf16 [B,H,L,64]
+ *   out[b,h,r] = softmax_c(q[b,h,r] . k[b,h/(H/H_kv),c] * sm_scale) v[...]     bf16 [B,H,L,D]
  *                (causal: keys c <= r only)
  *   Po[b,h,i,j] = max over queries r of block i and keys c of block j of the softmax P[r][c],
  *                 then each row of Po divided by its sum                          fp32 [B,H,nd,nd]
- * with blocks of block_size in {32, 64, 128} tokens, nd = ceil(L / block_size) <= 8192, and
+ * with D = 64 or 128, blocks of block_size in {32, 64, 128} tokens, nd = ceil(L / block_size)
+ * <= 8192, and
  * Po[i][j] = 0 for j > i when causal. k and v have H_kv heads (H_kv divides H). Po has
  * element strides po_strides (b, h, i) and unit stride over j. workspace: at least
  * sa_attn_pooling_workspace() bytes, 256-byte aligned (kv lists, per-row maxima of every
@@ -162,6 +178,18 @@ int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         int D, int causal, float sm_scale, int block_size, float* po,
                         const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
                         void* stream);
+
+/*
+ * sa_attn_pooling_fwd for fp16 q, k, v and out (the reference also takes fp16, :230-289):
+ * same arguments and contract, the attention computed as sa_block_sparse_fwd_f16; Po and the
+ * workspace stay fp32.
+ */
+int sa_attn_pooling_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                            const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                            uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L,
+                            int D, int causal, float sm_scale, int block_size, float* po,
+                            const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /*
  * (host) Dispatch order of the attention work items (one per list row) for a GPU whose
@@ -441,8 +469,8 @@ int sa_sta_block_masks(int text_len, int T, int Hp, int Wp, const int tile[3], c
                        int* n_slots);
 
 /*
- * Token gather out[b,h,j] = x[b,h,idx[j]] for j < L_out; an index outside [0, L_in) gives a
- * zero row. Serves the layout transforms that are copies: the sliding-tile order of k and v
+ * Token gather out[b,h,j] = x[b,h,idx[j]] for j < L_out (16-bit elements, D a multiple of 8);
+ * an index outside [0, L_in) gives a zero row. Serves the layout transforms that are copies: the sliding-tile order of k and v
  * (SildingTileAttention.py:111-131), the 1.5-5B rearranger/recover (combined_attn.py:17-41),
  * replicate padding (utils/mask_related.py:2-13) and preprocess_qkv/reverse_process_out
  * (utils/mask_related.py:87-187).

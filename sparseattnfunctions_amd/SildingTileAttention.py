@@ -23,7 +23,7 @@ import torch
 from . import _lib
 from ._gather import gather_tokens as _gather
 from ._kv import KVList
-from .utils.block_sparse_attn_kernel import _prep_qkv, block_sparse_attention, work_order
+from .utils.block_sparse_attn_kernel import block_sparse_attention
 
 config = {
     "kernel_size": (1, 9, 9),
@@ -134,21 +134,13 @@ class SildingTileAttention:
     def attention(self, q, k, v, sm_scale=None):
         """Sliding-tile attention on inputs already in the tile-major layout."""
         lay = self._get_layout(q.device)
-        q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
         B, H, L, D = q.shape
         if L != lay.L or k.shape != q.shape or v.shape != q.shape:
             raise ValueError(f"expected q, k, v of {lay.L} tokens for this configuration, got {tuple(q.shape)}")
         scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(D)
-        out = torch.empty_like(q)
-        order = work_order(B, H, lay.nb, lay.text_blocks, q.device)
-        with torch.cuda.device(q.device):
-            rc = _lib.load().sa_block_sparse_fwd_tilemask(
-                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
-                v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
-                B, H, L, L, D, lay.kv_idx.data_ptr(), lay.kv_cnt.data_ptr(), lay.kv_slot.data_ptr(), lay.nb, 1,
-                lay.masks.data_ptr(), float(scale), order.data_ptr(), order.numel(), _lib.stream_of(q))
-        _lib.check(rc, "sa_block_sparse_fwd_tilemask")
-        return out
+        kv = KVList(lay.kv_idx, lay.kv_cnt, 1, 1, lay.nb, lay.nb)
+        return block_sparse_attention(q, k, v, kv, scale, n_text_blocks=lay.text_blocks,
+                                      tile_masks=(lay.kv_slot, lay.masks, True))
 
     def forward(self, q, k, v):
         """preprocess -> attention -> process_out_back, with the query permutation and the

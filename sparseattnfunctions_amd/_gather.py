@@ -9,9 +9,10 @@ from .utils.block_sparse_attn_kernel import _prep_qkv
 
 
 def gather_tokens(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
-    """x bf16 [B, H, L, D] on the GPU, idx int32 [L_out] on the same device -> [B, H, L_out, D]."""
+    """x bf16 or fp16 [B, H, L, D] (D a multiple of 8) on the GPU, idx int32 [L_out] on the same
+    device -> [B, H, L_out, D]."""
     _lib.require_gpu(x, idx)
-    x = _prep_qkv(x)
+    x = _prep_qkv(x, (torch.bfloat16, torch.float16))
     idx = idx.to(torch.int32).contiguous()
     B, H, L, D = x.shape
     out = torch.empty(B, H, idx.numel(), D, dtype=x.dtype, device=x.device)

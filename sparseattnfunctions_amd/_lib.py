@@ -54,9 +54,19 @@ _PROTOTYPES = {
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P, _I64P, _F,
          _P, _I, _P, _I, _P, ctypes.c_int64, _P],
     ),
+    "sa_block_sparse_fwd_mapped_f16": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _I, _P, _P, _I64P, _F,
+         _P, _I, _P, _I, _P, ctypes.c_int64, _P],
+    ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
     "sa_attn_pooling_workspace": (_I, [_I, _I, _I, _I, _I64P]),
     "sa_attn_pooling_fwd": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,
+         ctypes.c_int64, _P],
+    ),
+    "sa_attn_pooling_fwd_f16": (
         _I,
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,
          ctypes.c_int64, _P],

@@ -235,8 +235,6 @@ template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64>
 __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs a) {
   static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
   static_assert(kD == 64 || kD == 128, "head dim 64 or 128");
-  static_assert((kD == 64 && std::is_same<T, __bf16>::value) || (!kMask && kPool == 0),
-                "tile masks and pooling: bf16, head dim 64");
   typedef Elem<T> E;
   constexpr int kDS = kD / 16;     // 16-wide d steps of S = K Q^T
   constexpr int kDC = kD / 32;     // 32-row d chunks of O^T
@@ -427,7 +425,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       
       if (kBias) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
         // The bias copy of this tile was issued before its V copy: wait for it only.
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 + kGroupK));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * kHalves + kGroupK));
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -745,6 +743,23 @@ struct PoolOut {
   int causal;
 };
 
+// One kernel variant per (tile masks, key bias, pooling columns): the caller has rejected
+// the combinations of tile masks or pooling with a key bias.
+template <typename T, int kD>
+void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask, bool bias, int pool_cols) {
+  if (mask) {
+    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 32, T, kD>), g, blk, 0, s, a);
+    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 64, T, kD>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 0, T, kD>), g, blk, 0, s, a);
+  } else if (bias) {
+    hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, T, kD>), g, blk, 0, s, a);
+  } else {
+    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 32, T, kD>), g, blk, 0, s, a);
+    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 64, T, kD>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD>), g, blk, 0, s, a);
+  }
+}
+
 int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
                const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B,
                int H, int Lq, int Lk, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
@@ -757,8 +772,6 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
   if (D != 64 && D != 128) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", fn, D);
-  if ((D != 64 || fp16) && (kv_slot || pool_cols))
-    return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks and pooling need bf16 and head_dim 64", fn);
   SA_REQUIRE(std::isfinite(sm_scale) && sm_scale > 0.f, "%s: sm_scale must be finite and > 0", fn);
   const int nqb = sa::cdiv(Lq, kBlock);
   const int nkb = sa::cdiv(Lk, kBlock);
@@ -832,33 +845,17 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   SA_REQUIRE(!pool_out || (pool_out->po && pool_cols && Lq == Lk && pool_out->nd == sa::cdiv(Lq, pool_cols)),
              "%s: fused pooled map needs pooling columns of the map's block size", fn);
 
+  if (kv_slot && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
+  if (pool_cols && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
   hipStream_t s = sa::as_stream(stream);
   const dim3 g((unsigned)grid), blk(64 * kWaves);
-  if (fp16 || D == 128) {
-    if (fp16 && D == 64) {
-      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, _Float16, 64>), g, blk, 0, s, a);
-      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, _Float16, 64>), g, blk, 0, s, a);
-    } else if (fp16) {
-      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, _Float16, 128>), g, blk, 0, s, a);
-      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, _Float16, 128>), g, blk, 0, s, a);
-    } else {
-      if (key_bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, __bf16, 128>), g, blk, 0, s, a);
-      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, __bf16, 128>), g, blk, 0, s, a);
-    }
-    return sa::check_launch(fn);
-  }
-  if (kv_slot) {
-    if (key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
-    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 32>), g, blk, 0, s, a);
-    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 64>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 0>), g, blk, 0, s, a);
-  } else if (key_bias) {
-    if (pool_cols) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
-    hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0>), g, blk, 0, s, a);
+  const bool mask = kv_slot != nullptr, bias = key_bias != nullptr;
+  if (fp16) {
+    if (D == 64) launch_variant<_Float16, 64>(a, g, blk, s, mask, bias, pool_cols);
+    else launch_variant<_Float16, 128>(a, g, blk, s, mask, bias, pool_cols);
   } else {
-    if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 32>), g, blk, 0, s, a);
-    else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 64>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0>), g, blk, 0, s, a);
+    if (D == 64) launch_variant<__bf16, 64>(a, g, blk, s, mask, bias, pool_cols);
+    else launch_variant<__bf16, 128>(a, g, blk, s, mask, bias, pool_cols);
   }
   return sa::check_launch(fn);
 }
@@ -912,6 +909,23 @@ extern "C" int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_str
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, lists_shared != 0, kv_slot, tile_masks, key_bias, bias_strides, sm_scale, work_order,
                     n_slots, q_rows, q_src_rows, o_rows, o_dst_rows, stream, "sa_block_sparse_fwd_mapped");
+}
+
+extern "C" int sa_block_sparse_fwd_mapped_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                              const int64_t k_strides[3], const uint16_t* v,
+                                              const int64_t v_strides[3], uint16_t* out,
+                                              const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                                              const int32_t* kv_idx, const int32_t* kv_cnt, const int32_t* kv_slot,
+                                              int max_cnt, int lists_shared, const uint64_t* tile_masks,
+                                              const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                              const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                                              int o_dst_rows, const int32_t* work_order, int64_t n_slots,
+                                              void* stream) {
+  SA_REQUIRE(!kv_slot == !tile_masks, "sa_block_sparse_fwd_mapped_f16: kv_slot and tile_masks go together");
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, lists_shared != 0, kv_slot, tile_masks, key_bias, bias_strides, sm_scale, work_order,
+                    n_slots, q_rows, q_src_rows, o_rows, o_dst_rows, stream, "sa_block_sparse_fwd_mapped_f16", 1, 0,
+                    nullptr, nullptr, nullptr, true);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1079,13 +1093,13 @@ extern "C" int sa_attn_pooling_workspace(int B, int H, int L, int block_size, in
   return sa::ok();
 }
 
-extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
-                                   const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
-                                   uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L, int D,
-                                   int causal, float sm_scale, int block_size, float* po,
-                                   const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
-                                   void* stream) {
-  const char* fn = "sa_attn_pooling_fwd";
+namespace {
+
+int attn_pooling(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
+                 const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B,
+                 int H, int H_kv, int L, int D, int causal, float sm_scale, int block_size, float* po,
+                 const int64_t po_strides[3], void* workspace, int64_t workspace_bytes, void* stream, bool fp16,
+                 const char* fn) {
   SA_REQUIRE(po && po_strides && workspace, "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && L > 0, "%s: bad shape B=%d H=%d L=%d", fn, B, H, L);
   SA_REQUIRE(H_kv > 0 && H % H_kv == 0, "%s: H_kv=%d must divide H=%d", fn, H_kv, H);
@@ -1116,11 +1130,13 @@ extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3]
     const PoolOut po_out{po, po_strides[0], po_strides[1], po_strides[2], nd, causal ? 1 : 0};
     return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, L, D, la.idx, la.cnt,
                       p.nkb, true, causal ? la.slot : nullptr, causal ? la.mask : nullptr, nullptr, nullptr,
-                      sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, nullptr, &po_out);
+                      sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, nullptr, &po_out,
+                      fp16);
   }
   if (int rc = launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, L, D, la.idx, la.cnt,
                           p.nkb, true, causal ? la.slot : nullptr, causal ? la.mask : nullptr, nullptr, nullptr,
-                          sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, lse))
+                          sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, lse, nullptr,
+                          fp16))
     return rc;
   PoolReduceArgs ra;
   ra.r = r; ra.nqb = p.nqb; ra.ncol_alloc = p.ncol_alloc; ra.lpad = p.lpad; ra.lse = lse;
@@ -1130,4 +1146,26 @@ extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3]
   SA_REQUIRE(ra.total < (1LL << 31), "%s: grid too large", fn);
   hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)ra.total), dim3(256), (unsigned)(nd * sizeof(float)), s, ra);
   return sa::check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                   const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                   uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L, int D,
+                                   int causal, float sm_scale, int block_size, float* po,
+                                   const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                                   void* stream) {
+  return attn_pooling(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, H_kv, L, D, causal, sm_scale,
+                      block_size, po, po_strides, workspace, workspace_bytes, stream, false, "sa_attn_pooling_fwd");
+}
+
+extern "C" int sa_attn_pooling_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                       const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                       uint16_t* out, const int64_t out_strides[3], int B, int H, int H_kv, int L,
+                                       int D, int causal, float sm_scale, int block_size, float* po,
+                                       const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  return attn_pooling(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, H_kv, L, D, causal, sm_scale,
+                      block_size, po, po_strides, workspace, workspace_bytes, stream, true, "sa_attn_pooling_fwd_f16");
 }

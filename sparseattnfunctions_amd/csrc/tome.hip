@@ -791,7 +791,8 @@ namespace {
 __global__ __launch_bounds__(256) void gather_tokens_kernel(const uint16_t* x, int64_t x_sb, int64_t x_sh,
                                                             int64_t x_sl, int L_in, const int32_t* idx, int L_out,
                                                             int H, int64_t rows, uint16_t* out, int64_t o_sb,
-                                                            int64_t o_sh, int64_t o_sl) {
+                                                            int64_t o_sh, int64_t o_sl, int nchunk) {
+  // Eight lanes per row, each moving 16-byte chunks c8, c8 + 8, ... of the row's nchunk.
   const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
   if (row >= rows) return;
   const int c8 = threadIdx.x & 7;
@@ -799,10 +800,14 @@ __global__ __launch_bounds__(256) void gather_tokens_kernel(const uint16_t* x, i
   const int j = (int)(row - bh * L_out);
   const int64_t b = bh / H, h = bh - b * H;
   const int src = idx[j];
-  uint4 w = make_uint4(0u, 0u, 0u, 0u);  // an index outside [0, L_in) gives a zero row (padding)
-  if ((unsigned)src < (unsigned)L_in)
-    w = *reinterpret_cast<const uint4*>(x + b * x_sb + h * x_sh + (int64_t)src * x_sl + 8 * c8);
-  *reinterpret_cast<uint4*>(out + b * o_sb + h * o_sh + (int64_t)j * o_sl + 8 * c8) = w;
+  const bool valid = (unsigned)src < (unsigned)L_in;  // outside [0, L_in): a zero row (padding)
+  const uint16_t* xr = x + b * x_sb + h * x_sh + (int64_t)(valid ? src : 0) * x_sl;
+  uint16_t* orow = out + b * o_sb + h * o_sh + (int64_t)j * o_sl;
+  for (int c = c8; c < nchunk; c += 8) {
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (valid) w = *reinterpret_cast<const uint4*>(xr + 8 * c);
+    *reinterpret_cast<uint4*>(orow + 8 * c) = w;
+  }
 }
 }  // namespace
 
@@ -811,7 +816,7 @@ extern "C" int sa_gather_tokens(const uint16_t* x, const int64_t x_strides[3], i
                                 void* stream) {
   SA_REQUIRE(x && x_strides && idx && out && out_strides, "sa_gather_tokens: null pointer");
   SA_REQUIRE(B > 0 && H > 0 && L_in > 0 && L_out > 0, "sa_gather_tokens: bad shape");
-  if (D != kD) return sa::fail(SA_ERR_UNSUPPORTED, "sa_gather_tokens: head_dim %d (only 64)", D);
+  if (D <= 0 || D % 8) return sa::fail(SA_ERR_UNSUPPORTED, "sa_gather_tokens: head_dim %d (a multiple of 8)", D);
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
     return sa::fail(SA_ERR_UNSUPPORTED, "sa_gather_tokens: base not 16-byte aligned");
   for (int i = 0; i < 3; ++i)
@@ -819,6 +824,6 @@ extern "C" int sa_gather_tokens(const uint16_t* x, const int64_t x_strides[3], i
   const int64_t rows = (int64_t)B * H * L_out;
   hipLaunchKernelGGL(gather_tokens_kernel, dim3(grid256(rows * 8)), dim3(256), 0, sa::as_stream(stream), x,
                      x_strides[0], x_strides[1], x_strides[2], L_in, idx, L_out, H, rows, out, out_strides[0],
-                     out_strides[1], out_strides[2]);
+                     out_strides[1], out_strides[2], D / 8);
   return sa::check_launch("sa_gather_tokens");
 }

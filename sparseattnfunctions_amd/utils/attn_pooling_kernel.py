@@ -14,10 +14,14 @@ its rows: Po = max over the block's rows of exp2(R - lse), normalised. For block
 rows' log-sum-exps are stored too, and a reduce kernel does this over two waves' rows. The
 probability matrix itself is never written.
 
-Differences from the reference: q, k and v must be bf16 (the reference also accepts fp16 and
-fp32, and casts bf16 up to fp32). head_dim must be 64. The rows of a last, partial query
-block that lie past L take no part in its maximum; the reference reads them without bounds
-checks.
+q, k and v are bf16 or fp16 (one dtype), head_dim 64 or 128. Po is fp32 for bf16 inputs and
+fp16 for fp16 inputs, the dtypes the reference returns (it computes bf16 inputs in fp32 and
+fp16 inputs in fp16, storing Po in that dtype).
+
+Differences from the reference: fp32 inputs raise TypeError (the reference also runs fp32,
+where this build has no fp32 MFMA path); bf16 inputs are computed with bf16 products where
+the reference casts them up to fp32 first. The rows of a last, partial query block that lie
+past L take no part in its maximum; the reference reads them without bounds checks.
 """
 from __future__ import annotations
 
@@ -37,7 +41,11 @@ class _attention_pooling(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, causal, sm_scale, block_size):
         assert block_size in {32, 64, 128}
-        q, k, v = _prep_qkv(q), _prep_qkv(k), _prep_qkv(v)
+        half = (torch.bfloat16, torch.float16)
+        q, k, v = _prep_qkv(q, half), _prep_qkv(k, half), _prep_qkv(v, half)
+        if not q.dtype == k.dtype == v.dtype:
+            raise TypeError(f"q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+        fp16 = q.dtype == torch.float16
         _lib.require_gpu(q, k, v)
         B, H, L, D = q.shape
         Hk = k.shape[1]
@@ -53,13 +61,14 @@ class _attention_pooling(torch.autograd.Function):
         _lib.check(lib.sa_attn_pooling_workspace(B, H, L, block_size, ctypes.byref(ws_bytes)),
                    "sa_attn_pooling_workspace")
         ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
+        fn = "sa_attn_pooling_fwd_f16" if fp16 else "sa_attn_pooling_fwd"
         with torch.cuda.device(q.device):
-            _lib.check(lib.sa_attn_pooling_fwd(
+            _lib.check(getattr(lib, fn)(
                 q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
                 v.data_ptr(), _lib.i64(*v.stride()[:3]), o.data_ptr(), _lib.i64(*o.stride()[:3]),
                 B, H, Hk, L, D, 1 if causal else 0, float(sm_scale), block_size, po.data_ptr(),
-                _lib.i64(*po.stride()[:3]), ws.data_ptr(), ws.numel(), _lib.stream_of(q)), "sa_attn_pooling_fwd")
-        return o, po
+                _lib.i64(*po.stride()[:3]), ws.data_ptr(), ws.numel(), _lib.stream_of(q)), fn)
+        return o, (po.to(torch.float16) if fp16 else po)
 
 
 attn_with_pooling = _attention_pooling.apply

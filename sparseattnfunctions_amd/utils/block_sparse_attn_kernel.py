@@ -76,7 +76,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128;
     key_bias optional fp32 [B,H,Lk] (any strides with a contiguous key axis, stride 0 to
     broadcast). `n_text_blocks` only affects scheduling (those block rows are dispatched
-    first). Row maps and tile masks need bf16 and D = 64.
+    first).
 
     Layout remapping inside the kernel (no copies): with `q_rows` (int32 [n]) the attention
     runs over n logical query rows, row i reading q's row q_rows[i] (zeros outside q); with
@@ -117,19 +117,18 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
         bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
     order = work_order(B, H, math.ceil(Lq / BLOCK), n_text_blocks, q.device)
     lib = _lib.load()
-    if fp16 and (q_rows is not None or o_rows is not None or tile_masks is not None):
-        raise NotImplementedError("row maps and tile masks need bf16 inputs")
     if q_rows is not None or o_rows is not None or tile_masks is not None:
         kv_slot, masks = (tile_masks[0], tile_masks[1]) if tile_masks is not None else (None, None)
+        fn = "sa_block_sparse_fwd_mapped_f16" if fp16 else "sa_block_sparse_fwd_mapped"
         with torch.cuda.device(q.device):
-            rc = lib.sa_block_sparse_fwd_mapped(
+            rc = getattr(lib, fn)(
                 q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
                 v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
                 B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), _lib.ptr(kv_slot), kv.max_cnt,
                 int(bool(lists_shared)), _lib.ptr(masks), bias_ptr, bias_strides, float(sm_scale),
                 _lib.ptr(q_rows), Lsrc, _lib.ptr(o_rows), out.shape[2], order.data_ptr(), order.numel(),
                 _lib.stream_of(q))
-        _lib.check(rc, "sa_block_sparse_fwd_mapped")
+        _lib.check(rc, fn)
         return out
     fn = "sa_block_sparse_fwd_f16" if fp16 else "sa_block_sparse_fwd"
     with torch.cuda.device(q.device):

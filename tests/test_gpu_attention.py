@@ -148,14 +148,15 @@ def test_uniform_negative_bias_is_shift_invariant(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125))
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float16, 64), (torch.float16, 128)])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_row_mapped_queries_and_outputs(dev, with_bias):
+def test_row_mapped_queries_and_outputs(dev, with_bias, dtype, D):
     # Logical query i reads q row q_rows[i] (-1: zero padding) and is written to out row
     # o_rows[i] (-1: dropped): a permute + pad -> attend -> unpad + unpermute in one launch.
-    case(f"row maps bias={with_bias}")
+    case(f"row maps bias={with_bias} dtype={dtype} D={D}")
     B, H, Lsrc, Lk = 2, 3, 300, 260
     g = torch.Generator().manual_seed(21)
-    q, k, v = _rand((B, H, Lsrc, 64), 150), _rand((B, H, Lk, 64), 151), _rand((B, H, Lk, 64), 152)
+    q, k, v = _rand((B, H, Lsrc, D), 150, dtype), _rand((B, H, Lk, D), 151, dtype), _rand((B, H, Lk, D), 152, dtype)
     perm = torch.randperm(Lsrc, generator=g)
     q_rows = torch.cat([perm[:150], torch.full((20,), -1), perm[150:], torch.full((10,), 7 * Lsrc)]).int()
     o_rows = q_rows.clone()
@@ -166,14 +167,15 @@ def test_row_mapped_queries_and_outputs(dev, with_bias):
     mask[..., 0] = True
     bias = torch.log(torch.randint(1, 5, (B, 1, Lk), generator=g).float()) if with_bias else None
     kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
-    out = torch.full((B, H, Lsrc, 64), 3.0, dtype=torch.bfloat16, device=dev)
-    block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=None if bias is None else bias.to(dev),
+    out = torch.full((B, H, Lsrc, D), 3.0, dtype=dtype, device=dev)
+    scale = 1 / math.sqrt(D)
+    block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, scale, key_bias=None if bias is None else bias.to(dev),
                            out=out, q_rows=q_rows.to(dev), o_rows=o_rows.to(dev))
     out = out.cpu()
     valid = (q_rows >= 0) & (q_rows < Lsrc)
-    ql = torch.zeros(B, H, Lq, 64, dtype=torch.bfloat16)
+    ql = torch.zeros(B, H, Lq, D, dtype=dtype)
     ql[:, :, valid] = q[:, :, q_rows[valid].long()]
-    want = masked_attention(ql, k, v, mask, 0.125, key_bias=None if bias is None else bias.double())
+    want = masked_attention(ql, k, v, mask, scale, key_bias=None if bias is None else bias.double())
     stored = valid.clone()
     stored[5] = False
     _check(out[:, :, o_rows[stored].long()], want[:, :, stored])

@@ -19,11 +19,11 @@ from sparseattnfunctions_amd.utils.attn_pooling_kernel import attn_with_pooling
 pytestmark = pytest.mark.gpu
 
 
-def _qkv(seed, B, H, Hk, L, scale=1.0):
+def _qkv(seed, B, H, Hk, L, scale=1.0, D=64, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
-    q = (torch.randn(B, H, L, 64, generator=g) * scale).to(torch.bfloat16)
-    k = (torch.randn(B, Hk, L, 64, generator=g) * scale).to(torch.bfloat16)
-    v = torch.randn(B, Hk, L, 64, generator=g).to(torch.bfloat16)
+    q = (torch.randn(B, H, L, D, generator=g) * scale).to(dtype)
+    k = (torch.randn(B, Hk, L, D, generator=g) * scale).to(dtype)
+    v = torch.randn(B, Hk, L, D, generator=g).to(dtype)
     return q, k, v
 
 
@@ -79,6 +79,33 @@ def test_pooled_attention_large_scores(dev):
     want_o, want_po = pooled_attention(q, k, v, False, 0.125, 64)
     assert (o.cpu().double() - want_o).abs().max().item() <= 2e-2
     assert torch.allclose(po.cpu().double(), want_po, rtol=5e-3, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128), (torch.float16, 128)])
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_pooled_attention_fp16_and_head_dim_128(dev, dtype, D, bs, causal):
+    # The reference takes fp16 as well as bf16, and any head dim of 16..256 (:252). Po comes
+    # back in the dtype the reference returns: fp16 for fp16 inputs, fp32 for bf16 ones. fp16
+    # Po adds one fp16 rounding (relative 2^-11; entries under 2^-14 are fp16 subnormals,
+    # absolute 2^-25).
+    case(f"attn_with_pooling dtype={dtype} D={D} bs={bs} causal={causal}")
+    q, k, v = _qkv(D + bs + causal, 1, 4, 2, 300, scale=1.5, D=D, dtype=dtype)
+    scale = 1 / math.sqrt(D)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, scale, bs)
+    want_o, want_po = pooled_attention(q, k, v, causal, scale, bs)
+    assert o.dtype == dtype and o.shape == q.shape
+    assert po.dtype == (torch.float16 if dtype == torch.float16 else torch.float32)
+    err = (o.cpu().double() - want_o).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3, (err.max().item(), err.mean().item())
+    assert torch.allclose(po.cpu().double(), want_po, rtol=6e-3, atol=1e-7), (po.cpu().double() - want_po).abs().max()
+
+
+def test_pooled_attention_fp32_rejected(dev):
+    case("attn_with_pooling fp32 inputs")
+    q, k, v = _qkv(3, 1, 1, 1, 64, dtype=torch.float32)
+    with pytest.raises(TypeError):
+        attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), False, 0.125, 64)
 
 
 @pytest.mark.parametrize("causal", [False, True])

@@ -45,6 +45,32 @@ def test_sta_small_config(dev):
     _check(out, _oracle(q, k, v, cfg))
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128), (torch.float16, 128)])
+def test_sta_small_config_fp16_and_head_dim_128(dev, dtype, D):
+    # flex_attention takes any 16-bit dtype and head dim: the tile-mask mode and the token
+    # gathers of both layouts (fused row maps in forward, copies in preprocess).
+    case(f"STA small grid dtype={dtype} D={D}")
+    cfg = {"kernel_size": (1, 3, 3), "tile_size": (2, 3, 3), "img_size": (4, 12, 15), "text_length": 226}
+    L = 226 + 4 * 12 * 15
+    g = torch.Generator().manual_seed(D)
+    q, k, v = (torch.randn(1, 2, L, D, generator=g).to(dtype) for _ in range(3))
+    proc = SildingTileAttention(cfg)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    out = proc(qd, kd, vd)
+    assert out.dtype == dtype and out.shape == q.shape
+    text, img, tile, kern = cfg["text_length"], cfg["img_size"], cfg["tile_size"], cfg["kernel_size"]
+    perm = sta.permutation(text, img, tile)
+    qp, kp, vp = (x[:, :, perm] for x in (q, k, v))
+    nb = math.ceil(L / 64)
+    want = masked_attention(qp, kp, vp, torch.ones(1, 1, nb, nb, dtype=torch.bool), 1 / math.sqrt(D),
+                            token_mask=lambda rows: sta.token_mask(rows, L, text, img, tile, kern))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(L)
+    _check(out, want[:, :, inv])
+    copies = proc.process_out_back(proc.attention(*proc.preprocess(qd, kd, vd)))
+    assert torch.equal(copies, out)
+
+
 def test_sta_default_config_full_shape(dev):
     case("STA CogVideoX-2B default config")
     q, k, v = cogvideox_qkv(0)
