@@ -208,6 +208,32 @@ __device__ inline void dma_tile(const void* base, uint32_t bytes, uint32_t tile_
                                              tile_off + 8 * i * row_bytes + goff[i & 1], 0, 0, 0);
 }
 
+// dma_tile for a tile of contiguous 128-byte rows (head dim 64, row stride 64 elements): the
+// same copies, with the descriptors based at the tile's rows 0 and 32, so that the lane
+// offsets stay loop invariant and the instruction offset (added to both the global and the
+// LDS address) steps the 8-row groups; no per-tile vector address arithmetic. Each
+// descriptor's size ends at the same byte as dma_tile's (0 when row 32 lies past it): a lane
+// reads offset goff + 1024 j of the descriptor at off iff off + goff + 1024 j < bytes, so rows
+// past Lk read as zero as before.
+__device__ inline void dma_tile_c128(const uint16_t* base, uint32_t bytes, uint32_t tile_off,
+                                     const uint32_t (&goff)[2], lds_u8* dst) {
+#pragma unroll
+  for (int hq = 0; hq < 2; ++hq) {
+    // Wave-uniform by construction; readfirstlane lets the compiler build the descriptor
+    // in scalar registers.
+    const uint32_t off = __builtin_amdgcn_readfirstlane(tile_off + 4096u * hq);
+    const uint32_t end = __builtin_amdgcn_readfirstlane(bytes);
+    const int size = __builtin_amdgcn_readfirstlane(end - min(off, end));
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(base) + off), (short)0, size, 0x00020000);
+    lds_u8* d = dst + 4096 * hq;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, d, 16, goff[0], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, d, 16, goff[1], 0, 1024, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, d, 16, goff[0], 0, 2048, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, d, 16, goff[1], 0, 3072, 0);
+  }
+}
+
 // Waits until at most n LDS reads are outstanding (n in 0..14, even), tying the wait to
 // the two registers it makes valid so that nothing reads them earlier.
 __device__ __forceinline__ void lgkm_wait_pair(int n, sa_u32x2v& a, sa_u32x2v& b) {
@@ -282,6 +308,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
   const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
   const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
+  const bool c128 = krow == 128 && vrow == 128;  // contiguous d = 64 rows: dma_tile_c128
   lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes * kHalves;
   lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes * kHalves;
   float* bl_lds = b_lds + (kBias ? wave * kBlock : 0);
@@ -357,8 +384,13 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       mw[0] = mrow[col];
       mw[1] = mrow[32 + col];
     }
+    if (kD == 64 && c128) {
+      dma_tile_c128(khead, kbytes, kb0 * krow, kgo, kl);
+    } else {
 #pragma unroll
-    for (int hf = 0; hf < kHalves; ++hf) dma_tile(khead + 64 * hf, kbytes, kb0 * krow, krow, kgo, kl + hf * kTileBytes);
+      for (int hf = 0; hf < kHalves; ++hf)
+        dma_tile(khead + 64 * hf, kbytes, kb0 * krow, krow, kgo, kl + hf * kTileBytes);
+    }
   };
   // Group V of tile `kb`: bias copy (keys past Lk read as zero), V copy.
   auto issue_v = [&](int kb) {
@@ -368,8 +400,13 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
                                                                           a.Lk * 4, 0x00020000);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_u8*)bl_lds, 4, (kb0 + lane) * 4, 0, 0, 0);
     }
+    if (kD == 64 && c128) {
+      dma_tile_c128(vhead, vbytes, kb0 * vrow, vgo, vl);
+    } else {
 #pragma unroll
-    for (int hf = 0; hf < kHalves; ++hf) dma_tile(vhead + 64 * hf, vbytes, kb0 * vrow, vrow, vgo, vl + hf * kTileBytes);
+      for (int hf = 0; hf < kHalves; ++hf)
+        dma_tile(vhead + 64 * hf, vbytes, kb0 * vrow, vrow, vgo, vl + hf * kTileBytes);
+    }
   };
 
   // One pass over the item's key blocks. Fast pass (kSafe = false): P = exp2(S) with no
