@@ -106,7 +106,6 @@ __device__ inline uint32_t order_bits(float f) {
 // writes the union with text rows/columns and the local window as the ascending kv list.
 template <int NCH>
 __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
-  __shared__ __attribute__((aligned(16))) float q_lds[kRowsPerWG][kPoolD];
   __shared__ __attribute__((aligned(16))) float k_lds[kColChunk * kKpStride];
 
   const int tid = threadIdx.x;
@@ -142,17 +141,27 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       }
     }
   } else {
-    // q rows and 64-column chunks of pooled K staged as float4; score = fmaf chain over
-    // d ascending (the same order as the oracle), 4 rows per thread.
-    for (int e = tid; e < kRowsPerWG * (kPoolD / 4); e += 256) {
-      const int rr = e >> 4, d4 = e & 15;
-      const float4 v = (r0 + rr < a.nqb)
-                           ? *reinterpret_cast<const float4*>(a.qp + (row_base + r0 + rr) * kPoolD + 4 * d4)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-      *reinterpret_cast<float4*>(&q_lds[rr][4 * d4]) = v;
-    }
+    // 64-column chunks of pooled K staged in LDS as float4; the wave's 4 q rows come through
+    // scalar loads (wave-uniform rows; rows past nqb read row nqb - 1 and are discarded).
+    // score = fmaf chain over d ascending (the same order as the oracle), 4 rows per thread.
     const float* kpb = a.kp + (int64_t)bh * a.nkb * kPoolD;
     const int rg = wave * 4;
+    const __attribute__((address_space(4))) float* qrow[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      qrow[u] = (const __attribute__((address_space(4))) float*)(a.qp + (row_base + min(r0 + rg + u, a.nqb - 1)) * kPoolD);
+    // Chunk e + 1 of pooled K is loaded into registers while chunk e is scored, so only
+    // the first chunk's load latency is exposed. Thread t holds float4 t + 256 j (j < 4) of
+    // a chunk: column (t + 256 j) / 16, dims 4 ((t + 256 j) % 16) .. + 3.
+    constexpr int kPer = kColChunk * (kPoolD / 4) / 256;  // float4 per thread and chunk: 4
+    float4 pre[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {  // chunk 0
+      const int i = tid + 256 * j;
+      pre[j] = i < min(kColChunk, a.nkb) * (kPoolD / 4)
+                   ? *reinterpret_cast<const float4*>(kpb + (int64_t)(i >> 4) * kPoolD + 4 * (i & 15))
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
     for (int e = 0; e < NCH; ++e) {
 #pragma unroll
@@ -161,12 +170,22 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
         const int c0 = e * kColChunk;
         __syncthreads();
         const int nc = min(kColChunk, a.nkb - c0);
-        for (int i = tid; i < nc * (kPoolD / 4); i += 256) {
-          const int c = i >> 4, d4 = i & 15;
-          *reinterpret_cast<float4*>(&k_lds[c * kKpStride + 4 * d4]) =
-              *reinterpret_cast<const float4*>(kpb + (int64_t)(c0 + c) * kPoolD + 4 * d4);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+          const int i = tid + 256 * j;
+          if (i < nc * (kPoolD / 4)) *reinterpret_cast<float4*>(&k_lds[(i >> 4) * kKpStride + 4 * (i & 15)]) = pre[j];
         }
         __syncthreads();
+        if (e + 1 < nch) {  // chunk e + 1 into registers while chunk e is scored
+          const int c1 = c0 + kColChunk;
+          const int nc1 = min(kColChunk, a.nkb - c1);
+#pragma unroll
+          for (int j = 0; j < kPer; ++j) {
+            const int i = tid + 256 * j;
+            if (i < nc1 * (kPoolD / 4))
+              pre[j] = *reinterpret_cast<const float4*>(kpb + (int64_t)(c1 + (i >> 4)) * kPoolD + 4 * (i & 15));
+          }
+        }
         if (lane < nc) {
           float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
@@ -174,7 +193,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
             const float4 kv = *reinterpret_cast<const float4*>(&k_lds[lane * kKpStride + d]);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-              const float4 qv = *reinterpret_cast<const float4*>(&q_lds[rg + u][d]);
+              const float4 qv = make_float4(qrow[u][d], qrow[u][d + 1], qrow[u][d + 2], qrow[u][d + 3]);
               acc[u] = fmaf(qv.x, kv.x, acc[u]);
               acc[u] = fmaf(qv.y, kv.y, acc[u]);
               acc[u] = fmaf(qv.z, kv.z, acc[u]);
