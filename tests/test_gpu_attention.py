@@ -107,6 +107,38 @@ def test_strided_and_broadcast(dev):
     _check(out, want)
 
 
+@pytest.mark.parametrize("Lk", [20, 33, 57, 100, 300, 1000])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_contiguous_and_strided_key_rows_agree(dev, Lk, with_bias):
+    # Contiguous 64-element K/V rows are copied through per-tile buffer descriptors based at
+    # the tile's rows 0 and 32 (sized to the head's last row; empty when row 32 is past it);
+    # strided rows through per-load offsets. Same values, same arithmetic: bit-identical
+    # outputs, including the partial last tile and Lk < 32 (an empty second descriptor).
+    case(f"contiguous vs strided K/V Lk={Lk} bias={with_bias}")
+    B, H, Lq = 2, 3, 130
+    q = _rand((B, H, Lq, 64), 160).to(dev)
+    kc, vc = _rand((B, H, Lk, 64), 161).to(dev), _rand((B, H, Lk, 64), 162).to(dev)
+    ks = torch.empty(B, Lk, H, 64, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+    vs = torch.empty(B, Lk, H, 64, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+    ks.copy_(kc)
+    vs.copy_(vc)
+    assert ks.stride(2) == H * 64 and kc.stride(2) == 64
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    g = torch.Generator().manual_seed(Lk)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.7
+    mask[..., nkb - 1] = True  # the partial last tile in every row
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    bias = None
+    if with_bias:
+        bias = torch.log(torch.randint(1, 5, (B, H, Lk), generator=g).float()).to(dev)
+    oc = block_sparse_attention(q, kc, vc, kv, 0.125, key_bias=bias)
+    os_ = block_sparse_attention(q, ks, vs, kv, 0.125, key_bias=bias)
+    assert torch.equal(oc, os_)
+    want = masked_attention(q.cpu(), kc.cpu(), vc.cpu(), mask, 0.125,
+                            key_bias=None if bias is None else bias.cpu().double())
+    _check(oc, want)
+
+
 def test_key_bias(dev):
     case("key bias")
     B, H, L = 2, 3, 700
