@@ -117,13 +117,18 @@ def other_configs(q, k, v, dev):
     out = {}
     B, H, L, D = q.shape
 
-    # C1: the reference's CPU-runnable case (B=1, H=2, L=2048, random block mask), in bf16.
+    # C1: the reference's CPU-runnable case (B=1, H=2, L=2048, random block mask), in bf16 and in
+    # the configuration's own fp32 (the fp32 kernel).
     q1, k1, v1, m1, s1 = config1_inputs()
     q1, k1, v1, m1 = (t.to(dev) for t in (q1.bfloat16(), k1.bfloat16(), v1.bfloat16(), m1))
     ms = time_fn(lambda: block_sparse_triton_fn(q1, k1, v1, m1, s1))
     f1 = 4 * 64 * kv_list_from_mask(m1, 1, 2, 32, 32).computed_pairs(2048, 2048)
+    q1f, k1f, v1f, _, _ = config1_inputs()
+    q1f, k1f, v1f = (t.to(dev) for t in (q1f, k1f, v1f))
+    ms_f32 = time_fn(lambda: block_sparse_triton_fn(q1f, k1f, v1f, m1, s1))
     out["c1"] = {"ms": round(ms, 4), "tflops": _tflops(f1, ms), "block_density": round(m1.float().mean().item(), 4),
-                 "dtype": "bf16 (the fp32 inputs of the configuration rounded to bf16: the kernel takes bf16)"}
+                 "dtype": "bf16 (the configuration's fp32 inputs rounded to bf16)",
+                 "fp32_ms": round(ms_f32, 4), "fp32_tflops": _tflops(f1, ms_f32)}
 
     _progress("c1 done")
 
@@ -282,13 +287,16 @@ def other_configs(q, k, v, dev):
     out["reference_perf_no_mask"] = sweep
     _progress("reference_perf_no_mask done")
 
-    # The kernel's other input types on the C2 kv lists: fp16 q/k/v, and head dim 128 (15 heads
+    # The kernel's other input types on the C2 kv lists: fp16 and fp32 q/k/v, and head dim 128 (15 heads
     # of 128 = the same hidden size 1920, the lists of the first 15 heads of each batch item).
     kvc = BlockSparseAttention(64, keep_ratio=0.2).build_kv_list(q, k)
     f_c2 = 4 * D * kvc.computed_pairs(L, L)
     q16, k16, v16 = q.half(), k.half(), v.half()
     ms_f16 = time_fn(lambda: block_sparse_attention(q16, k16, v16, kvc, 0.125, n_text_blocks=4))
     del q16, k16, v16
+    q32, k32, v32 = q.float(), k.float(), v.float()
+    ms_f32 = time_fn(lambda: block_sparse_attention(q32, k32, v32, kvc, 0.125, n_text_blocks=4))
+    del q32, k32, v32
     sel = (torch.arange(2)[:, None] * 30 + torch.arange(15)[None, :]).reshape(-1)
     rows = (sel[:, None] * kvc.nqb + torch.arange(kvc.nqb)[None, :]).reshape(-1).to(dev)
     kv128 = KVList(kvc.idx[rows].contiguous(), kvc.cnt[rows].contiguous(), 2, 15, kvc.nqb, kvc.nkb)
@@ -298,6 +306,7 @@ def other_configs(q, k, v, dev):
     ms_128 = time_fn(lambda: block_sparse_attention(q8, k8, v8, kv128, 1 / math.sqrt(128), n_text_blocks=4))
     del q8, k8, v8
     out["attention_variants"] = {"fp16_c2_ms": round(ms_f16, 4), "fp16_c2_tflops": _tflops(f_c2, ms_f16),
+                                 "fp32_c2_ms": round(ms_f32, 4), "fp32_c2_tflops": _tflops(f_c2, ms_f32),
                                  "head_dim_128_ms": round(ms_128, 4), "head_dim_128_tflops": _tflops(f128, ms_128),
                                  "head_dim_128_shape": [2, 15, L, 128]}
     _progress("attention_variants done")

@@ -99,6 +99,20 @@ int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const
                             const int32_t* work_order, int64_t n_slots, void* stream);
 
 /*
+ * sa_block_sparse_fwd for fp32 q, k, v and out (the reference kernel also runs on fp32 tiles,
+ * :52-209, with P cast to v's dtype, :107, so kept in fp32): same arguments and list contract,
+ * head dim 64, key_bias must be NULL (SA_ERR_UNSUPPORTED otherwise). fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32), running row maximum, P and row sums in fp32. Strides in elements,
+ * multiples of 4; bases 16-byte aligned.
+ */
+int sa_block_sparse_fwd_f32(const float* q, const int64_t q_strides[3], const float* k,
+                            const int64_t k_strides[3], const float* v, const int64_t v_strides[3],
+                            float* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                            int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                            const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                            const int32_t* work_order, int64_t n_slots, void* stream);
+
+/*
  * Block-sparse attention with token-level masks inside cut blocks: as sa_block_sparse_fwd
  * (bf16, D = 64 or 128), plus kv_slot[row][i] = -1 (every pair of the tile attends) or the index of a 64x64
  * bitmask in tile_masks (uint64 [slots][64]: bit c of word r = query r of the block may

@@ -18,9 +18,9 @@ q, k and v are bf16 or fp16 (one dtype), head_dim 64 or 128. Po is fp32 for bf16
 fp16 for fp16 inputs, the dtypes the reference returns (it computes bf16 inputs in fp32 and
 fp16 inputs in fp16, storing Po in that dtype).
 
-Differences from the reference: fp32 inputs raise TypeError (the reference also runs fp32,
-where this build has no fp32 MFMA path); bf16 inputs are computed with bf16 products where
-the reference casts them up to fp32 first. The rows of a last, partial query block that lie
+Differences from the reference: fp32 inputs raise TypeError (the reference also runs fp32;
+this build's fp32 attention kernel has no pooling mode); bf16 inputs are computed with bf16
+products where the reference casts them up to fp32 first. The rows of a last, partial query block that lie
 past L take no part in its maximum; the reference reads them without bounds checks.
 """
 from __future__ import annotations

@@ -11,9 +11,11 @@ libsa_hip.so (`sa_mask_to_kv_list` + `sa_block_sparse_fwd`), not Triton.
 
 Inputs are bf16 or fp16 (all three the same), head_dim 64 or 128 as the reference asserts
 (:231); P is rounded to the input dtype before P.V as the reference rounds it to v's (:107).
+fp32 inputs run the fp32 kernel (`sa_block_sparse_fwd_f32`: fp32 MFMA, P kept in fp32, as the
+reference's cast to v's dtype leaves it), head_dim 64.
 
 Differences from the reference, by design:
-  * fp32 inputs are not accepted (the reference's tl.dot would take them): TypeError;
+  * fp32 inputs need head_dim 64 (the reference also takes 128);
   * a query block whose mask row is empty yields 0 instead of NaN (:201-203);
   * sm_scale must be > 0.
 """
@@ -35,7 +37,8 @@ def _prep_qkv(t: torch.Tensor, dtypes=(torch.bfloat16,)) -> torch.Tensor:
     vector loads)."""
     if t.dtype not in dtypes:
         raise TypeError(f"expected {' or '.join(str(d) for d in dtypes)} tensors, got {t.dtype}")
-    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:-1]):
+    per16 = 16 // t.element_size()  # elements per 16 bytes
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % per16 for s in t.stride()[:-1]):
         t = t.contiguous()
     return t
 
@@ -73,7 +76,8 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                            n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
-    q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128;
+    q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128, or fp32
+    with D = 64 (plain lists only: fp32 MFMA, P kept in fp32 as the reference's kernel does);
     key_bias optional fp32 [B,H,Lk] (any strides with a contiguous key axis, stride 0 to
     broadcast). `n_text_blocks` only affects scheduling (those block rows are dispatched
     first).
@@ -85,11 +89,14 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     lists_shared) adds token-level masks inside cut blocks.
     """
     _lib.require_gpu(q, k, v)
-    half = (torch.bfloat16, torch.float16)
-    q, k, v = _prep_qkv(q, half), _prep_qkv(k, half), _prep_qkv(v, half)
+    types = (torch.bfloat16, torch.float16, torch.float32)
+    q, k, v = _prep_qkv(q, types), _prep_qkv(k, types), _prep_qkv(v, types)
     if not q.dtype == k.dtype == v.dtype:
         raise TypeError(f"q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     fp16 = q.dtype == torch.float16
+    fp32 = q.dtype == torch.float32
+    if fp32 and (key_bias is not None or q_rows is not None or o_rows is not None or tile_masks is not None):
+        raise NotImplementedError("fp32 inputs: plain block lists only (no key_bias, row maps or tile masks)")
     B, H, Lsrc, D = q.shape
     q_rows, o_rows = _row_map(q_rows, q.device), _row_map(o_rows, q.device)
     Lq = q_rows.numel() if q_rows is not None else (o_rows.numel() if o_rows is not None else Lsrc)
@@ -130,7 +137,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                 _lib.stream_of(q))
         _lib.check(rc, fn)
         return out
-    fn = "sa_block_sparse_fwd_f16" if fp16 else "sa_block_sparse_fwd"
+    fn = "sa_block_sparse_fwd_f16" if fp16 else ("sa_block_sparse_fwd_f32" if fp32 else "sa_block_sparse_fwd")
     with torch.cuda.device(q.device):
         rc = getattr(lib, fn)(
             q.data_ptr(), _lib.i64(*q.stride()[:3]),

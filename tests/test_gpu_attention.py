@@ -323,11 +323,75 @@ def test_fp16_large_scores_use_running_max(dev):
     _check(out, masked_attention(q, k, v, mask, 1 / 8))
 
 
-def test_mixed_or_fp32_dtypes_rejected(dev):
+def test_mixed_or_fp64_dtypes_rejected(dev):
     case("dtype errors")
     q = _rand((1, 1, 64, 64), 150).to(dev)
     m = torch.ones(1, 1, 1, 1, dtype=torch.bool, device=dev)
     with pytest.raises(TypeError):
         block_sparse_triton_fn(q, q.half(), q, m, 1 / 8)
     with pytest.raises(TypeError):
-        block_sparse_triton_fn(q.float(), q.float(), q.float(), m, 1 / 8)
+        block_sparse_triton_fn(q.float(), q.float(), q, m, 1 / 8)
+    with pytest.raises(TypeError):
+        block_sparse_triton_fn(q.double(), q.double(), q.double(), m, 1 / 8)
+    with pytest.raises(NotImplementedError):  # fp32 kernel: head dim 64
+        qq = torch.randn(1, 1, 64, 128, device=dev)
+        block_sparse_triton_fn(qq, qq, qq, m, 1 / 8)
+
+
+# fp32 inputs: the reference's kernel takes them too (tl.dot on fp32 tiles, P cast to v's
+# dtype, so kept in fp32). Without the bf16 rounding of P the bar is fp32 accuracy: max-abs
+# 2e-5, mean-abs 2e-6 against the fp64 oracle on the same fp32 inputs.
+F32_MAX, F32_MEAN = 2e-5, 2e-6
+
+
+def _check_f32(got, want, max_abs=F32_MAX, mean_abs=F32_MEAN):
+    assert got.dtype == torch.float32
+    err = (got.cpu().double() - want).abs()
+    assert torch.isfinite(got).all()
+    assert err.max().item() <= max_abs, err.max().item()
+    assert err.mean().item() <= mean_abs, err.mean().item()
+
+
+def test_config1_parity_fp32(dev):
+    # BASELINE configs[0] in its own dtype: B=1, H=2, L=2048, d=64, fp32, the seed-1 mask.
+    case("C1 fp32")
+    q, k, v, mask, scale = config1_inputs()
+    assert q.dtype == torch.float32
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+    _check_f32(out, masked_attention(q, k, v, mask, scale))
+
+
+@pytest.mark.parametrize("Lq,Lk,seed", [(257, 257, 1), (130, 385, 2), (64, 20, 3), (1000, 1000, 4)])
+def test_fp32_random_masks(dev, Lq, Lk, seed):
+    # partial last tiles, Lq != Lk, an empty row, an entry outside the grid in one list
+    case(f"fp32 Lq={Lq} Lk={Lk}")
+    B, H = 2, 3
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, n, 64, generator=g) for n in (Lq, Lk, Lk))
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.5
+    mask[..., nkb - 1] = True
+    mask[1, 2, 0] = False  # an empty row writes 0
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    first = kv.idx[0, 0].item()  # row (0, 0, 0): its first entry moved outside the grid is skipped
+    kv.idx[0, 0] = nkb + 3
+    mask[0, 0, 0, first] = False
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125)
+    _check_f32(out, masked_attention(q, k, v, mask, 0.125))
+    assert torch.all(out[1, 2, :64] == 0)
+
+
+def test_fp32_strided_and_large_scores(dev):
+    # BLHD views (strided rows) and scores of several hundred (the running maximum)
+    case("fp32 strided, large scores")
+    B, L, H = 1, 300, 2
+    g = torch.Generator().manual_seed(9)
+    base = [torch.randn(B, L, H, 64, generator=g) * (6.0 if i < 2 else 1.0) for i in range(3)]
+    q, k, v = (t.to(dev).permute(0, 2, 1, 3) for t in base)
+    nb = math.ceil(L / 64)
+    mask = torch.rand(1, 1, nb, nb, generator=g) < 0.6
+    mask[..., 0] = True
+    out = block_sparse_triton_fn(q, k, v, mask.to(dev), 0.125)
+    # logits up to ~300: fp32 rounding of a logit alone is 2^-24 * 300 ~ 2e-5, so the bar
+    # scales with them (max-abs 1e-4)
+    _check_f32(out, masked_attention(*(t.permute(0, 2, 1, 3) for t in base), mask, 0.125), 1e-4, 1e-5)
