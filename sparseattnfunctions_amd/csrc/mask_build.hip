@@ -20,7 +20,8 @@
 namespace {
 
 constexpr int kPoolD = 64;        // head dim handled by the pooling kernel
-constexpr int kRowsPerWG = 16;    // score rows per top-k workgroup (4 per wave)
+constexpr int kRowsPerWG = 24;    // score rows per top-k workgroup
+constexpr int kTopkR = 3;         // score rows per top-k wave (8 waves per workgroup)
 constexpr int kColChunk = 64;     // key blocks staged in LDS per step
 constexpr int kKpStride = 68;     // LDS stride (floats) of a staged pooled-K row (float4, conflict-free)
 static_assert(kColChunk == 64, "topk_kernel maps chunk e to the wave's key column 64e + lane");
@@ -79,7 +80,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Top-k: workgroup = 16 score rows of one (b, h); wave w selects rows 4w..4w+3.
+// Top-k: workgroup = kRowsPerWG score rows of one (b, h); wave w selects rows kR w .. kR w + kR - 1.
 struct TopkArgs {
   const float* qp;         // [BH][nqb][D] (null when scores_in is given)
   const float* kp;         // [BH][nkb][D]
@@ -104,8 +105,9 @@ __device__ inline uint32_t order_bits(float f) {
 // in ascending column order keeps every key > T and the lowest-index keys == T until k are
 // kept -- exactly the first k columns in (score descending, column ascending) order -- and
 // writes the union with text rows/columns and the local window as the ascending kv list.
-template <int NCH>
-__global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
+template <int NCH, int kR>
+__global__ __launch_bounds__(64 * kRowsPerWG / kR) void topk_kernel(TopkArgs a) {
+  constexpr int kThreads = 64 * kRowsPerWG / kR;  // kR score rows per wave
   __shared__ __attribute__((aligned(16))) float k_lds[kColChunk * kKpStride];
 
   const int tid = threadIdx.x;
@@ -117,19 +119,19 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   const int nch = (a.nkb + 63) >> 6;
   const int k = a.topk < a.nkb ? a.topk : a.nkb;
 
-  // Lane `lane` of wave w holds column 64e + lane of rows 4w..4w+3 as ordered keys (0 =
+  // Lane `lane` of wave w holds column 64e + lane of rows kR w + u as ordered keys (0 =
   // unused). The score loop below produces exactly this mapping, so the scores go from
   // the FMA accumulators into the keys without an LDS round trip; the workgroup's LDS is
   // only the staged q rows and one 64-column chunk of pooled K.
-  uint32_t key[4][NCH];
-  bool live[4];
+  uint32_t key[kR][NCH];
+  bool live[kR];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) live[u] = r0 + wave * 4 + u < a.nqb;  // wave-uniform
+  for (int u = 0; u < kR; ++u) live[u] = r0 + wave * kR + u < a.nqb;  // wave-uniform
 
   if (a.scores_in) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t row = row_base + r0 + wave * 4 + u;
+    for (int u = 0; u < kR; ++u) {
+      const int64_t row = row_base + r0 + wave * kR + u;
 #pragma unroll
       for (int e = 0; e < NCH; ++e) {
         const int c = 64 * e + lane;
@@ -141,23 +143,24 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       }
     }
   } else {
-    // 64-column chunks of pooled K staged in LDS as float4; the wave's 4 q rows come through
+    // 64-column chunks of pooled K staged in LDS as float4; the wave's kR q rows come through
     // scalar loads (wave-uniform rows; rows past nqb read row nqb - 1 and are discarded).
-    // score = fmaf chain over d ascending (the same order as the oracle), 4 rows per thread.
+    // score = fmaf chain over d ascending (the same order as the oracle), kR rows per thread.
     const float* kpb = a.kp + (int64_t)bh * a.nkb * kPoolD;
-    const int rg = wave * 4;
-    const __attribute__((address_space(4))) float* qrow[4];
+    const int rg = wave * kR;
+    const __attribute__((address_space(4))) float* qrow[kR];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < kR; ++u)
       qrow[u] = (const __attribute__((address_space(4))) float*)(a.qp + (row_base + min(r0 + rg + u, a.nqb - 1)) * kPoolD);
     // Chunk e + 1 of pooled K is loaded into registers while chunk e is scored, so only
-    // the first chunk's load latency is exposed. Thread t holds float4 t + 256 j (j < 4) of
-    // a chunk: column (t + 256 j) / 16, dims 4 ((t + 256 j) % 16) .. + 3.
-    constexpr int kPer = kColChunk * (kPoolD / 4) / 256;  // float4 per thread and chunk: 4
+    // the first chunk's load latency is exposed. Thread t holds float4 t + kThreads j (j < kPer)
+    // of a chunk: column (t + kThreads j) / 16, dims 4 ((t + kThreads j) % 16) .. + 3.
+    constexpr int kPer = kColChunk * (kPoolD / 4) / kThreads;  // float4 per thread and chunk
+    static_assert(kPer * kThreads == kColChunk * (kPoolD / 4), "a chunk is whole float4 per thread");
     float4 pre[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {  // chunk 0
-      const int i = tid + 256 * j;
+      const int i = tid + kThreads * j;
       pre[j] = i < min(kColChunk, a.nkb) * (kPoolD / 4)
                    ? *reinterpret_cast<const float4*>(kpb + (int64_t)(i >> 4) * kPoolD + 4 * (i & 15))
                    : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -165,14 +168,14 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
 #pragma unroll
     for (int e = 0; e < NCH; ++e) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) key[u][e] = 0u;
+      for (int u = 0; u < kR; ++u) key[u][e] = 0u;
       if (e < nch) {  // workgroup-uniform, so the barriers below are too
         const int c0 = e * kColChunk;
         __syncthreads();
         const int nc = min(kColChunk, a.nkb - c0);
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
-          const int i = tid + 256 * j;
+          const int i = tid + kThreads * j;
           if (i < nc * (kPoolD / 4)) *reinterpret_cast<float4*>(&k_lds[(i >> 4) * kKpStride + 4 * (i & 15)]) = pre[j];
         }
         __syncthreads();
@@ -181,18 +184,20 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
           const int nc1 = min(kColChunk, a.nkb - c1);
 #pragma unroll
           for (int j = 0; j < kPer; ++j) {
-            const int i = tid + 256 * j;
+            const int i = tid + kThreads * j;
             if (i < nc1 * (kPoolD / 4))
               pre[j] = *reinterpret_cast<const float4*>(kpb + (int64_t)(c1 + (i >> 4)) * kPoolD + 4 * (i & 15));
           }
         }
         if (lane < nc) {
-          float acc[4] = {0.f, 0.f, 0.f, 0.f};
+          float acc[kR];
+#pragma unroll
+          for (int u = 0; u < kR; ++u) acc[u] = 0.f;
 #pragma unroll 4
           for (int d = 0; d < kPoolD; d += 4) {
             const float4 kv = *reinterpret_cast<const float4*>(&k_lds[lane * kKpStride + d]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < kR; ++u) {
               const float4 qv = make_float4(qrow[u][d], qrow[u][d + 1], qrow[u][d + 2], qrow[u][d + 3]);
               acc[u] = fmaf(qv.x, kv.x, acc[u]);
               acc[u] = fmaf(qv.y, kv.y, acc[u]);
@@ -201,7 +206,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
             }
           }
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
+          for (int u = 0; u < kR; ++u) {
             if (!live[u]) continue;
             key[u][e] = order_bits(acc[u]);
             if (a.scores_out) a.scores_out[(row_base + r0 + rg + u) * a.nkb + c0 + lane] = acc[u];
@@ -211,7 +216,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     }
   }
 
-  // The wave's 4 rows are selected together: their 32-step searches are independent chains
+  // The wave's kR rows are selected together: their 32-step searches are independent chains
   // of ballot -> popcount -> compare, interleaved to hide each other's latency.
   // The search keeps thr = the largest prefix with count(key >= thr) >= k. Once a candidate
   // has exactly k keys at or above it, every later accepted candidate has exactly k as well,
@@ -219,15 +224,17 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
   // minimum m. So the wave stops when each of its rows has seen an exact count, and every
   // row then takes thr = min{key >= thr} (for a row that ran all 32 steps thr is already a
   // key, and the minimum returns it). On C2 rows this ends the search after ~20 of 32 steps.
-  uint32_t thr[4] = {0u, 0u, 0u, 0u};  // the k-th largest key (0 when k == 0: nothing selected)
+  uint32_t thr[kR];  // the k-th largest key (0 when k == 0: nothing selected)
+#pragma unroll
+  for (int u = 0; u < kR; ++u) thr[u] = 0u;
   if (k > 0) {
     // Bit u set: row u has seen an exact count (rows past nqb never search). Scalar.
     int exact = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) exact |= live[u] ? 0 : 1 << u;
-    for (int bit = 31; bit >= 0 && exact != 15; --bit) {
+    for (int u = 0; u < kR; ++u) exact |= live[u] ? 0 : 1 << u;
+    for (int bit = 31; bit >= 0 && exact != (1 << kR) - 1; --bit) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kR; ++u) {
         const uint32_t cand = thr[u] | (1u << bit);
         int count = 0;
 #pragma unroll
@@ -237,7 +244,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kR; ++u) {
       uint32_t m = 0xffffffffu;
 #pragma unroll
       for (int e = 0; e < NCH; ++e) m = key[u][e] >= thr[u] ? min(m, key[u][e]) : m;
@@ -247,9 +254,9 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
     }
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < kR; ++u) {
     if (!live[u]) break;  // wave-uniform; later rows are past nqb as well
-    const int r = r0 + wave * 4 + u;
+    const int r = r0 + wave * kR + u;
     const int64_t row = row_base + r;
     int need = 0;  // keys equal to thr to keep, lowest columns first
     if (k > 0) {
@@ -341,13 +348,13 @@ extern "C" int sa_block_topk_kv_list(const float* q_pooled, const float* k_poole
   SA_REQUIRE(grid < (1LL << 31), "sa_block_topk_kv_list: grid too large");
   hipStream_t s = sa::as_stream(stream);
   if (nkb <= 256) {
-    hipLaunchKernelGGL(topk_kernel<4>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((topk_kernel<4, kTopkR>), dim3((unsigned)grid), dim3(64 * kRowsPerWG / kTopkR), 0, s, a);
   } else if (nkb <= 320) {
-    hipLaunchKernelGGL(topk_kernel<5>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((topk_kernel<5, kTopkR>), dim3((unsigned)grid), dim3(64 * kRowsPerWG / kTopkR), 0, s, a);
   } else if (nkb <= 512) {
-    hipLaunchKernelGGL(topk_kernel<8>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((topk_kernel<8, kTopkR>), dim3((unsigned)grid), dim3(64 * kRowsPerWG / kTopkR), 0, s, a);
   } else {
-    hipLaunchKernelGGL(topk_kernel<16>, dim3((unsigned)grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((topk_kernel<16, kTopkR>), dim3((unsigned)grid), dim3(64 * kRowsPerWG / kTopkR), 0, s, a);
   }
   return sa::check_launch("sa_block_topk_kv_list");
 }
