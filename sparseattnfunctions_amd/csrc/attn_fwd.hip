@@ -269,9 +269,11 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // tell a copy into one from a read of another.
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes * kHalves];
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kWaves * kTileBytes * kHalves];
-  __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * kBlock : 4];
+  // Bias rows: three 64-key slots per wave (list positions of even and odd index, and a slot
+  // for the copies issued past the end of the list, which nothing reads).
+  __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * 3 * kBlock : 4];
   // Vector-memory operations per tile, in issue order: group K = [mask rows (2)] [K (8 per
-  // half)], group V = [bias (1)] [V (8 per half)]. The waits below count them.
+  // half)], group V = [bias of the next tile (1)] [V (8 per half)]. The waits below count them.
   constexpr int kGroupK = 8 * kHalves + (kMask ? 2 : 0);
   constexpr int kGroupV = 8 * kHalves + (kBias ? 1 : 0);
 
@@ -311,7 +313,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const bool c128 = krow == 128 && vrow == 128;  // contiguous d = 64 rows: dma_tile_c128
   lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes * kHalves;
   lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes * kHalves;
-  float* bl_lds = b_lds + (kBias ? wave * kBlock : 0);
+  float* bl_lds = b_lds + (kBias ? wave * 3 * kBlock : 0);
 
   // Lane constants: copy offsets, K operand read offsets, V^T transposed read offsets.
   uint32_t kgo[2], vgo[2];
@@ -392,14 +394,21 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         dma_tile(khead + 64 * hf, kbytes, kb0 * krow, krow, kgo, kl + hf * kTileBytes);
     }
   };
-  // Group V of tile `kb`: bias copy (keys past Lk read as zero), V copy.
-  auto issue_v = [&](int kb) {
+  // Bias copy of list position `it` (keys past Lk read as zero) into slot it % 2, or into
+  // the unread slot 2 past the end of the list.
+  auto issue_bias = [&](int it) {
+    const int kb = entry(it);
     const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
-    if (kBias) {
-      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bhead), (short)0,
-                                                                          a.Lk * 4, 0x00020000);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_u8*)bl_lds, 4, (kb0 + lane) * 4, 0, 0, 0);
-    }
+    const int bslot = it < cnt ? (it & 1) : 2;
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(bhead), (short)0,
+                                                                        a.Lk * 4, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_u8*)(bl_lds + bslot * kBlock), 4, (kb0 + lane) * 4, 0, 0, 0);
+  };
+  // Group V of tile `kb` (list position it): the bias copy of position it + 1 (two tiles
+  // ahead of its use, so it has landed when the tile's K copy is waited for), V copy.
+  auto issue_v = [&](int kb, int it) {
+    const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
+    if (kBias) issue_bias(it + 1);
     if (kD == 64 && c128) {
       dma_tile_c128(vhead, vbytes, kb0 * vrow, vgo, vl);
     } else {
@@ -425,8 +434,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     int it = 0;
     int kb = entry(0);
     if (cnt > 0) {
+      if (kBias) issue_bias(0);
       issue_k(kb, 0);
-      issue_v(kb);
+      issue_v(kb, 0);
     }
     while (it < cnt) {
       // Past the end of the list the copies re-load the current block, so every iteration
@@ -461,13 +471,14 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         }
       
       if (kBias) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
-        // The bias copy of this tile was issued before its V copy: wait for it only.
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * kHalves + kGroupK));
+        // This tile's bias copy was issued before the previous tile's V copy, so the wait for
+        // this tile's K copy at the top covered it.
+        const float* bt = bl_lds + (it & 1) * kBlock;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const float4 b4 = *reinterpret_cast<const float4*>(bl_lds + 32 * c + 8 * q4 + 4 * hh);
+            const float4 b4 = *reinterpret_cast<const float4*>(bt + 32 * c + 8 * q4 + 4 * hh);
             const float bq[4] = {b4.x * kLog2e, b4.y * kLog2e, b4.z * kLog2e, b4.w * kLog2e};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -611,7 +622,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
                                               acc[2 * hp + dc][g]);
             }
       }
-      issue_v(kb_next);
+      issue_v(kb_next, it + 1);
 
       it = it + 1;
       kb = kb_next;
