@@ -248,6 +248,134 @@ __global__ __launch_bounds__(256) void match_kernel(MatchArgs a) {
   }
 }
 
+// Match on the matrix core for C = 64 (the head-averaged k metric). v_mfma_f32_16x16x4_f32
+// adds its four products to the accumulator as an fmaf chain over k = 0..3 in order
+// (checked on the hardware against fmaf chains for normal and subnormal operands), so the
+// 16 chained steps j (channels 4j .. 4j + 3) give every score the same fmaf chain over
+// c = 0..63 as match_kernel, and the maxima are bit-identical. D[m][n] = score(dst m, src n):
+// lane l holds A[m = l % 16][k = l / 16] (a staged dst row), B[k = l / 16][n = l % 16] (its
+// src rows, kept in registers for the whole range) and D rows 4 (l / 16) .. + 3 of column
+// l % 16. Workgroup: 4 waves x 64 src rows (4 blocks of 16), the split's dst range in
+// 64-row tiles staged in LDS (double-buffered, loaded into registers one tile ahead).
+constexpr int kMfC = 64;           // channels
+constexpr int kMfSrcW = 64;        // src rows per wave
+constexpr int kMfSrc = 4 * kMfSrcW;
+constexpr int kMfDst = 64;         // dst rows per staged tile
+constexpr int kMfLd = kMfC + 4;    // floats per staged dst row: A reads hit 64 distinct banks
+
+__global__ __launch_bounds__(256, 2) void match_mfma_kernel(MatchArgs a) {
+  __shared__ __attribute__((aligned(16))) float dl[2][kMfDst * kMfLd];
+  const int g = blockIdx.y, split = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m16 = lane & 15, kg = lane >> 4;
+  const float* mg = a.metric + (int64_t)g * a.N * kMfC;
+  const int sw0 = blockIdx.x * kMfSrc + wave * kMfSrcW;
+  // B operands: src block sb, step j = channel 4j + kg of src row sw0 + 16 sb + m16.
+  float bop[4][kMfC / 4];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb) {
+    const int sr = sw0 + 16 * sb + m16;
+    const float* row = sr < a.n_src ? mg + (int64_t)a.a_idx[sr] * kMfC : nullptr;
+#pragma unroll
+    for (int j = 0; j < kMfC / 4; ++j) bop[sb][j] = row ? row[4 * j + kg] : 0.f;
+  }
+  float best[4];
+  int bidx[4];
+#pragma unroll
+  for (int sb = 0; sb < 4; ++sb) {
+    best[sb] = -INFINITY;
+    bidx[sb] = 0;
+  }
+  const int d_lo = split * a.dst_per_split;
+  const int d_hi = min(a.n_dst, d_lo + a.dst_per_split);
+  // Staging: thread tid holds float4 q = tid + 256 i of a tile, row q / 16, channels
+  // 4 (q % 16) .. + 3 (rows past the range are zero and never compete).
+  float4 pre[4];
+  auto load_tile = [&](int d0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = tid + 256 * i, d = d0 + (q >> 4);
+      pre[i] = d < d_hi ? *reinterpret_cast<const float4*>(mg + (int64_t)a.b_idx[d] * kMfC + 4 * (q & 15))
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = tid + 256 * i;
+      *reinterpret_cast<float4*>(&dl[buf][(q >> 4) * kMfLd + 4 * (q & 15)]) = pre[i];
+    }
+  };
+  int buf = 0;
+  if (d_lo < d_hi) {
+    load_tile(d_lo);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int d0 = d_lo; d0 < d_hi; d0 += kMfDst) {  // workgroup-uniform trip count
+    const bool more = d0 + kMfDst < d_hi;
+    if (more) load_tile(d0 + kMfDst);
+    sa_f32x4 acc[4][4];  // [dst block][src block]
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) acc[db][sb] = sa_f32x4{0.f, 0.f, 0.f, 0.f};
+    const float* t = dl[buf] + m16 * kMfLd + kg;
+#pragma unroll
+    for (int j = 0; j < kMfC / 4; ++j) {
+      float aop[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) aop[db] = t[16 * db * kMfLd + 4 * j];
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb)
+          acc[db][sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aop[db], bop[sb][j], acc[db][sb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = d0 + 16 * db + 4 * kg + i;
+        if (d < d_hi) {
+#pragma unroll
+          for (int sb = 0; sb < 4; ++sb)
+            if (better(acc[db][sb][i], d, best[sb], bidx[sb])) {
+              best[sb] = acc[db][sb][i];
+              bidx[sb] = d;
+            }
+        }
+      }
+    if (more) store_tile(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  // Lanes m16 + 16 kg hold the same src columns over different dst rows.
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      const float ov = __shfl_xor(best[sb], off);
+      const int oi = __shfl_xor(bidx[sb], off);
+      if (better(ov, oi, best[sb], bidx[sb])) {
+        best[sb] = ov;
+        bidx[sb] = oi;
+      }
+    }
+  }
+  if (kg == 0) {
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      const int sr = sw0 + 16 * sb + m16;
+      if (sr < a.n_src) {
+        const int64_t o = ((int64_t)g * a.splits + split) * a.n_src + sr;
+        a.part_max[o] = best[sb];
+        a.part_idx[o] = bidx[sb];
+      }
+    }
+  }
+}
+
 // Dst splits of the match grid: whole 128-column tiles, at most kMMaxSplits splits.
 int match_tiles_per_split(int n_dst) {
   const int n_dt = (n_dst + kMTile - 1) / kMTile;
@@ -636,7 +764,10 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
     a.n_src = m.n_src; a.n_dst = m.n_dst; a.splits = splits;
     a.dst_per_split = match_tiles_per_split(m.n_dst) * kMTile;
     a.part_max = part_max; a.part_idx = part_idx;
-    hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kMTile - 1) / kMTile, m.G, splits), dim3(256), 0, s, a);
+    if (C == kMfC)
+      hipLaunchKernelGGL(match_mfma_kernel, dim3((m.n_src + kMfSrc - 1) / kMfSrc, m.G, splits), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kMTile - 1) / kMTile, m.G, splits), dim3(256), 0, s, a);
     if ((rc = sa::check_launch(fn))) return rc;
   }
   MapArgs ma;
