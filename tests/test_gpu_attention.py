@@ -151,6 +151,25 @@ def test_key_bias(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125, key_bias=bias.double()))
 
 
+def test_key_bias_short_lists(dev):
+    # Lists of 0, 1, 2, 3 and all 11 blocks (random blocks, the last one partial) with a
+    # per-head bias: the bias rows are copied two tiles ahead into alternating slots, and past
+    # the end of a list into a slot nothing reads.
+    case("key bias, lists of 0-3 and 11 blocks")
+    B, H, L, nb = 1, 2, 700, 11
+    q, k, v = (_rand((B, H, L, 64), 150 + i) for i in range(3))
+    g = torch.Generator().manual_seed(17)
+    mask = torch.zeros(B, H, nb, nb, dtype=torch.bool)
+    for h in range(H):
+        for r in range(nb):
+            n = (0, 1, 2, 3, nb)[(r + h) % 5]
+            mask[0, h, r, torch.randperm(nb, generator=g)[:n]] = True
+    bias = 2 * torch.randn(B, H, L, generator=g)
+    kv = kv_list_from_mask(mask.to(dev), B, H, nb, nb)
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bias.to(dev))
+    _check(out, masked_attention(q, k, v, mask, 0.125, key_bias=bias.double()))
+
+
 def test_large_scores_redo_with_running_max(dev):
     # Head 0 has scores of several hundred (exp2 overflows without the max subtraction),
     # head 1 ordinary ones: the kernel must redo exactly the items whose sums left range.
