@@ -32,6 +32,7 @@ from .block_mask_attn import dense_kv_list
 from .estimator import energy_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
 from .utils.mask_related import calc_attn_block_sum_efficient
+from .utils.tools import rng_state_preserved
 
 N_TEXT_BLOCKS = 4  # the reference forces rows and columns 0..3 (:81-82)
 
@@ -57,22 +58,6 @@ def concentrated_interpolation(min_val, max_val, n_points, concentration=0.2):
     x = np.linspace(-6, 6, n_points)
     cdf = 1 / (1 + np.exp(-x / (2 * (1 - c))))
     return np.clip(max_val - cdf * (max_val - min_val), min_val, max_val)
-
-
-class _RngGuard:
-    """Restores the CPU and CUDA generator states on exit (the reference's preserve_rng_state,
-    utils/tools.py:162-181): every sparse call samples with the same draws."""
-
-    def __enter__(self):
-        self.cpu = torch.get_rng_state()
-        self.cuda = [torch.cuda.get_rng_state(d) for d in range(torch.cuda.device_count())]
-        return self
-
-    def __exit__(self, *exc):
-        torch.set_rng_state(self.cpu)
-        for d, s in enumerate(self.cuda):
-            torch.cuda.set_rng_state(s, d)
-        return False
 
 
 class LayerMasks:
@@ -160,7 +145,7 @@ class BlockSparseAttention:
         """Sparse step: sampled block scores -> energy mask -> block-sparse attention."""
         self.sm_scale = 1 / q.size(-1) ** 0.5
         layer, max_r, min_r, thr, cur_k = self._schedule()
-        with _RngGuard():
+        with rng_state_preserved():
             pool = calc_attn_block_sum_efficient(q, k, num_keep=8)
         kv = transfer_attn_to_kv_list(pool, mode="energy", init_k=cur_k, max_retain_ratio=max_r,
                                       min_retain_ratio=min_r, energy_threshold=thr)

@@ -19,6 +19,7 @@ _SUBMODULES = (
     "utils.merge_unmerge",
     "utils.mask_related",
     "utils.attn_pooling_kernel",
+    "utils.tools",
     "block_mask_attn",
     "SparseGen_Plus",
     "combined_attn",

@@ -4,6 +4,7 @@ hot path). No GPU calls."""
 import importlib
 
 import pytest
+import torch
 
 import sparseattnfunctions_amd
 
@@ -17,6 +18,7 @@ NAMES = {
                            "preprocess_qkv", "reverse_process_out", "generate_attention_mask_frame_scope",
                            "calc_attn", "get_inner_frame_mask", "get_block_mask"],
     "utils.attn_pooling_kernel": ["is_hip", "_attention_pooling", "attn_with_pooling"],
+    "utils.tools": ["timeit", "preserve_rng_state"],
     "block_mask_attn": ["BlockSparseAttention"],
     "SparseGen_Plus": ["transfer_attn_to_mask", "concentrated_interpolation", "BlockSparseAttention"],
     "combined_attn": ["CombinedAttn"],
@@ -35,3 +37,37 @@ def test_reference_names_import_through_alias(module):
     missing = [n for n in NAMES[module] if not hasattr(mod, n)]
     assert not missing, missing
     exec(f"from special_attentions.{module} import {', '.join(NAMES[module])}", {})
+
+
+def test_preserve_rng_state_restores_generator_and_timeit_prints(capsys):
+    from sparseattnfunctions_amd.utils.tools import preserve_rng_state, timeit
+
+    @preserve_rng_state
+    def draw():
+        return torch.rand(3)
+
+    torch.manual_seed(11)
+    inside = draw()
+    after = torch.rand(3)
+    torch.manual_seed(11)
+    assert torch.equal(inside, torch.rand(3)) and torch.equal(after, inside)
+
+    @preserve_rng_state
+    def fails():
+        torch.rand(5)
+        raise ValueError("x")
+
+    torch.manual_seed(12)
+    with pytest.raises(ValueError):
+        fails()
+    got = torch.rand(2)
+    torch.manual_seed(12)
+    assert torch.equal(got, torch.rand(2))
+
+    @timeit
+    def twice(x):
+        return 2 * x
+
+    assert twice(21) == 42
+    out = capsys.readouterr().out
+    assert out.startswith("twice execution took ") and out.rstrip().endswith("ms")
