@@ -499,14 +499,18 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
           }
       }
       if (kMask && mslot_cur >= 0) {  // token-level mask of a tile cut by a mask boundary
+        // Element e of S[g][c] is key 32c + 8(e/4) + 4hh + e%4: its bit, sign-extended to
+        // 0 or all ones (v_bfe_i32), selects between the score and -inf (v_bfi_b32).
 #pragma unroll
         for (int g = 0; g < 2; ++g)
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            const uint32_t bits = (uint32_t)(mw_cur[g] >> (32 * c));
+            const int bits = (int)((uint32_t)(mw_cur[g] >> (32 * c)) >> (4 * hh));
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              if (!((bits >> (8 * (e >> 2) + 4 * hh + (e & 3))) & 1u)) S[g][c][e] = -INFINITY;
+            for (int e = 0; e < 16; ++e) {
+              const uint32_t keep = (uint32_t)__builtin_amdgcn_sbfe(bits, 8 * (e >> 2) + (e & 3), 1);
+              S[g][c][e] = __uint_as_float((__float_as_uint(S[g][c][e]) & keep) | (0xFF800000u & ~keep));
+            }
           }
       }
 
