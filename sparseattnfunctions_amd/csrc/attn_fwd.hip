@@ -570,11 +570,13 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
         for (int g = 0; g < 2; ++g) mu[g] = (m[g] == -INFINITY) ? 0.f : m[g];
       }
+      // In the order the S MFMA chains complete (c outer): the first softmax work needs only
+      // the first half of the S MFMAs. Each row sum l[g] still adds its pairs c-major.
       uint32_t P[2][2][8];
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int g = 0; g < 2; ++g)
 #pragma unroll
           for (int e = 0; e < 16; e += 2) {
             const float p0 = fast_exp2(kSafe ? fmaf(S[g][c][e], sc, -mu[g]) : S[g][c][e] * sc);
