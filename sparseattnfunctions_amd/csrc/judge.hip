@@ -27,6 +27,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 typedef unsigned jd_u32x4 __attribute__((ext_vector_type(4)));
 typedef float jd_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short jd_u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline sa_f32x16 score_tile_k(const jd_u32x4 (&kop)[4], const sa_bf16x8 (&qf)[4]) {
   sa_f32x16 t = {};
@@ -240,8 +241,31 @@ __global__ __launch_bounds__(256) void share_kernel(ShareArgs a) {
     const uint32_t tot = part_u[bit & 1][0] + part_u[bit & 1][1] + part_u[bit & 1][2] + part_u[bit & 1][3];
     return tot >= (uint32_t)a.K ? cand : thr;
   };
+  // The first kShareHi steps compare top bits only (their candidates' low 16 bits are zero),
+  // two entries per register: the top halves of non-negative fp32 patterns are below 0x8000
+  // and the candidates' at most 0x8000, so x < c is the sign bit of the 16-bit difference
+  // x - c (packed subtract, shift and add; no compare results in VCC).
+  jd_u16x2 hp[kPer / 2];
+#pragma unroll
+  for (int i = 0; i < kPer / 2; ++i)
+    hp[i] = jd_u16x2{(unsigned short)(v[2 * i] >> 16), (unsigned short)(v[2 * i + 1] >> 16)};
+  auto step_hi = [&](uint32_t thr, int bit) {
+    const uint32_t cand = thr | (1u << bit);
+    const unsigned short c16 = (unsigned short)(cand >> 16);
+    const jd_u16x2 cc = {c16, c16};
+    jd_u16x2 lt = {0, 0};
+#pragma unroll
+    for (int i = 0; i < kPer / 2; ++i) lt += (jd_u16x2)(hp[i] - cc) >> (unsigned short)15;
+    uint32_t c = (uint32_t)kPer - ((uint32_t)lt.x + (uint32_t)lt.y);
+    c = wave_sum_u(c);
+    if (lane == 0) part_u[bit & 1][wave] = c;
+    __syncthreads();
+    const uint32_t tot = part_u[bit & 1][0] + part_u[bit & 1][1] + part_u[bit & 1][2] + part_u[bit & 1][3];
+    return tot >= (uint32_t)a.K ? cand : thr;
+  };
+  static_assert(32 - kShareHi >= 16, "the packed steps need candidates with zero low 16 bits");
   uint32_t thr = 0;
-  for (int bit = 31; bit >= 32 - kShareHi; --bit) thr = step(thr, bit);
+  for (int bit = 31; bit >= 32 - kShareHi; --bit) thr = step_hi(thr, bit);
   // Bucket: entries whose top kShareHi bits equal thr's; above: entries with larger top bits.
   const uint32_t hi = thr >> (32 - kShareHi);
   uint32_t nb = 0, above = 0;
