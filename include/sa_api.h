@@ -76,6 +76,11 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
  *   sm_scale  > 0 and finite.
  *   work_order nullable int32 [n_slots] from sa_attn_work_order (device copy): dispatch
  *             slot -> list row, -1 = idle. NULL visits rows in index order.
+ * A launch with few query blocks and long lists (plain lists without key_bias; see
+ * sa_attn_split_parts) splits each block's list into key ranges, one wave each, and merges
+ * their fp32 partials in a second kernel; work_order is then not read. The partials are
+ * allocated stream-ordered on `stream` (hipMallocAsync, freed with hipFreeAsync after the
+ * merge); if that allocation fails the launch runs unsplit.
  */
 int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                         const int64_t k_strides[3], const uint16_t* v,
@@ -215,6 +220,17 @@ int sa_attn_pooling_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const
  */
 int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int n_xcd, int32_t* order,
                        int64_t* n_slots);
+
+/*
+ * Key-range parts per query block that the attention entry points use on the current device
+ * for a launch of n_items = B*H*ceil(Lq/64) query blocks with lists of width max_cnt and
+ * head dim D (plain lists: no key_bias, no tile masks, no pooling). *parts = 1: no split.
+ * Parts are chosen to fill the device's wave slots (compute units x resident waves) once, with
+ * at least 32 list positions per part at the list width; lists narrower than 64 are never
+ * split, nor launches whose blocks fill half the slots. No counterpart in the reference (its
+ * Triton launch has one program per query block); for tests and for integrators sizing calls.
+ */
+int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int* parts);
 
 /*
  * Block means of q and k: pooled[(b*H + h)*nb + blk][d] = mean over the block's tokens,

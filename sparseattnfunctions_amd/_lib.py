@@ -65,6 +65,7 @@ _PROTOTYPES = {
          _P, _I, _P, _I, _P, ctypes.c_int64, _P],
     ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
+    "sa_attn_split_parts": (_I, [ctypes.c_int64, _I, _I, ctypes.POINTER(_I)]),
     "sa_attn_pooling_workspace": (_I, [_I, _I, _I, _I, _I64P]),
     "sa_attn_pooling_fwd": (
         _I,

@@ -37,6 +37,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <type_traits>
@@ -49,6 +50,9 @@ namespace {
 constexpr int kBlock = 64;       // query rows per block == keys per key block
 constexpr int kHeadDim = 64;     // head dimension handled by this kernel
 constexpr int kWaves = 4;        // independent waves per workgroup
+// Floats per key-range partial: acc [64 rows][kD], row sums [64], row maxima [64].
+template <int kD>
+constexpr int kSplitFloats = kBlock * kD + 2 * kBlock;
 constexpr int kTileBytes = kBlock * kHeadDim * 2;  // one K or V tile: 64 rows x 128 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
@@ -70,6 +74,13 @@ struct FwdArgs {
   int n_items;             // B*H*nqb
   const int32_t* order;    // dispatch slot -> item (bh*nqb + qb), -1 = idle; may be null
   int n_slots;
+  // Key-range split (n_parts > 1; plain lists only): slot (bh * n_parts + p) * nqb + qb
+  // computes list positions [cnt * p / n_parts, cnt * (p + 1) / n_parts) of item bh * nqb + qb
+  // and stores its unnormalised partial to ws[item * n_parts + p] (kSplitFloats each: acc
+  // [64 rows][kD], then the row sums and the row maxima, log2 domain); split_merge_kernel
+  // forms the output. `order` is not read.
+  int n_parts;
+  float* ws;
   const int32_t* kv_idx;
   const int32_t* kv_cnt;
   int max_cnt;
@@ -285,7 +296,19 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const int hh = lane >> 5;   // lane half (MFMA k group)
   const int slot = blockIdx.x * kWaves + wave;
   if (slot >= a.n_slots) return;
-  const int item = __builtin_amdgcn_readfirstlane(a.order ? a.order[slot] : slot);
+  // Key-range parts exist for plain lists only; the other variants compile without them.
+  constexpr bool kSplit = !kBias && !kMask && kPool == 0;
+  const bool split = kSplit && a.n_parts > 1;
+  int item, part = 0;
+  if (split) {
+    const int per_bh = a.n_parts * a.nqb;
+    const int bh_s = slot / per_bh;
+    const int rem = slot - bh_s * per_bh;
+    part = rem / a.nqb;
+    item = bh_s * a.nqb + (rem - part * a.nqb);
+  } else {
+    item = __builtin_amdgcn_readfirstlane(a.order ? a.order[slot] : slot);
+  }
   if (item < 0 || item >= a.n_items) return;  // idle slot (no workgroup barriers below)
   const int bh = item / a.nqb;
   const int qb = item - bh * a.nqb;
@@ -295,6 +318,12 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const int64_t list_row = (int64_t)bh * a.list_bh_stride + qb;
   int cnt = a.kv_cnt[list_row];
   cnt = cnt < 0 ? 0 : (cnt > a.max_cnt ? a.max_cnt : cnt);
+  int beg = 0;  // list positions [beg, cnt) of this wave
+  if (split) {
+    beg = cnt * part / a.n_parts;
+    cnt = cnt * (part + 1) / a.n_parts;
+  }
+  __builtin_assume(beg >= 0);
   // Constant address space: the compiler may use scalar loads (nothing here writes them).
   const __attribute__((address_space(4))) int32_t* list =
       (const __attribute__((address_space(4))) int32_t*)(a.kv_idx + list_row * a.max_cnt);
@@ -431,12 +460,12 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       for (int g = 0; g < 2; ++g) acc[dc][g] = sa_f32x16{};
     m[0] = m[1] = -INFINITY;
     l[0] = l[1] = 0.f;
-    int it = 0;
-    int kb = entry(0);
-    if (cnt > 0) {
-      if (kBias) issue_bias(0);
-      issue_k(kb, 0);
-      issue_v(kb, 0);
+    int it = beg;
+    int kb = entry(beg);
+    if (cnt > beg) {
+      if (kBias) issue_bias(beg);
+      issue_k(kb, beg);
+      issue_v(kb, beg);
     }
     while (it < cnt) {
       // Past the end of the list the copies re-load the current block, so every iteration
@@ -644,7 +673,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   else run(std::true_type{});
   // The fast pass is exact unless a row's sum left [2^-90, 2^90] (scores far from 0, where
   // exp2 would lose range) or an accumulator overflowed; then redo the item safely.
-  if (kFast && cnt > 0) {
+  if (kFast && cnt > beg) {
     bool bad = false;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -665,6 +694,23 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const float l_tot = xhalf_sum(l[g]);
+    if (split) {  // partial of a key-range part: acc, row sum, row max (0 in the fast pass)
+      float* w = a.ws + ((int64_t)item * a.n_parts + part) * kSplitFloats<kD>;
+      const int r = 32 * g + col;
+#pragma unroll
+      for (int dc = 0; dc < kDC; ++dc)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const sa_f32x16& A = acc[dc][g];
+          *reinterpret_cast<float4*>(w + r * kD + 32 * dc + 8 * q4 + 4 * hh) =
+              make_float4(A[4 * q4], A[4 * q4 + 1], A[4 * q4 + 2], A[4 * q4 + 3]);
+        }
+      if (hh == 0) {
+        w[kBlock * kD + r] = l_tot;
+        w[kBlock * kD + kBlock + r] = m[g] == -INFINITY ? 0.f : m[g];
+      }
+      continue;
+    }
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     if constexpr (kPool != 0) {
       // log2-sum-exp2 of the row: P = exp2(S * sc - m) / l_tot (m = -inf: the fast pass, 0).
@@ -797,6 +843,89 @@ struct PoolOut {
   int causal;
 };
 
+// Output of key-range split items: one workgroup per item, thread t forms row t / 4, head
+// dims (t % 4) * kD / 4 + 0 .. kD / 4 - 1, from the item's n_parts partials (in part order):
+// out = sum_p acc_p * 2^(m_p - M) / sum_p l_p * 2^(m_p - M), M = max_p m_p.
+template <typename T, int kD>
+__global__ __launch_bounds__(256) void split_merge_kernel(FwdArgs a) {
+  typedef Elem<T> E;
+  constexpr int kSeg = kD / 4;
+  const int item = blockIdx.x;
+  if (item >= a.n_items) return;
+  const int bh = item / a.nqb;
+  const int qb = item - bh * a.nqb;
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int r = threadIdx.x >> 2;
+  const int d0 = (threadIdx.x & 3) * kSeg;
+  const float* w0 = a.ws + (int64_t)item * a.n_parts * kSplitFloats<kD>;
+  float mx = -INFINITY;
+  for (int p = 0; p < a.n_parts; ++p) mx = fmaxf(mx, w0[(int64_t)p * kSplitFloats<kD> + kBlock * kD + kBlock + r]);
+  float lsum = 0.f;
+  float o[kSeg];
+#pragma unroll
+  for (int j = 0; j < kSeg; ++j) o[j] = 0.f;
+  for (int p = 0; p < a.n_parts; ++p) {
+    const float* w = w0 + (int64_t)p * kSplitFloats<kD>;
+    const float f = exp2f(w[kBlock * kD + kBlock + r] - mx);
+    lsum = fmaf(w[kBlock * kD + r], f, lsum);
+#pragma unroll
+    for (int j = 0; j < kSeg; j += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(w + r * kD + d0 + j);
+      o[j] = fmaf(x.x, f, o[j]);
+      o[j + 1] = fmaf(x.y, f, o[j + 1]);
+      o[j + 2] = fmaf(x.z, f, o[j + 2]);
+      o[j + 3] = fmaf(x.w, f, o[j + 3]);
+    }
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  int row = qb * kBlock + r;
+  if (row >= a.Lq) return;
+  if (a.o_rows) {
+    row = a.o_rows[row];
+    if ((unsigned)row >= (unsigned)a.o_dst_rows) return;
+  }
+  uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_sl + d0;
+#pragma unroll
+  for (int j = 0; j < kSeg; j += 8)
+    *reinterpret_cast<uint4*>(orow + j) =
+        make_uint4(E::pack(o[j] * inv, o[j + 1] * inv), E::pack(o[j + 2] * inv, o[j + 3] * inv),
+                   E::pack(o[j + 4] * inv, o[j + 5] * inv), E::pack(o[j + 6] * inv, o[j + 7] * inv));
+}
+
+// Key-range split of a launch with few items: parts per item so that the parts fill the
+// device's wave slots once (CUs x resident waves per CU), with at least kSplitPartTiles list
+// positions per part at the list width; 1 = no split (also below kSplitMinTiles, or when the
+// items already fill half the slots).
+constexpr int kSplitMinTiles = 64;
+constexpr int kSplitPartTiles = 32;
+constexpr int kSplitMaxParts = 16;
+
+int split_parts(int64_t n_items, int max_cnt, int D) {
+  if (max_cnt < kSplitMinTiles) return 1;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  // Stream-ordered allocations of the partials: keep freed blocks in the device's default
+  // pool instead of returning them at every synchronisation (set once per device).
+  static std::atomic<uint64_t> pool_set{0};
+  if (dev < 64 && !(pool_set.load() & (1ull << dev))) {
+    hipMemPool_t pool;
+    uint64_t keep = UINT64_MAX;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess ||
+        hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess)
+      (void)hipGetLastError();
+    pool_set.fetch_or(1ull << dev);
+  }
+  const int64_t slots = (int64_t)cus * (D == 64 ? 2 : 1) * kWaves;
+  if (n_items * 2 > slots) return 1;
+  const int64_t p = std::min<int64_t>({slots / n_items, max_cnt / kSplitPartTiles, kSplitMaxParts});
+  return p > 1 ? (int)p : 1;
+}
+
 // One kernel variant per (tile masks, key bias, pooling columns): the caller has rejected
 // the combinations of tile masks or pooling with a key bias.
 template <typename T, int kD>
@@ -870,6 +999,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.n_items = (int)n_items;
   a.order = work_order;
   a.n_slots = (int)n_slots;
+  a.n_parts = 1;
+  a.ws = nullptr;
   a.kv_idx = kv_idx; a.kv_cnt = kv_cnt; a.max_cnt = max_cnt;
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
@@ -902,8 +1033,28 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   if (kv_slot && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
   if (pool_cols && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
   hipStream_t s = sa::as_stream(stream);
-  const dim3 g((unsigned)grid), blk(64 * kWaves);
   const bool mask = kv_slot != nullptr, bias = key_bias != nullptr;
+  // Few items with long plain lists leave most wave slots idle: each item's list is split
+  // into key ranges, one wave each, and split_merge_kernel forms the outputs from the
+  // partials. The partials live in stream-ordered memory (hipMallocAsync / hipFreeAsync on
+  // the call's stream); without it the launch runs unsplit.
+  int64_t grid_x = grid;
+  if (!mask && !bias && pool_cols == 0) {
+    const int parts = split_parts(n_items, max_cnt, D);
+    if (parts > 1) {
+      const size_t bytes = (size_t)n_items * parts * (D == 64 ? kSplitFloats<64> : kSplitFloats<128>) * sizeof(float);
+      void* ws = nullptr;
+      if (hipMallocAsync(&ws, bytes, s) == hipSuccess && ws) {
+        a.n_parts = parts;
+        a.ws = static_cast<float*>(ws);
+        a.n_slots = (int)((n_items * parts + kWaves - 1) / kWaves * kWaves);
+        grid_x = a.n_slots / kWaves;
+      } else {
+        (void)hipGetLastError();
+      }
+    }
+  }
+  const dim3 g((unsigned)grid_x), blk(64 * kWaves);
   if (fp16) {
     if (D == 64) launch_variant<_Float16, 64>(a, g, blk, s, mask, bias, pool_cols);
     else launch_variant<_Float16, 128>(a, g, blk, s, mask, bias, pool_cols);
@@ -911,10 +1062,31 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
     if (D == 64) launch_variant<__bf16, 64>(a, g, blk, s, mask, bias, pool_cols);
     else launch_variant<__bf16, 128>(a, g, blk, s, mask, bias, pool_cols);
   }
+  if (a.n_parts > 1) {
+    const dim3 gm((unsigned)n_items), bm(256);
+    if (fp16) {
+      if (D == 64) hipLaunchKernelGGL((split_merge_kernel<_Float16, 64>), gm, bm, 0, s, a);
+      else hipLaunchKernelGGL((split_merge_kernel<_Float16, 128>), gm, bm, 0, s, a);
+    } else {
+      if (D == 64) hipLaunchKernelGGL((split_merge_kernel<__bf16, 64>), gm, bm, 0, s, a);
+      else hipLaunchKernelGGL((split_merge_kernel<__bf16, 128>), gm, bm, 0, s, a);
+    }
+    const int rc = sa::check_launch(fn);
+    (void)hipFreeAsync(a.ws, s);
+    return rc;
+  }
   return sa::check_launch(fn);
 }
 
 }  // namespace
+
+extern "C" int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int* parts) {
+  SA_REQUIRE(parts, "sa_attn_split_parts: null parts");
+  SA_REQUIRE(n_items > 0 && max_cnt > 0 && (D == 64 || D == 128),
+             "sa_attn_split_parts: bad arguments n_items=%lld max_cnt=%d D=%d", (long long)n_items, max_cnt, D);
+  *parts = split_parts(n_items, max_cnt, D);
+  return sa::ok();
+}
 
 extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                                    const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],

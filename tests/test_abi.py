@@ -91,3 +91,14 @@ def test_work_order_is_a_permutation(lib):
             text = (mine % nqb) < nt
             if text.any() and (~text).any():
                 assert text.nonzero().max() < (~text).nonzero().min()
+
+
+def test_split_parts_query(lib):
+    parts = ctypes.c_int(-1)
+    assert lib.sa_attn_split_parts(0, 128, 64, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_parts(4, 128, 96, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_parts(4, 128, 64, None) == _lib.SA_ERR_INVALID
+    # lists narrower than 64 positions are never split (no device query needed)
+    assert lib.sa_attn_split_parts(4, 63, 64, ctypes.byref(parts)) == _lib.SA_OK and parts.value == 1
+    # wide lists: 1 without a GPU (no device to size against), else >= 1
+    assert lib.sa_attn_split_parts(4, 128, 64, ctypes.byref(parts)) == _lib.SA_OK and parts.value >= 1

@@ -12,6 +12,7 @@ import torch
 from conftest import case
 from oracle.attention import masked_attention
 from sparseattnfunctions_amd._kv import KVList, kv_list_from_mask
+from sparseattnfunctions_amd.block_mask_attn import dense_kv_list
 from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import (
     block_sparse_attention, block_sparse_triton_fn, sparse_attention_factory)
 from sparseattnfunctions_amd.workloads import config1_inputs
@@ -414,3 +415,109 @@ def test_fp32_strided_and_large_scores(dev):
     # logits up to ~300: fp32 rounding of a logit alone is 2^-24 * 300 ~ 2e-5, so the bar
     # scales with them (max-abs 1e-4)
     _check_f32(out, masked_attention(*(t.permute(0, 2, 1, 3) for t in base), mask, 0.125), 1e-4, 1e-5)
+
+
+def _split_parts(n_items, max_cnt, D=64):
+    import ctypes
+    from sparseattnfunctions_amd import _lib
+    parts = ctypes.c_int(0)
+    _lib.check(_lib.load().sa_attn_split_parts(n_items, max_cnt, D, ctypes.byref(parts)), "sa_attn_split_parts")
+    return parts.value
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,D,dtype,amp", [
+    (1, 2, 200, 8192, 64, torch.bfloat16, 1.0),   # partial last query block
+    (2, 3, 64, 4500, 64, torch.bfloat16, 1.0),    # partial last key block
+    (1, 2, 64, 4096, 128, torch.bfloat16, 1.0),   # head dim 128
+    (1, 2, 100, 4096, 64, torch.float16, 1.0),    # fp16 (running maximum in every part)
+    (1, 2, 128, 6000, 64, torch.bfloat16, 8.0),   # scores of several hundred: parts redo safely
+])
+def test_key_range_split_dense(dev, B, H, Lq, Lk, D, dtype, amp):
+    # Few query blocks over long lists: each block's list is split into key ranges whose fp32
+    # partials a second kernel merges (the reference's Triton grid has one program per block).
+    case(f"key-range split B={B} H={H} Lq={Lq} Lk={Lk} D={D} {dtype} amp={amp}")
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    assert _split_parts(B * H * nqb, nkb, D) > 1
+    q = (_rand((B, H, Lq, D), 500, torch.float32) * amp).to(dtype)
+    k = (_rand((B, H, Lk, D), 501, torch.float32) * amp).to(dtype)
+    v = _rand((B, H, Lk, D), 502, dtype)
+    mask = torch.ones(B, H, nqb, nkb, dtype=torch.bool)
+    scale = 1 / math.sqrt(D)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+    # scores of several hundred: fp32 rounding of the logits alone is ~2e-5 of them, and the
+    # softmax is near one-hot, so the bar stays the attention bar
+    _check(out, masked_attention(q, k, v, mask, scale))
+
+
+def test_key_range_split_sparse_lists(dev):
+    # Lists shorter than the parts (empty key ranges), an empty list (writes 0), entries
+    # outside the grid, and a one-block list.
+    case("key-range split, sparse lists")
+    B, H, Lq, Lk = 1, 3, 192, 6000
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    assert _split_parts(B * H * nqb, nkb) > 1
+    q, k, v = (_rand((B, H, n, 64), 510 + i) for i, n in enumerate((Lq, Lk, Lk)))
+    g = torch.Generator().manual_seed(51)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.08
+    mask[0, 0, 1] = False
+    mask[0, 1, 2] = False
+    mask[0, 1, 2, 17] = True
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    kv.idx[2, kv.cnt[2].item()] = nkb + 5  # past the count: never read
+    assert kv.cnt[4].item() > 0
+    first = kv.idx[4, 0].item()
+    kv.idx[4, 0] = -3  # an entry outside the grid is skipped
+    mask[0, 1, 1, first] = False
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125).cpu()
+    assert torch.all(out[0, 0, 64:128] == 0)
+    _check(out, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_key_range_split_matches_unsplit(dev):
+    # The same query blocks in a launch with enough blocks to run unsplit: the outputs agree
+    # up to the fp32 summation order of the partials (one bf16 rounding step).
+    case("key-range split vs unsplit")
+    Lk = 8192
+    q, k, v = _rand((1, 2, 128, 64), 520), _rand((1, 2, Lk, 64), 521), _rand((1, 2, Lk, 64), 522)
+    reps = 300
+    assert _split_parts(1 * 2 * 2, Lk // 64) > 1 and _split_parts(1 * 2 * 2 * reps, Lk // 64) == 1
+    kd, vd = k.to(dev), v.to(dev)
+    small = block_sparse_attention(q.to(dev), kd, vd, dense_kv_list(1, 2, 2, Lk // 64, dev), 0.125)
+    big = block_sparse_attention(q.repeat(1, 1, reps, 1).to(dev), kd, vd, dense_kv_list(1, 2, 2 * reps, Lk // 64, dev),
+                                 0.125)
+    torch.cuda.synchronize()
+    d = (small.float() - big[:, :, :128].float()).abs()
+    assert d.max().item() <= 2 ** -8, d.max().item()
+    assert (d > 0).float().mean().item() < 0.05
+    _check(small, masked_attention(q, k, v, torch.ones(1, 2, 2, Lk // 64, dtype=torch.bool), 0.125))
+
+
+def test_key_range_split_row_maps(dev):
+    # Row-mapped queries and outputs with a split launch: the merge kernel writes through o_rows.
+    case("key-range split with row maps")
+    B, H, Lsrc, Lk = 1, 2, 200, 4096
+    g = torch.Generator().manual_seed(53)
+    q, k, v = _rand((B, H, Lsrc, 64), 530), _rand((B, H, Lk, 64), 531), _rand((B, H, Lk, 64), 532)
+    perm = torch.randperm(Lsrc, generator=g)
+    q_rows = torch.cat([perm[:120], torch.full((8,), -1), perm[120:]]).int()
+    o_rows = q_rows.clone()
+    o_rows[3] = -1
+    Lq = q_rows.numel()
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    assert _split_parts(B * H * nqb, nkb) > 1
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.7
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    out = torch.full((B, H, Lsrc, 64), 3.0, dtype=torch.bfloat16, device=dev)
+    block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, out=out, q_rows=q_rows.to(dev),
+                           o_rows=o_rows.to(dev))
+    out = out.cpu()
+    valid = q_rows >= 0
+    ql = torch.zeros(B, H, Lq, 64, dtype=torch.bfloat16)
+    ql[:, :, valid] = q[:, :, q_rows[valid].long()]
+    want = masked_attention(ql, k, v, mask, 0.125)
+    stored = valid.clone()
+    stored[3] = False
+    _check(out[:, :, o_rows[stored].long()], want[:, :, stored])
+    untouched = torch.ones(Lsrc, dtype=torch.bool)
+    untouched[o_rows[stored].long()] = False
+    assert torch.all(out[:, :, untouched] == 3.0)
