@@ -104,6 +104,21 @@ int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const
                             const int32_t* work_order, int64_t n_slots, void* stream);
 
 /*
+ * sa_block_sparse_fwd (bf16, head dim 64) where only the first 32 columns of v enter P.V and
+ * out has 32 columns: v [B,H,Lk,64] as there (its tiles are read whole), out [B,H,Lq,32].
+ * For a v whose other columns are zero or unused: the segment-indicator v of the
+ * frame-pattern masses (ParternAttentionColVersion_V2.get_weight_for_patch and the
+ * first-frame softmax, partern_attention.py:321-358, 400-420) has 1 + frames <= 32 nonzero
+ * columns. Same lists, key_bias, work order and error contract; never split into key ranges.
+ */
+int sa_block_sparse_fwd_v32(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                            const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                            uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                            const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                            const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                            const int32_t* work_order, int64_t n_slots, void* stream);
+
+/*
  * sa_block_sparse_fwd for fp32 q, k, v and out (the reference kernel also runs on fp32 tiles,
  * :52-209, with P cast to v's dtype, :107, so kept in fp32): same arguments and list contract,
  * head dim 64, key_bias must be NULL (SA_ERR_UNSUPPORTED otherwise). fp32 MFMA

@@ -44,6 +44,11 @@ _PROTOTYPES = {
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,
          ctypes.c_int64, _P],
     ),
+    "sa_block_sparse_fwd_v32": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,
+         ctypes.c_int64, _P],
+    ),
     "sa_block_sparse_fwd_f32": (
         _I,
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,

@@ -268,14 +268,18 @@ constexpr int kWaitLgkm0 = 0xC07F;
 // two 128-byte half rows in two half tiles with the 64-dim layout, so every read pattern of
 // the 64-dim kernel applies per half; at 128 dims a wave holds ~420 registers, so one
 // workgroup (one wave per SIMD) runs per CU.
-template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64>
+// kDV: value columns that enter P.V and the output, kD or 32 (head dim 64: v tiles are
+// copied as usual and only their first 32 columns are read; out has 32 columns).
+template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64, int kDV = kD>
 __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs a) {
   static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
   static_assert(kD == 64 || kD == 128, "head dim 64 or 128");
+  static_assert(kDV == kD || (kDV == 32 && kD == 64 && kPool == 0 && !kMask), "32 value columns: head dim 64");
   typedef Elem<T> E;
   constexpr int kDS = kD / 16;     // 16-wide d steps of S = K Q^T
-  constexpr int kDC = kD / 32;     // 32-row d chunks of O^T
+  constexpr int kDC = kDV / 32;    // 32-row d chunks of O^T
   constexpr int kHalves = kD / 64;  // 128-byte half rows per token
+  constexpr int kVC = kDC / kHalves;  // d chunks of O^T per 128-byte half row of v
   // Separate LDS objects for K, V and bias so that the compiler's own wait analysis can
   // tell a copy into one from a read of another.
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kWaves * kTileBytes * kHalves];
@@ -297,7 +301,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const int slot = blockIdx.x * kWaves + wave;
   if (slot >= a.n_slots) return;
   // Key-range parts exist for plain lists only; the other variants compile without them.
-  constexpr bool kSplit = !kBias && !kMask && kPool == 0;
+  constexpr bool kSplit = !kBias && !kMask && kPool == 0 && kDV == kD;
   const bool split = kSplit && a.n_parts > 1;
   int item, part = 0;
   if (split) {
@@ -630,7 +634,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
           for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int dc = 0; dc < 2; ++dc)
+            for (int dc = 0; dc < kVC; ++dc)
 #pragma unroll
               for (int t = 0; t < 2; ++t) {
                 const uint32_t base = (uint32_t)(uintptr_t)(vl + hp * kTileBytes + vro[dc][t]);
@@ -644,17 +648,17 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
           for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int dc = 0; dc < 2; ++dc) {
-              constexpr int kReads = 16;
-              const int done = 2 * ((c * 2 + u) * 2 + dc) + 2;  // reads this MFMA pair needs
+            for (int dc = 0; dc < kVC; ++dc) {
+              constexpr int kReads = 8 * kVC;
+              const int done = 2 * ((c * 2 + u) * kVC + dc) + 2;  // reads this MFMA pair needs
               lgkm_wait_pair(kReads - done, vr[c][u][dc][0], vr[c][u][dc][1]);
               const sa_u32x4v vop = {vr[c][u][dc][0].x, vr[c][u][dc][0].y, vr[c][u][dc][1].x, vr[c][u][dc][1].y};
 #pragma unroll
               for (int g = 0; g < 2; ++g)
-                acc[2 * hp + dc][g] = E::mfma(E::as8(vop),
+                acc[kVC * hp + dc][g] = E::mfma(E::as8(vop),
                                               E::as8(sa_u32x4v{P[g][c][4 * u], P[g][c][4 * u + 1], P[g][c][4 * u + 2],
                                                                P[g][c][4 * u + 3]}),
-                                              acc[2 * hp + dc][g]);
+                                              acc[kVC * hp + dc][g]);
             }
       }
       issue_v(kb_next, it + 1);
@@ -929,7 +933,15 @@ int split_parts(int64_t n_items, int max_cnt, int D) {
 // One kernel variant per (tile masks, key bias, pooling columns): the caller has rejected
 // the combinations of tile masks or pooling with a key bias.
 template <typename T, int kD>
-void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask, bool bias, int pool_cols) {
+void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask, bool bias, int pool_cols,
+                    bool v32 = false) {
+  if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
+    if (v32) {  // 32 value columns (the caller has rejected tile masks and pooling)
+      if (bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, T, kD, 32>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, 32>), g, blk, 0, s, a);
+      return;
+    }
+  }
   if (mask) {
     if (pool_cols == 32) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 32, T, kD>), g, blk, 0, s, a);
     else if (pool_cols == 64) hipLaunchKernelGGL((bsa_fwd_kernel<false, true, 64, T, kD>), g, blk, 0, s, a);
@@ -950,7 +962,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                const int64_t bias_strides[2], float sm_scale, const int32_t* work_order, int64_t n_slots,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
                const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
-               float* pool_lse = nullptr, const PoolOut* pool_out = nullptr, bool fp16 = false) {
+               float* pool_lse = nullptr, const PoolOut* pool_out = nullptr, bool fp16 = false,
+               bool v32 = false) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -1031,6 +1044,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
              "%s: fused pooled map needs pooling columns of the map's block size", fn);
 
   if (kv_slot && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: tile masks with key_bias", fn);
+  if (v32 && (D != 64 || fp16 || kv_slot || pool_cols))
+    return sa::fail(SA_ERR_UNSUPPORTED, "%s: 32 value columns need bf16, head dim 64, no tile masks or pooling", fn);
   if (pool_cols && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
   hipStream_t s = sa::as_stream(stream);
   const bool mask = kv_slot != nullptr, bias = key_bias != nullptr;
@@ -1039,7 +1054,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   // partials. The partials live in stream-ordered memory (hipMallocAsync / hipFreeAsync on
   // the call's stream); without it the launch runs unsplit.
   int64_t grid_x = grid;
-  if (!mask && !bias && pool_cols == 0) {
+  if (!mask && !bias && pool_cols == 0 && !v32) {
     const int parts = split_parts(n_items, max_cnt, D);
     if (parts > 1) {
       const size_t bytes = (size_t)n_items * parts * (D == 64 ? kSplitFloats<64> : kSplitFloats<128>) * sizeof(float);
@@ -1059,7 +1074,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
     if (D == 64) launch_variant<_Float16, 64>(a, g, blk, s, mask, bias, pool_cols);
     else launch_variant<_Float16, 128>(a, g, blk, s, mask, bias, pool_cols);
   } else {
-    if (D == 64) launch_variant<__bf16, 64>(a, g, blk, s, mask, bias, pool_cols);
+    if (D == 64) launch_variant<__bf16, 64>(a, g, blk, s, mask, bias, pool_cols, v32);
     else launch_variant<__bf16, 128>(a, g, blk, s, mask, bias, pool_cols);
   }
   if (a.n_parts > 1) {
@@ -1108,6 +1123,17 @@ extern "C" int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_stride
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
                     0, nullptr, 0, stream, "sa_block_sparse_fwd_f16", 1, 0, nullptr, nullptr, nullptr, true);
+}
+
+extern "C" int sa_block_sparse_fwd_v32(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                       const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                       uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                       const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                       const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                       const int32_t* work_order, int64_t n_slots, void* stream) {
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, 64, kv_idx, kv_cnt,
+                    max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
+                    0, nullptr, 0, stream, "sa_block_sparse_fwd_v32", 1, 0, nullptr, nullptr, nullptr, false, true);
 }
 
 extern "C" int sa_block_sparse_fwd_tilemask(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,

@@ -82,6 +82,12 @@ def _indicator(seg_of_key: torch.Tensor, device):
     return ind.to(device)
 
 
+def _mass_cols(g: PatternGeometry):
+    """Output columns of the segment-mass attention: 32 (only v's first 32 columns enter P.V)
+    when the 1 + frames segments fit, else all 64."""
+    return 32 if 1 + g.frames <= 32 else None
+
+
 def _frame_indicator(g: PatternGeometry, device):
     def make():
         j = torch.arange(g.L)
@@ -131,7 +137,8 @@ class ParternAttentionColVersion_V2:
     def sampled_masses(self, q, k, index_k, sm_scale: float = scale_factor):
         """Segment masses of the sampled attention (get_weight_for_patch, :321-358): for every
         sampled video row, the softmax mass (with log(ns/S) added to text keys) on the text
-        keys (column 0) and on each frame's samples (column 1 + f). bf16 [B, H, F*ns, 64]."""
+        keys (column 0) and on each frame's samples (column 1 + f). bf16 [B, H, F*ns, 32] (64 columns
+        for more than 31 frames)."""
         g = self.geometry
         B, H = q.shape[:2]
         idx = index_k.to(device=q.device, dtype=torch.int32)
@@ -141,7 +148,7 @@ class ParternAttentionColVersion_V2:
             torch.arange(nk, device=q.device) < g.text_length, composition_bias(g), 0.0).float())
         return block_sparse_attention(qs[:, :, g.text_length:], ks, _bcast(_sample_indicator(g, q.device), B, H),
                                       _dense(B, H, g.frames * g.sample_num, nk, q.device), sm_scale,
-                                      key_bias=_bcast(bias, B, H))
+                                      key_bias=_bcast(bias, B, H), v_cols=_mass_cols(g))
 
     def forward(self, q, k, v, index_k=None):
         q, k, v = self._check(q, k, v)
@@ -156,7 +163,7 @@ class ParternAttentionColVersion_V2:
         block_sparse_attention(q[:, :, :T], k, v, _dense(B, H, T, L, dev), scale_factor, out=out[:, :, :T])
         # First-frame rows over every key: per-segment masses (text, frame i).
         ff_mass = block_sparse_attention(q[:, :, T:T + S], k, _bcast(_frame_indicator(g, dev), B, H),
-                                         _dense(B, H, S, L, dev), scale_factor)
+                                         _dense(B, H, S, L, dev), scale_factor, v_cols=_mass_cols(g))
         map_mass = self.sampled_masses(q, k, index_k)
         # Video rows over the text keys (img2text_detailed_attention @ v_text).
         o_text = block_sparse_attention(q[:, :, T:], k[:, :, :T], v[:, :, :T], _dense(B, H, F * S, T, dev),

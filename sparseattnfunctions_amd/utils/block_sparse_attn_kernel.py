@@ -73,7 +73,7 @@ def _row_map(rows, device):
 
 
 def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None,
-                           n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None):
+                           n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None, v_cols: int = None):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128, or fp32
@@ -87,6 +87,9 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     `o_rows` (int32 [n]) logical row i is written to out row o_rows[i] (dropped outside
     out). `tile_masks` = (kv_slot [rows, max_cnt] int32, masks uint64 [slots, 64],
     lists_shared) adds token-level masks inside cut blocks.
+
+    `v_cols=32` (bf16, head dim 64, no row maps or tile masks): only v's first 32 columns
+    enter P.V and the output is [B,H,Lq,32] (`sa_block_sparse_fwd_v32`; segment-indicator v).
     """
     _lib.require_gpu(q, k, v)
     types = (torch.bfloat16, torch.float16, torch.float32)
@@ -107,14 +110,19 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     Lk = k.shape[2]
     if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
         raise ValueError(f"shape mismatch q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)}")
+    if v_cols not in (None, D):
+        if v_cols != 32 or D != 64 or q.dtype != torch.bfloat16 or q_rows is not None or o_rows is not None \
+                or tile_masks is not None:
+            raise NotImplementedError("v_cols=32: bf16, head dim 64, plain or key-bias lists only")
+    Dout = D if v_cols is None else v_cols
     lists_shared = tile_masks is not None and tile_masks[2]
     want_rows = (1 if lists_shared else B * H) * math.ceil(Lq / BLOCK)
     if kv.rows != want_rows:
         raise ValueError(f"kv list has {kv.rows} rows, expected {want_rows}")
     if out is None:
-        out = torch.empty_like(q) if o_rows is not None else torch.empty(B, H, Lq, D, dtype=q.dtype,
+        out = torch.empty_like(q) if o_rows is not None else torch.empty(B, H, Lq, Dout, dtype=q.dtype,
                                                                           device=q.device)
-    elif out.shape[:2] != (B, H) or out.shape[3] != D or (o_rows is None and out.shape[2] != Lq):
+    elif out.shape[:2] != (B, H) or out.shape[3] != Dout or (o_rows is None and out.shape[2] != Lq):
         raise ValueError(f"out has shape {tuple(out.shape)}")
     bias_ptr, bias_strides = None, None
     if key_bias is not None:
@@ -136,6 +144,15 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                 _lib.ptr(q_rows), Lsrc, _lib.ptr(o_rows), out.shape[2], order.data_ptr(), order.numel(),
                 _lib.stream_of(q))
         _lib.check(rc, fn)
+        return out
+    if Dout == 32 and D == 64:
+        with torch.cuda.device(q.device):
+            rc = lib.sa_block_sparse_fwd_v32(
+                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
+                B, H, Lq, Lk, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, bias_ptr, bias_strides,
+                float(sm_scale), order.data_ptr(), order.numel(), _lib.stream_of(q))
+        _lib.check(rc, "sa_block_sparse_fwd_v32")
         return out
     fn = "sa_block_sparse_fwd_f16" if fp16 else ("sa_block_sparse_fwd_f32" if fp32 else "sa_block_sparse_fwd")
     with torch.cuda.device(q.device):

@@ -220,7 +220,7 @@ def inner_frame_cell_sums(q, k, original_length=FRAME_LENGTH, stride=64):
     ind[torch.arange(k_len), torch.arange(k_len) // stride] = 1
     ind = ind.to(q.device).expand(B, H, k_len, 64)
     mass = block_sparse_attention(q[:, :, :q_len], k[:, :, :k_len], ind, dense_kv_list(B, H, Qr, Kr, q.device),
-                                  1 / 8)
+                                  1 / 8, v_cols=32 if Kr <= 32 and q.dtype == torch.bfloat16 else None)
     out = torch.empty(B, H, Qr, Kr, dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
         rc = _lib.load().sa_row_group_sums(mass.data_ptr(), _lib.i64(*mass.stride()[:3]), B, H, q_len, stride, 0, Kr,

@@ -521,3 +521,34 @@ def test_key_range_split_row_maps(dev):
     untouched = torch.ones(Lsrc, dtype=torch.bool)
     untouched[o_rows[stored].long()] = False
     assert torch.all(out[:, :, untouched] == 3.0)
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_v32_matches_first_columns(dev, with_bias):
+    # 32 value columns (segment-indicator v): the output equals the first 32 columns of the
+    # full launch bit for bit (same scores, softmax and P.V chains), and the oracle within the
+    # attention bar; partial last tiles, an empty list, strided 32-column output.
+    case(f"v32 bias={with_bias}")
+    B, H, Lq, Lk = 2, 3, 300, 1000
+    q, k, v = _rand((B, H, Lq, 64), 540), _rand((B, H, Lk, 64), 541), _rand((B, H, Lk, 64), 542)
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    g = torch.Generator().manual_seed(54)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.5
+    mask[..., 0] = True
+    mask[1, 0, 2] = False  # an empty list writes 0
+    bias = torch.log(torch.randint(1, 5, (B, 1, Lk), generator=g).float()) if with_bias else None
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    bd = None if bias is None else bias.to(dev)
+    full = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bd)
+    wide = torch.full((B, H, Lq, 48), 5.0, dtype=torch.bfloat16, device=dev)
+    got = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bd, out=wide[..., 8:40],
+                                 v_cols=32)
+    torch.cuda.synchronize()
+    assert got.shape == (B, H, Lq, 32)
+    assert torch.equal(got, full[..., :32])
+    assert torch.all(wide[..., :8] == 5.0) and torch.all(wide[..., 40:] == 5.0)
+    want = masked_attention(q, k, v, mask, 0.125, key_bias=None if bias is None else bias.double())
+    _check(got, want[..., :32])
+    assert torch.all(got.cpu()[1, 0, 128:192] == 0)
+    with pytest.raises(NotImplementedError):
+        block_sparse_attention(q.half().to(dev), k.half().to(dev), v.half().to(dev), kv, 0.125, v_cols=32)
