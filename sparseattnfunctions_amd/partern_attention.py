@@ -188,12 +188,11 @@ class ParternAttentionColVersion_V2:
                 q.data_ptr(), _lib.i64(*q.stride()[:3]), B, H, L, D, q_idx.data_ptr(), F * S, q_sel.data_ptr(),
                 _lib.i64(*q_sel.stride()[:3]), stream), "sa_gather_tokens_heads")
         o_frames = torch.empty(B, H, F * S, D, dtype=q.dtype, device=dev)
-        frame_kv = _dense(B, H, S, S, dev)
-        for i in range(F):
-            rows = slice(i * S, (i + 1) * S)
-            keys = slice(T + i * S, T + (i + 1) * S)
-            block_sparse_attention(q_sel[:, :, rows], k[:, :, keys], v[:, :, keys], frame_kv, scale_factor,
-                                   out=o_frames[:, :, rows])
+        # Frame i's selected rows over frame i's keys, for every frame in one launch: (b, h) as
+        # the batch index and the frame as the head index of [B*H, F, S, D] views.
+        block_sparse_attention(q_sel.view(B * H, F, S, D), k[:, :, T:T + F * S].view(B * H, F, S, D),
+                               v[:, :, T:T + F * S].view(B * H, F, S, D), _dense(B * H, F, S, S, dev),
+                               scale_factor, out=o_frames.view(B * H, F, S, D))
         with torch.cuda.device(dev):
             _lib.check(lib.sa_pattern_combine(
                 o_frames.data_ptr(), _lib.i64(*o_frames.stride()[:3]), o_text.data_ptr(),
