@@ -108,8 +108,9 @@ int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const
  * out has 32 columns: v [B,H,Lk,64] as there (its tiles are read whole), out [B,H,Lq,32].
  * For a v whose other columns are zero or unused: the segment-indicator v of the
  * frame-pattern masses (ParternAttentionColVersion_V2.get_weight_for_patch and the
- * first-frame softmax, partern_attention.py:321-358, 400-420) has 1 + frames <= 32 nonzero
- * columns. Same lists, key_bias, work order and error contract; never split into key ranges.
+ * first-frame softmax and its segment sums, partern_attention.py:321-358, 413, 430, 443) has
+ * 1 + frames <= 32 nonzero columns. Same lists, key_bias, work order and error contract;
+ * never split into key ranges.
  */
 int sa_block_sparse_fwd_v32(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                             const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
