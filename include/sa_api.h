@@ -80,7 +80,9 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
  * sa_attn_split_parts) splits each block's list into key ranges, one wave each, and merges
  * their fp32 partials in a second kernel; work_order is then not read. The partials are
  * allocated stream-ordered on `stream` (hipMallocAsync, freed with hipFreeAsync after the
- * merge); if that allocation fails the launch runs unsplit.
+ * merge); if that allocation fails the launch runs unsplit. A caller that must not allocate
+ * at all keeps to launches that sa_attn_split_parts reports as unsplit (for instance by
+ * giving lists narrower than 64 blocks, or enough query blocks).
  */
 int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                         const int64_t k_strides[3], const uint16_t* v,
