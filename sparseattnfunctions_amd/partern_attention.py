@@ -60,6 +60,15 @@ sample_rate = torch.tensor(sample_num / (width * height))
 composition = torch.log(sample_rate).view(1, 1, 1, 1)
 
 _CACHE = {}
+OVERLAP_TEXT = True  # video-to-text rows on a second stream (see forward)
+_SIDE = {}
+
+
+def _side_stream(device):
+    s = _SIDE.get(str(device))
+    if s is None:
+        s = _SIDE[str(device)] = torch.cuda.Stream(device=device)
+    return s
 
 
 def _cached(key, make):
@@ -159,15 +168,21 @@ class ParternAttentionColVersion_V2:
         if index_k is None:
             _, index_k = get_indexs(g)
         out = torch.empty_like(q)
+        # Video rows over the text keys (img2text_detailed_attention @ v_text): many short,
+        # latency-bound blocks, launched on a second stream (default priority) so that they
+        # run alongside the compute-bound launches below; joined before the final mix.
+        main = torch.cuda.current_stream(dev)
+        text_kv = _dense(B, H, F * S, T, dev)
+        side = _side_stream(dev) if OVERLAP_TEXT else main
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            o_text = block_sparse_attention(q[:, :, T:], k[:, :, :T], v[:, :, :T], text_kv, scale_factor)
         # Text rows over every key (the reference's SDPA, :442).
         block_sparse_attention(q[:, :, :T], k, v, _dense(B, H, T, L, dev), scale_factor, out=out[:, :, :T])
         # First-frame rows over every key: per-segment masses (text, frame i).
         ff_mass = block_sparse_attention(q[:, :, T:T + S], k, _bcast(_frame_indicator(g, dev), B, H),
                                          _dense(B, H, S, L, dev), scale_factor, v_cols=_mass_cols(g))
         map_mass = self.sampled_masses(q, k, index_k)
-        # Video rows over the text keys (img2text_detailed_attention @ v_text).
-        o_text = block_sparse_attention(q[:, :, T:], k[:, :, :T], v[:, :, :T], _dense(B, H, F * S, T, dev),
-                                        scale_factor)
         BH = B * H
         f32 = dict(dtype=torch.float32, device=dev)
         i2i, i2t = self._maps(map_mass)
@@ -189,10 +204,22 @@ class ParternAttentionColVersion_V2:
                 _lib.i64(*q_sel.stride()[:3]), stream), "sa_gather_tokens_heads")
         o_frames = torch.empty(B, H, F * S, D, dtype=q.dtype, device=dev)
         # Frame i's selected rows over frame i's keys, for every frame in one launch: (b, h) as
-        # the batch index and the frame as the head index of [B*H, F, S, D] views.
-        block_sparse_attention(q_sel.view(B * H, F, S, D), k[:, :, T:T + F * S].view(B * H, F, S, D),
-                               v[:, :, T:T + F * S].view(B * H, F, S, D), _dense(B * H, F, S, S, dev),
-                               scale_factor, out=o_frames.view(B * H, F, S, D))
+        # the batch index and the frame as the head index of [B*H, F, S, D] views. Inputs whose
+        # batch and head axes do not merge into one stride (a slice of a tensor's heads) take
+        # one launch per frame.
+        if all(x.stride(0) == H * x.stride(1) or B == 1 for x in (k, v)):
+            block_sparse_attention(q_sel.view(B * H, F, S, D), k[:, :, T:T + F * S].reshape(B * H, F, S, D),
+                                   v[:, :, T:T + F * S].reshape(B * H, F, S, D), _dense(B * H, F, S, S, dev),
+                                   scale_factor, out=o_frames.view(B * H, F, S, D))
+        else:
+            frame_kv = _dense(B, H, S, S, dev)
+            for i in range(F):
+                rows = slice(i * S, (i + 1) * S)
+                keys = slice(T + i * S, T + (i + 1) * S)
+                block_sparse_attention(q_sel[:, :, rows], k[:, :, keys], v[:, :, keys], frame_kv, scale_factor,
+                                       out=o_frames[:, :, rows])
+        main.wait_stream(side)
+        o_text.record_stream(main)
         with torch.cuda.device(dev):
             _lib.check(lib.sa_pattern_combine(
                 o_frames.data_ptr(), _lib.i64(*o_frames.stride()[:3]), o_text.data_ptr(),

@@ -63,6 +63,28 @@ def test_forward_matches_oracle(dev, seed):
     assert err.mean().item() <= 3e-3, err.mean().item()
 
 
+
+def test_forward_head_slices_and_streams_agree(dev):
+    # The frames run as one launch over [B*H, F, S, 64] views when the batch and head axes of
+    # k and v merge, else one launch per frame (a slice of a tensor's heads, B = 2); the
+    # video-to-text rows run on a second stream or not. Every variant gives the same bits.
+    case("pattern forward: head slices, one or eleven frame launches, one or two streams")
+    q, k, v = _inputs(4, B=2, H=8)
+    _, idx = pa.get_indexs(G)
+    proc = pa.ParternAttentionColVersion_V2(G)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    sliced = proc(qd[:, 2:6], kd[:, 2:6], vd[:, 2:6], index_k=idx)
+    whole = proc(qd[:, 2:6].contiguous(), kd[:, 2:6].contiguous(), vd[:, 2:6].contiguous(), index_k=idx)
+    try:
+        pa.OVERLAP_TEXT = not pa.OVERLAP_TEXT
+        other = proc(qd[:, 2:6].contiguous(), kd[:, 2:6].contiguous(), vd[:, 2:6].contiguous(), index_k=idx)
+    finally:
+        pa.OVERLAP_TEXT = not pa.OVERLAP_TEXT
+    torch.cuda.synchronize()
+    assert torch.equal(sliced, whole)
+    assert torch.equal(other, whole)
+
+
 def _directed(a=2.5):
     # Frame f's queries boost the keys of frame f+1 and carry a per-frame slope g_f on a
     # position channel (first-frame rows also a per-row text component); v is one direction
