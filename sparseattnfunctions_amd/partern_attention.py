@@ -168,17 +168,19 @@ class ParternAttentionColVersion_V2:
         if index_k is None:
             _, index_k = get_indexs(g)
         out = torch.empty_like(q)
-        # Video rows over the text keys (img2text_detailed_attention @ v_text): many short,
-        # latency-bound blocks, launched on a second stream (default priority) so that they
-        # run alongside the compute-bound launches below; joined before the final mix.
+        # Video rows over the text keys (img2text_detailed_attention @ v_text; many short,
+        # latency-bound blocks) and the text rows, launched on a second stream (default
+        # priority) so that they run alongside the compute-bound launches below; joined before
+        # the final mix.
         main = torch.cuda.current_stream(dev)
         text_kv = _dense(B, H, F * S, T, dev)
         side = _side_stream(dev) if OVERLAP_TEXT else main
         side.wait_stream(main)
+        text_rows_kv = _dense(B, H, T, L, dev)
         with torch.cuda.stream(side):
             o_text = block_sparse_attention(q[:, :, T:], k[:, :, :T], v[:, :, :T], text_kv, scale_factor)
-        # Text rows over every key (the reference's SDPA, :442).
-        block_sparse_attention(q[:, :, :T], k, v, _dense(B, H, T, L, dev), scale_factor, out=out[:, :, :T])
+            # Text rows over every key (the reference's SDPA, :442).
+            block_sparse_attention(q[:, :, :T], k, v, text_rows_kv, scale_factor, out=out[:, :, :T])
         # First-frame rows over every key: per-segment masses (text, frame i).
         ff_mass = block_sparse_attention(q[:, :, T:T + S], k, _bcast(_frame_indicator(g, dev), B, H),
                                          _dense(B, H, S, L, dev), scale_factor, v_cols=_mass_cols(g))
