@@ -60,7 +60,8 @@ sample_rate = torch.tensor(sample_num / (width * height))
 composition = torch.log(sample_rate).view(1, 1, 1, 1)
 
 _CACHE = {}
-OVERLAP_TEXT = True  # video-to-text rows on a second stream (see forward)
+OVERLAP_TEXT = True  # text and video-to-text rows on a second stream (see forward)
+OVERLAP_JUDGE = True  # sparsity judge on a second stream (see unified_judge)
 _SIDE = {}
 
 
@@ -424,8 +425,16 @@ def unified_judge(q, k, geometry: PatternGeometry = DEFAULT, draws=None):
     else:
         idx_q, ik1, ik2 = draws
     B, H = q.shape[:2]
-    share = _sparsity_rows(q, k, g, idx_q)
+    # The sparsity judge (written probabilities and a latency-bound top-k pass) runs on a
+    # second stream (default priority) beside the two similarity judges (exp2/VALU-bound).
+    main = torch.cuda.current_stream(q.device)
+    side = _side_stream(q.device) if OVERLAP_JUDGE else main
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        share = _sparsity_rows(q, k, g, idx_q)
     G1 = _similarity_gram(q, k, g, ik1)
     G2 = _similarity_gram(q, k, g, ik2)
+    main.wait_stream(side)
+    share.record_stream(main)
     sm, c1, c2, use = _finish(share, G1, G2, B * H, idx_q.numel(), g.frames, g.sample_num, q.device)
     return use.view(B, H).bool()
