@@ -174,6 +174,12 @@ def test_judges_match_oracle(dev):
     p2 = ik2[G.text_length: G.text_length + G.sample_num] - G.text_length
     want = opat.unified_judge(q, k, idx_q, p1, p2, G.frames, G.S, G.text_length)
     assert torch.equal(use.cpu(), want)
+    try:  # the sparsity judge on the caller's stream instead of the second one: same decisions
+        pa.OVERLAP_JUDGE = not pa.OVERLAP_JUDGE
+        other = pa.unified_judge(qd, kd, G, draws=(idx_q, ik1, ik2))
+    finally:
+        pa.OVERLAP_JUDGE = not pa.OVERLAP_JUDGE
+    assert torch.equal(other.cpu(), want)
 
 
 def test_fused_gram_matches_written_probabilities(dev):
