@@ -10,8 +10,10 @@
  *    strides {stride_b, stride_h, stride_l}; the D axis must be contiguous (stride 1).
  *    Element type is bf16 (uint16_t bit patterns) unless stated otherwise.
  *  - Device buffers are owned by the caller (PyTorch's caching allocator in the Python
- *    package). The library allocates no device memory; its one device-resident buffer is
- *    the fixed scratch array of sa_tome_match_noalloc, part of the loaded code object.
+ *    package), including every workspace (sized by the *_workspace queries). The library
+ *    allocates no device memory and changes no allocator or device setting; its one
+ *    device-resident buffer is the fixed scratch array of sa_tome_match_noalloc, part of the
+ *    loaded code object.
  *  - `stream` is a hipStream_t passed as void*; NULL means the default stream. All GPU
  *    work is enqueued asynchronously on it; no entry point synchronises the device.
  *  - Entry points documented as "host" run on the CPU only and touch no GPU state.
@@ -37,7 +39,7 @@ extern "C" {
 #define SA_ERR_UNSUPPORTED (-2) /* valid but not implemented (e.g. head_dim != 64) */
 #define SA_ERR_HIP (-3)         /* a HIP runtime call failed (launch, device query) */
 
-#define SA_ABI_VERSION 2
+#define SA_ABI_VERSION 3
 
 /* Version of this ABI (SA_ABI_VERSION). */
 int sa_abi_version(void);
@@ -76,13 +78,8 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
  *   sm_scale  > 0 and finite.
  *   work_order nullable int32 [n_slots] from sa_attn_work_order (device copy): dispatch
  *             slot -> list row, -1 = idle. NULL visits rows in index order.
- * A launch with few query blocks and long lists (plain lists without key_bias; see
- * sa_attn_split_parts) splits each block's list into key ranges, one wave each, and merges
- * their fp32 partials in a second kernel; work_order is then not read. The partials are
- * allocated stream-ordered on `stream` (hipMallocAsync, freed with hipFreeAsync after the
- * merge); if that allocation fails the launch runs unsplit. A caller that must not allocate
- * at all keeps to launches that sa_attn_split_parts reports as unsplit (for instance by
- * giving lists narrower than 64 blocks, or enough query blocks).
+ * One wave per query block, never split into key ranges (sa_block_sparse_fwd_split is the
+ * variant for few query blocks over long lists).
  */
 int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                         const int64_t k_strides[3], const uint16_t* v,
@@ -240,15 +237,59 @@ int sa_attn_work_order(int B, int H, int nqb, int n_text_blocks, int n_xcd, int3
                        int64_t* n_slots);
 
 /*
- * Key-range parts per query block that the attention entry points use on the current device
- * for a launch of n_items = B*H*ceil(Lq/64) query blocks with lists of width max_cnt and
- * head dim D (plain lists: no key_bias, no tile masks, no pooling). *parts = 1: no split.
- * Parts are chosen to fill the device's wave slots (compute units x resident waves) once, with
- * at least 32 list positions per part at the list width; lists narrower than 64 are never
- * split, nor launches whose blocks fill half the slots. No counterpart in the reference (its
- * Triton launch has one program per query block); for tests and for integrators sizing calls.
+ * Host. Suggested key-range parts per query block for sa_block_sparse_fwd_split: a launch of
+ * n_items = B*H*ceil(Lq/64) query blocks with lists of width max_cnt, head dim D, on a device
+ * of n_cus compute units (MI355X: 256). *parts = 1: no split. Parts are chosen to fill the
+ * wave slots (n_cus x 8 waves at D = 64, x 4 at 128) once, with at least 32 list positions per
+ * part at the list width, at most 16; lists narrower than 64 are never split, nor launches
+ * whose blocks fill half the slots. A pure function of its arguments (no device query). No
+ * counterpart in the reference (its Triton launch has one program per query block).
  */
-int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int* parts);
+int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int n_cus, int* parts);
+
+/*
+ * Host. Workspace bytes sa_block_sparse_fwd_split needs for n_items query blocks, head dim D
+ * and `parts` key-range parts (1..16): n_items * parts * (64*D + 128) * 4 (fp32 acc, row
+ * sums and row maxima per part); 0 for parts = 1.
+ */
+int sa_attn_split_workspace(int64_t n_items, int D, int parts, int64_t* bytes);
+
+/*
+ * Block-sparse attention with each query block's list split into `parts` key ranges: as
+ * sa_block_sparse_fwd (bf16, D = 64 or 128, plain lists, no key_bias) with the optional row
+ * maps of sa_block_sparse_fwd_mapped (NULL: identity), for launches with few query blocks
+ * over long lists, where one wave per block would leave most of the GPU idle. Part p of a
+ * block with c list entries visits positions [c*p/parts, c*(p+1)/parts) in one wave and stores
+ * its unnormalised fp32 partial (acc, row sum, row maximum) to `workspace`; a second kernel
+ * on the same stream rescales the partials by their row maxima, sums them in part order and
+ * normalises once. The output is a deterministic function of the arguments (parts included)
+ * and equals the unsplit launch up to the fp32 summation order (one bf16 rounding step);
+ * parts = 1 is the unsplit launch itself.
+ * Replaces the same reference work as sa_block_sparse_fwd
+ * (utils/block_sparse_attn_kernel.py:52-265), one Triton program per query block there.
+ *   parts      1..16 (sa_attn_split_parts suggests one).
+ *   workspace  device memory of >= sa_attn_split_workspace(B*H*ceil(Lq/64), D, parts) bytes,
+ *              16-byte aligned, owned by the caller; read and written by this call's kernels
+ *              on `stream` only (free or reuse it after them in stream order). NULL only with
+ *              parts = 1.
+ */
+int sa_block_sparse_fwd_split(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                              const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                              uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                              int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                              float sm_scale, const int32_t* q_rows, int q_src_rows,
+                              const int32_t* o_rows, int o_dst_rows, int parts, void* workspace,
+                              int64_t workspace_bytes, void* stream);
+
+/* sa_block_sparse_fwd_split for fp16 q, k, v and out (P rounded to fp16, running row maximum). */
+int sa_block_sparse_fwd_split_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                  const int64_t k_strides[3], const uint16_t* v,
+                                  const int64_t v_strides[3], uint16_t* out,
+                                  const int64_t out_strides[3], int B, int H, int Lq, int Lk, int D,
+                                  const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                  float sm_scale, const int32_t* q_rows, int q_src_rows,
+                                  const int32_t* o_rows, int o_dst_rows, int parts, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
 
 /*
  * Block means of q and k: pooled[(b*H + h)*nb + blk][d] = mean over the block's tokens,

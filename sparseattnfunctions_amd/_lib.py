@@ -15,7 +15,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsa_hip.so")
 
-ABI_VERSION = 2  # SA_ABI_VERSION of include/sa_api.h these prototypes describe
+ABI_VERSION = 3  # SA_ABI_VERSION of include/sa_api.h these prototypes describe
 
 SA_OK = 0
 SA_ERR_INVALID = -1
@@ -70,7 +70,18 @@ _PROTOTYPES = {
          _P, _I, _P, _I, _P, ctypes.c_int64, _P],
     ),
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
-    "sa_attn_split_parts": (_I, [ctypes.c_int64, _I, _I, ctypes.POINTER(_I)]),
+    "sa_attn_split_parts": (_I, [ctypes.c_int64, _I, _I, _I, ctypes.POINTER(_I)]),
+    "sa_attn_split_workspace": (_I, [ctypes.c_int64, _I, _I, _I64P]),
+    "sa_block_sparse_fwd_split": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P, _I, _P, _I, _I, _P,
+         ctypes.c_int64, _P],
+    ),
+    "sa_block_sparse_fwd_split_f16": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P, _I, _P, _I, _I, _P,
+         ctypes.c_int64, _P],
+    ),
     "sa_attn_pooling_workspace": (_I, [_I, _I, _I, _I, _I64P]),
     "sa_attn_pooling_fwd": (
         _I,

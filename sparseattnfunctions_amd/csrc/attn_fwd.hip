@@ -37,7 +37,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <atomic>
 #include <climits>
 #include <cmath>
 #include <type_traits>
@@ -898,36 +897,25 @@ __global__ __launch_bounds__(256) void split_merge_kernel(FwdArgs a) {
 }
 
 // Key-range split of a launch with few items: parts per item so that the parts fill the
-// device's wave slots once (CUs x resident waves per CU), with at least kSplitPartTiles list
-// positions per part at the list width; 1 = no split (also below kSplitMinTiles, or when the
-// items already fill half the slots).
+// wave slots of n_cus CUs once (resident waves per CU: 8 at head dim 64, 4 at 128), with at
+// least kSplitPartTiles list positions per part at the list width; 1 = no split (also below
+// kSplitMinTiles, or when the items already fill half the slots). A pure function of its
+// arguments: the caller passes the result to the split entry points, so a launch's bits
+// depend on nothing but its arguments.
 constexpr int kSplitMinTiles = 64;
 constexpr int kSplitPartTiles = 32;
 constexpr int kSplitMaxParts = 16;
 
-int split_parts(int64_t n_items, int max_cnt, int D) {
+int split_parts(int64_t n_items, int max_cnt, int D, int n_cus) {
   if (max_cnt < kSplitMinTiles) return 1;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                              hipSuccess || cus <= 0) {
-    (void)hipGetLastError();
-    return 1;
-  }
-  // Stream-ordered allocations of the partials: keep freed blocks in the device's default
-  // pool instead of returning them at every synchronisation (set once per device).
-  static std::atomic<uint64_t> pool_set{0};
-  if (dev < 64 && !(pool_set.load() & (1ull << dev))) {
-    hipMemPool_t pool;
-    uint64_t keep = UINT64_MAX;
-    if (hipDeviceGetDefaultMemPool(&pool, dev) != hipSuccess ||
-        hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep) != hipSuccess)
-      (void)hipGetLastError();
-    pool_set.fetch_or(1ull << dev);
-  }
-  const int64_t slots = (int64_t)cus * (D == 64 ? 2 : 1) * kWaves;
+  const int64_t slots = (int64_t)n_cus * (D == 64 ? 2 : 1) * kWaves;
   if (n_items * 2 > slots) return 1;
   const int64_t p = std::min<int64_t>({slots / n_items, max_cnt / kSplitPartTiles, kSplitMaxParts});
   return p > 1 ? (int)p : 1;
+}
+
+size_t split_workspace_bytes(int64_t n_items, int D, int parts) {
+  return (size_t)n_items * parts * (D == 64 ? kSplitFloats<64> : kSplitFloats<128>) * sizeof(float);
 }
 
 // One kernel variant per (tile masks, key bias, pooling columns): the caller has rejected
@@ -963,7 +951,7 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
                const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
                float* pool_lse = nullptr, const PoolOut* pool_out = nullptr, bool fp16 = false,
-               bool v32 = false) {
+               bool v32 = false, int parts = 1, void* split_ws = nullptr, int64_t split_ws_bytes = 0) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -1049,25 +1037,25 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   if (pool_cols && key_bias) return sa::fail(SA_ERR_UNSUPPORTED, "%s: pooling with key_bias", fn);
   hipStream_t s = sa::as_stream(stream);
   const bool mask = kv_slot != nullptr, bias = key_bias != nullptr;
-  // Few items with long plain lists leave most wave slots idle: each item's list is split
-  // into key ranges, one wave each, and split_merge_kernel forms the outputs from the
-  // partials. The partials live in stream-ordered memory (hipMallocAsync / hipFreeAsync on
-  // the call's stream); without it the launch runs unsplit.
+  // Few items with long plain lists leave most wave slots idle: with parts > 1 each item's
+  // list is split into key ranges, one wave each, whose partials go to the caller's
+  // workspace, and split_merge_kernel forms the outputs from them.
   int64_t grid_x = grid;
-  if (!mask && !bias && pool_cols == 0 && !v32) {
-    const int parts = split_parts(n_items, max_cnt, D);
-    if (parts > 1) {
-      const size_t bytes = (size_t)n_items * parts * (D == 64 ? kSplitFloats<64> : kSplitFloats<128>) * sizeof(float);
-      void* ws = nullptr;
-      if (hipMallocAsync(&ws, bytes, s) == hipSuccess && ws) {
-        a.n_parts = parts;
-        a.ws = static_cast<float*>(ws);
-        a.n_slots = (int)((n_items * parts + kWaves - 1) / kWaves * kWaves);
-        grid_x = a.n_slots / kWaves;
-      } else {
-        (void)hipGetLastError();
-      }
-    }
+  if (parts > 1) {
+    if (mask || bias || pool_cols || v32)
+      return sa::fail(SA_ERR_UNSUPPORTED, "%s: key-range parts with tile masks, key_bias, pooling or 32 value columns",
+                      fn);
+    SA_REQUIRE(parts <= kSplitMaxParts, "%s: parts=%d > %d", fn, parts, kSplitMaxParts);
+    const size_t need = split_workspace_bytes(n_items, D, parts);
+    SA_REQUIRE(split_ws, "%s: null workspace with parts=%d", fn, parts);
+    SA_REQUIRE(reinterpret_cast<uintptr_t>(split_ws) % 16 == 0, "%s: workspace not 16-byte aligned", fn);
+    SA_REQUIRE(split_ws_bytes >= 0 && (size_t)split_ws_bytes >= need, "%s: workspace of %lld bytes < %zu", fn,
+               (long long)split_ws_bytes, need);
+    SA_REQUIRE(n_items * parts < (1LL << 30), "%s: too many key-range parts", fn);
+    a.n_parts = parts;
+    a.ws = static_cast<float*>(split_ws);
+    a.n_slots = (int)((n_items * parts + kWaves - 1) / kWaves * kWaves);
+    grid_x = a.n_slots / kWaves;
   }
   const dim3 g((unsigned)grid_x), blk(64 * kWaves);
   if (fp16) {
@@ -1086,21 +1074,68 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
       if (D == 64) hipLaunchKernelGGL((split_merge_kernel<__bf16, 64>), gm, bm, 0, s, a);
       else hipLaunchKernelGGL((split_merge_kernel<__bf16, 128>), gm, bm, 0, s, a);
     }
-    const int rc = sa::check_launch(fn);
-    (void)hipFreeAsync(a.ws, s);
-    return rc;
   }
   return sa::check_launch(fn);
 }
 
 }  // namespace
 
-extern "C" int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int* parts) {
+extern "C" int sa_attn_split_parts(int64_t n_items, int max_cnt, int D, int n_cus, int* parts) {
   SA_REQUIRE(parts, "sa_attn_split_parts: null parts");
-  SA_REQUIRE(n_items > 0 && max_cnt > 0 && (D == 64 || D == 128),
-             "sa_attn_split_parts: bad arguments n_items=%lld max_cnt=%d D=%d", (long long)n_items, max_cnt, D);
-  *parts = split_parts(n_items, max_cnt, D);
+  SA_REQUIRE(n_items > 0 && max_cnt > 0 && (D == 64 || D == 128) && n_cus > 0,
+             "sa_attn_split_parts: bad arguments n_items=%lld max_cnt=%d D=%d n_cus=%d", (long long)n_items, max_cnt,
+             D, n_cus);
+  *parts = split_parts(n_items, max_cnt, D, n_cus);
   return sa::ok();
+}
+
+extern "C" int sa_attn_split_workspace(int64_t n_items, int D, int parts, int64_t* bytes) {
+  SA_REQUIRE(bytes, "sa_attn_split_workspace: null bytes");
+  SA_REQUIRE(n_items > 0 && n_items < (1LL << 30) && (D == 64 || D == 128) && parts >= 1 && parts <= kSplitMaxParts,
+             "sa_attn_split_workspace: bad arguments n_items=%lld D=%d parts=%d", (long long)n_items, D, parts);
+  *bytes = parts > 1 ? (int64_t)split_workspace_bytes(n_items, D, parts) : 0;
+  return sa::ok();
+}
+
+namespace {
+
+int fwd_split(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
+              const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B, int H,
+              int Lq, int Lk, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt, float sm_scale,
+              const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, int parts,
+              void* workspace, int64_t workspace_bytes, void* stream, bool fp16, const char* fn) {
+  SA_REQUIRE(parts >= 1, "%s: parts=%d must be >= 1", fn, parts);
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, false, nullptr, nullptr, nullptr, nullptr, sm_scale, nullptr, 0, q_rows, q_src_rows,
+                    o_rows, o_dst_rows, stream, fn, 1, 0, nullptr, nullptr, nullptr, fp16, false, parts, workspace,
+                    workspace_bytes);
+}
+
+}  // namespace
+
+extern "C" int sa_block_sparse_fwd_split(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                         const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                         uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                         int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                         float sm_scale, const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                                         int o_dst_rows, int parts, void* workspace, int64_t workspace_bytes,
+                                         void* stream) {
+  return fwd_split(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                   max_cnt, sm_scale, q_rows, q_src_rows, o_rows, o_dst_rows, parts, workspace, workspace_bytes,
+                   stream, false, "sa_block_sparse_fwd_split");
+}
+
+extern "C" int sa_block_sparse_fwd_split_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                             const int64_t k_strides[3], const uint16_t* v,
+                                             const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3],
+                                             int B, int H, int Lq, int Lk, int D, const int32_t* kv_idx,
+                                             const int32_t* kv_cnt, int max_cnt, float sm_scale,
+                                             const int32_t* q_rows, int q_src_rows, const int32_t* o_rows,
+                                             int o_dst_rows, int parts, void* workspace, int64_t workspace_bytes,
+                                             void* stream) {
+  return fwd_split(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                   max_cnt, sm_scale, q_rows, q_src_rows, o_rows, o_dst_rows, parts, workspace, workspace_bytes,
+                   stream, true, "sa_block_sparse_fwd_split_f16");
 }
 
 extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,

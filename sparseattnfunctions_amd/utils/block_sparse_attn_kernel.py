@@ -44,6 +44,25 @@ def _prep_qkv(t: torch.Tensor, dtypes=(torch.bfloat16,)) -> torch.Tensor:
 
 
 N_XCD = 8  # MI355X: workgroups are dealt round-robin to 8 XCDs, each with its own L2
+# MI355X compute units. The key-range split is sized for this fixed count rather than the
+# runtime's, so that a launch's parts, and with them its output bits, depend on its shape only.
+N_CU = 256
+
+
+def split_parts(n_items: int, max_cnt: int, D: int) -> int:
+    """Key-range parts per query block (`sa_attn_split_parts`) for a plain launch of n_items
+    query blocks over lists of width max_cnt: 1 means one wave per block."""
+    parts = ctypes.c_int(0)
+    _lib.check(_lib.load().sa_attn_split_parts(int(n_items), int(max_cnt), int(D), N_CU, ctypes.byref(parts)),
+               "sa_attn_split_parts")
+    return parts.value
+
+
+def split_workspace_bytes(n_items: int, D: int, parts: int) -> int:
+    n = ctypes.c_int64(0)
+    _lib.check(_lib.load().sa_attn_split_workspace(int(n_items), int(D), int(parts), ctypes.byref(n)),
+               "sa_attn_split_workspace")
+    return n.value
 
 _ORDER_CACHE = {}
 
@@ -130,8 +149,26 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
             raise ValueError("key_bias must be fp32 [B,H,Lk] with a contiguous key axis")
         key_bias = key_bias.expand(B, H, Lk)
         bias_ptr, bias_strides = key_bias.data_ptr(), _lib.i64(key_bias.stride(0), key_bias.stride(1))
-    order = work_order(B, H, math.ceil(Lq / BLOCK), n_text_blocks, q.device)
     lib = _lib.load()
+    nqb = math.ceil(Lq / BLOCK)
+    parts = 1
+    if not fp32 and key_bias is None and tile_masks is None and Dout == D:
+        parts = split_parts(B * H * nqb, kv.max_cnt, D)
+    if parts > 1:
+        # Few query blocks over long lists: key-range parts, their partials in a workspace
+        # from the caching allocator on this stream (the kernels use it in stream order).
+        ws = torch.empty(split_workspace_bytes(B * H * nqb, D, parts), dtype=torch.uint8, device=q.device)
+        fn = "sa_block_sparse_fwd_split_f16" if fp16 else "sa_block_sparse_fwd_split"
+        with torch.cuda.device(q.device):
+            rc = getattr(lib, fn)(
+                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
+                B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, float(sm_scale),
+                _lib.ptr(q_rows), Lsrc, _lib.ptr(o_rows), out.shape[2], parts, ws.data_ptr(), ws.numel(),
+                _lib.stream_of(q))
+        _lib.check(rc, fn)
+        return out
+    order = work_order(B, H, nqb, n_text_blocks, q.device)
     if q_rows is not None or o_rows is not None or tile_masks is not None:
         kv_slot, masks = (tile_masks[0], tile_masks[1]) if tile_masks is not None else (None, None)
         fn = "sa_block_sparse_fwd_mapped_f16" if fp16 else "sa_block_sparse_fwd_mapped"

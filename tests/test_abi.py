@@ -32,7 +32,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.sa_abi_version() == 2 == _lib.ABI_VERSION
+    assert lib.sa_abi_version() == 3 == _lib.ABI_VERSION
     assert lib.sa_last_error() is not None
 
 
@@ -95,10 +95,65 @@ def test_work_order_is_a_permutation(lib):
 
 def test_split_parts_query(lib):
     parts = ctypes.c_int(-1)
-    assert lib.sa_attn_split_parts(0, 128, 64, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
-    assert lib.sa_attn_split_parts(4, 128, 96, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
-    assert lib.sa_attn_split_parts(4, 128, 64, None) == _lib.SA_ERR_INVALID
-    # lists narrower than 64 positions are never split (no device query needed)
-    assert lib.sa_attn_split_parts(4, 63, 64, ctypes.byref(parts)) == _lib.SA_OK and parts.value == 1
-    # wide lists: 1 without a GPU (no device to size against), else >= 1
-    assert lib.sa_attn_split_parts(4, 128, 64, ctypes.byref(parts)) == _lib.SA_OK and parts.value >= 1
+    assert lib.sa_attn_split_parts(0, 128, 64, 256, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_parts(4, 128, 96, 256, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_parts(4, 128, 64, 0, ctypes.byref(parts)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_parts(4, 128, 64, 256, None) == _lib.SA_ERR_INVALID
+
+    def q(n, w, d, cus=256):
+        assert lib.sa_attn_split_parts(n, w, d, cus, ctypes.byref(parts)) == _lib.SA_OK
+        return parts.value
+
+    # A pure function of its arguments: min(slots / n, width / 32, 16) parts while the blocks
+    # fill at most half of the slots (256 CUs x 8 waves at head dim 64, x 4 at 128), lists of
+    # at least 64 positions.
+    assert q(4, 63, 64) == 1
+    assert q(4, 128, 64) == 4 and q(4, 705, 64) == 16 and q(4, 705, 128) == 16
+    assert q(384, 705, 64) == 5 and q(384, 705, 128) == 2
+    assert q(1024, 705, 64) == 2 and q(1025, 705, 64) == 1 and q(513, 705, 128) == 1
+    assert q(384, 705, 64, cus=32) == 1 and q(8, 705, 64, cus=32) == 16
+    assert [q(384, 705, 64) for _ in range(3)] == [5, 5, 5]
+
+
+def test_split_workspace_query(lib):
+    n = ctypes.c_int64(-1)
+    assert lib.sa_attn_split_workspace(10, 64, 4, ctypes.byref(n)) == _lib.SA_OK
+    assert n.value == 10 * 4 * (64 * 64 + 128) * 4
+    assert lib.sa_attn_split_workspace(10, 128, 16, ctypes.byref(n)) == _lib.SA_OK
+    assert n.value == 10 * 16 * (64 * 128 + 128) * 4
+    assert lib.sa_attn_split_workspace(10, 64, 1, ctypes.byref(n)) == _lib.SA_OK and n.value == 0
+    for bad in [(0, 64, 2), (10, 96, 2), (10, 64, 0), (10, 64, 17)]:
+        assert lib.sa_attn_split_workspace(*bad, ctypes.byref(n)) == _lib.SA_ERR_INVALID
+    assert lib.sa_attn_split_workspace(10, 64, 2, None) == _lib.SA_ERR_INVALID
+
+
+def test_split_launch_validates_workspace(lib):
+    # Rejected before any GPU work: parts out of range, no workspace, a short or misaligned one.
+    dummy = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    s3 = _lib.i64(0, 0, 0)
+    B, H, Lq, Lk, D = 1, 2, 64, 8192, 64
+    need = ctypes.c_int64(0)
+    assert lib.sa_attn_split_workspace(B * H, D, 4, ctypes.byref(need)) == _lib.SA_OK
+
+    def call(parts, ws, nbytes):
+        return lib.sa_block_sparse_fwd_split(dummy, s3, dummy, s3, dummy, s3, dummy, s3, B, H, Lq, Lk, D, dummy,
+                                             dummy, Lk // 64, 0.125, None, 0, None, 0, parts, ws, nbytes, None)
+
+    assert call(0, dummy, need.value) == _lib.SA_ERR_INVALID and b"parts" in lib.sa_last_error()
+    assert call(17, dummy, 1 << 30) == _lib.SA_ERR_INVALID and b"parts" in lib.sa_last_error()
+    assert call(4, None, need.value) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
+    assert call(4, dummy, need.value - 1) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
+    assert call(4, ctypes.c_void_p(4104), need.value) == _lib.SA_ERR_INVALID
+    assert b"aligned" in lib.sa_last_error()
+
+
+def test_library_allocates_no_device_memory():
+    # The only device buffer the library owns is the fixed scratch array of the no-alloc
+    # matching entry point; no source calls an allocator or changes a memory pool.
+    csrc = os.path.join(os.path.dirname(HEADER), "..", "sparseattnfunctions_amd", "csrc")
+    names = sorted(f for f in os.listdir(csrc) if f.endswith((".hip", ".h")))
+    assert "attn_fwd.hip" in names
+    pat = re.compile(r"\bhip(Malloc|Free|MemPool|ExtMalloc|HostMalloc|MallocManaged|DeviceSetMemPool)\w*")
+    for f in names:
+        hits = pat.findall(open(os.path.join(csrc, f)).read())
+        assert not hits, (f, hits)

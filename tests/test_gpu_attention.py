@@ -418,11 +418,8 @@ def test_fp32_strided_and_large_scores(dev):
 
 
 def _split_parts(n_items, max_cnt, D=64):
-    import ctypes
-    from sparseattnfunctions_amd import _lib
-    parts = ctypes.c_int(0)
-    _lib.check(_lib.load().sa_attn_split_parts(n_items, max_cnt, D, ctypes.byref(parts)), "sa_attn_split_parts")
-    return parts.value
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import split_parts
+    return split_parts(n_items, max_cnt, D)
 
 
 @pytest.mark.parametrize("B,H,Lq,Lk,D,dtype,amp", [
@@ -552,3 +549,67 @@ def test_v32_matches_first_columns(dev, with_bias):
     assert torch.all(got.cpu()[1, 0, 128:192] == 0)
     with pytest.raises(NotImplementedError):
         block_sparse_attention(q.half().to(dev), k.half().to(dev), v.half().to(dev), kv, 0.125, v_cols=32)
+
+
+def _split_call(q, k, v, kv, scale, parts, ws, nbytes, out, fp16=False):
+    from sparseattnfunctions_amd import _lib
+    B, H, Lq, D = q.shape
+    fn = "sa_block_sparse_fwd_split_f16" if fp16 else "sa_block_sparse_fwd_split"
+    rc = getattr(_lib.load(), fn)(
+        q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+        v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
+        B, H, Lq, k.shape[2], D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, float(scale),
+        None, 0, None, 0, parts, None if ws is None else ws.data_ptr(), nbytes, _lib.stream_of(q))
+    _lib.check(rc, fn)
+    return out
+
+
+def test_key_range_split_caller_workspace(dev):
+    # The split runs in a workspace the caller owns: two calls with the same arguments give
+    # the same bits (also after the workspace held other data), both match the fp64 oracle,
+    # and parts = 1 without a workspace is the plain entry point's unsplit launch, bit for bit.
+    from sparseattnfunctions_amd import _lib
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import split_workspace_bytes
+    case("key-range split with a caller workspace")
+    B, H, Lq, Lk, D = 1, 3, 130, 7000, 64
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    parts = _split_parts(B * H * nqb, nkb, D)
+    assert parts > 1
+    q, k, v = _rand((B, H, Lq, D), 540), _rand((B, H, Lk, D), 541), _rand((B, H, Lk, D), 542)
+    g = torch.Generator().manual_seed(54)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.6
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    nbytes = split_workspace_bytes(B * H * nqb, D, parts)
+    ws = torch.full((nbytes,), 0x7F, dtype=torch.uint8, device=dev)
+    o1 = _split_call(qd, kd, vd, kv, 0.125, parts, ws, nbytes, torch.empty_like(qd))
+    ws.fill_(0xFF)  # NaN patterns: every partial is rewritten by the next call
+    o2 = _split_call(qd, kd, vd, kv, 0.125, parts, ws, nbytes, torch.empty_like(qd))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    want = masked_attention(q, k, v, mask, 0.125)
+    _check(o1, want)
+    # Other part counts: the same result up to the fp32 summation order of the partials.
+    o3 = _split_call(qd, kd, vd, kv, 0.125, 3, ws, nbytes, torch.empty_like(qd))
+    _check(o3, want)
+    # parts = 1 with no workspace, and the plain entry point (never split): one wave per block.
+    o4 = _split_call(qd, kd, vd, kv, 0.125, 1, None, 0, torch.empty_like(qd))
+    o5 = torch.empty_like(qd)
+    rc = _lib.load().sa_block_sparse_fwd(
+        qd.data_ptr(), _lib.i64(*qd.stride()[:3]), kd.data_ptr(), _lib.i64(*kd.stride()[:3]),
+        vd.data_ptr(), _lib.i64(*vd.stride()[:3]), o5.data_ptr(), _lib.i64(*o5.stride()[:3]),
+        B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, None, None, 0.125, None, 0,
+        _lib.stream_of(qd))
+    _lib.check(rc, "sa_block_sparse_fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(o4, o5)
+    _check(o5, want)
+    d = (o1.float() - o5.float()).abs()
+    assert d.max().item() <= 2 ** -8, d.max().item()
+    # A short workspace is refused before any launch.
+    rc = _lib.load().sa_block_sparse_fwd_split(
+        qd.data_ptr(), _lib.i64(*qd.stride()[:3]), kd.data_ptr(), _lib.i64(*kd.stride()[:3]),
+        vd.data_ptr(), _lib.i64(*vd.stride()[:3]), o5.data_ptr(), _lib.i64(*o5.stride()[:3]),
+        B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, 0.125, None, 0, None, 0, parts,
+        ws.data_ptr(), nbytes - 4, _lib.stream_of(qd))
+    assert rc == _lib.SA_ERR_INVALID

@@ -7,7 +7,6 @@ exp2 pass. Long key ranges with few query blocks take the key-range split. The b
 attention bar of test_gpu_attention.py (max-abs 2e-2, mean-abs 2e-3 and the reference's
 allclose(1e-2, 1e-2) against the oracle on the same 16-bit inputs).
 """
-import ctypes
 import math
 import random
 
@@ -16,7 +15,6 @@ import torch
 
 from conftest import case
 from oracle.attention import masked_attention
-from sparseattnfunctions_amd import _lib
 from sparseattnfunctions_amd._kv import kv_list_from_mask
 from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention
 
@@ -41,9 +39,8 @@ def _draw(seed):
 
 
 def _parts(n_items, max_cnt, D):
-    p = ctypes.c_int(0)
-    _lib.check(_lib.load().sa_attn_split_parts(n_items, max_cnt, D, ctypes.byref(p)), "sa_attn_split_parts")
-    return p.value
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import split_parts
+    return split_parts(n_items, max_cnt, D)
 
 
 @pytest.mark.parametrize("seed", range(24))
