@@ -386,8 +386,8 @@ int check_bf16_rows(const void* p, const int64_t s[3], const char* fn) {
 // constrained_mod_factor (partern_attention.py:262-315) on a standalone factor tensor
 // x [BH][L] fp32. modfac_stats_kernel: one workgroup per head, fixed-order sum (thread t adds
 // entries t, t + 256, ... in order, then a tree over the 256 partials), min and max.
-// modfac_apply_kernel: the "any head out of range" decision from every head's statistics,
-// then per element the affine map of [min, max] onto [max(min, lo), min(max, hi)], the
+// modfac_apply_kernel: the "any head out of range" decision from every head's statistics
+// (once per workgroup of 2048 elements), then per element the affine map of [min, max] onto [max(min, lo), min(max, hi)], the
 // rescale to the original sum (the mapped sum in closed form, (sum - L min) / range *
 // (tmax - tmin) + L tmin), heads with range < 1e-6 unchanged, and the clamp to [lo, hi].
 struct ModStatsArgs {
@@ -434,27 +434,33 @@ struct ModApplyArgs {
   float* out;
 };
 
+constexpr int kModApplyPerBlock = 2048;  // elements per workgroup of modfac_apply_kernel
+
 __global__ __launch_bounds__(256) void modfac_apply_kernel(ModApplyArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)a.BH * a.L) return;
-  bool need = false;
-  for (int h = 0; h < a.BH; ++h) need |= a.stats[h * 3 + 1] < a.lo || a.stats[h * 3 + 2] > a.hi;
-  const float v = a.x[i];
-  if (!need) {
-    a.out[i] = v;
-    return;
+  // The cross-head decision, once per workgroup: threads share the heads, then one barrier OR.
+  bool any = false;
+  for (int h = threadIdx.x; h < a.BH; h += 256) any |= a.stats[h * 3 + 1] < a.lo || a.stats[h * 3 + 2] > a.hi;
+  const bool need = __syncthreads_or(any);
+  const int64_t n_all = (int64_t)a.BH * a.L;
+  const int64_t i0 = (int64_t)blockIdx.x * kModApplyPerBlock + threadIdx.x;
+  for (int64_t i = i0; i < min(n_all, (int64_t)(blockIdx.x + 1) * kModApplyPerBlock); i += 256) {
+    const float v = a.x[i];
+    if (!need) {
+      a.out[i] = v;
+      continue;
+    }
+    const int64_t bh = i / a.L;
+    const float sum = a.stats[bh * 3 + 0], cmin = a.stats[bh * 3 + 1], cmax = a.stats[bh * 3 + 2];
+    const float tmin = cmin < a.lo ? a.lo : cmin;
+    const float tmax = cmax > a.hi ? a.hi : cmax;
+    const bool flat = (cmax - cmin) < 1e-6f;
+    const float rng = flat ? 1.f : cmax - cmin;
+    const float n = (float)a.L;
+    const float new_sum = (sum - n * cmin) / rng * (tmax - tmin) + n * tmin;
+    const float scaled = (v - cmin) / rng * (tmax - tmin) + tmin;
+    const float f = flat ? v : scaled * (sum / new_sum);
+    a.out[i] = fminf(fmaxf(f, a.lo), a.hi);
   }
-  const int64_t bh = i / a.L;
-  const float sum = a.stats[bh * 3 + 0], cmin = a.stats[bh * 3 + 1], cmax = a.stats[bh * 3 + 2];
-  const float tmin = cmin < a.lo ? a.lo : cmin;
-  const float tmax = cmax > a.hi ? a.hi : cmax;
-  const bool flat = (cmax - cmin) < 1e-6f;
-  const float rng = flat ? 1.f : cmax - cmin;
-  const float n = (float)a.L;
-  const float new_sum = (sum - n * cmin) / rng * (tmax - tmin) + n * tmin;
-  const float scaled = (v - cmin) / rng * (tmax - tmin) + tmin;
-  const float f = flat ? v : scaled * (sum / new_sum);
-  a.out[i] = fminf(fmaxf(f, a.lo), a.hi);
 }
 }  // namespace
 
@@ -470,8 +476,9 @@ extern "C" int sa_constrained_mod_factor(const float* x, int BH, int64_t L, floa
   if (int rc = sa::check_launch(fn)) return rc;
   ModApplyArgs aa{x, stats, BH, L, lo, hi, out};
   const int64_t n = (int64_t)BH * L;
-  SA_REQUIRE((n + 255) / 256 < (1LL << 31), "%s: grid too large", fn);
-  hipLaunchKernelGGL(modfac_apply_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, aa);
+  const int64_t blocks = (n + kModApplyPerBlock - 1) / kModApplyPerBlock;
+  SA_REQUIRE(blocks < (1LL << 31), "%s: grid too large", fn);
+  hipLaunchKernelGGL(modfac_apply_kernel, dim3((unsigned)blocks), dim3(256), 0, s, aa);
   return sa::check_launch(fn);
 }
 

@@ -174,10 +174,12 @@ class ParternAttentionColVersion_V2:
         # priority) so that they run alongside the compute-bound launches below; joined before
         # the final mix.
         main = torch.cuda.current_stream(dev)
+        # Every cached list the side stream reads is built (on a first call: by kernels on the
+        # main stream) before the side stream waits for the main one.
         text_kv = _dense(B, H, F * S, T, dev)
+        text_rows_kv = _dense(B, H, T, L, dev)
         side = _side_stream(dev) if OVERLAP_TEXT else main
         side.wait_stream(main)
-        text_rows_kv = _dense(B, H, T, L, dev)
         with torch.cuda.stream(side):
             o_text = block_sparse_attention(q[:, :, T:], k[:, :, :T], v[:, :, :T], text_kv, scale_factor)
             # Text rows over every key (the reference's SDPA, :442).
@@ -259,7 +261,10 @@ def constrained_mod_factor(modify_factor, min_threshold=0.01, max_threshold=50.0
     """partern_attention.py:262-315 on the GPU (`sa_constrained_mod_factor`): modify_factor
     [B, H, L, 1] fp32 (other float dtypes are converted); unchanged when every head lies within
     [min_threshold, max_threshold], else each head is mapped affinely onto the clipped range,
-    rescaled to its original sum and clamped. Returns fp32 of the input's shape."""
+    rescaled to its original sum and clamped. Computed in fp32 and returned in the input's
+    dtype and shape. Where the reference returns `modify_factor` itself (no head out of range)
+    this returns a new tensor of equal values: the decision stays on the GPU, with no host
+    synchronisation."""
     _lib.require_gpu(modify_factor)
     if modify_factor.dim() != 4 or modify_factor.shape[-1] != 1:
         raise ValueError(f"modify_factor must be [B, H, L, 1], got {tuple(modify_factor.shape)}")
@@ -271,7 +276,7 @@ def constrained_mod_factor(modify_factor, min_threshold=0.01, max_threshold=50.0
         _lib.check(_lib.load().sa_constrained_mod_factor(x.data_ptr(), B * H, L, float(min_threshold),
                                                          float(max_threshold), stats.data_ptr(), out.data_ptr(),
                                                          _lib.stream_of(x)), "sa_constrained_mod_factor")
-    return out
+    return out if modify_factor.dtype == torch.float32 else out.to(modify_factor.dtype)
 
 
 def get_softmax(q, k):

@@ -85,6 +85,30 @@ def test_forward_head_slices_and_streams_agree(dev):
     assert torch.equal(other, whole)
 
 
+def test_forward_first_call_streams_agree(dev):
+    # On a first call the cached kv lists are built by kernels on the main stream; the side
+    # stream's text and video-to-text rows must see them. Each call starts from an empty cache.
+    case("pattern forward: first call with an empty list cache, one or two streams")
+    from sparseattnfunctions_amd.utils import block_sparse_attn_kernel as bsak
+    q, k, v = _inputs(5, B=1, H=6)
+    _, idx = pa.get_indexs(G)
+    proc = pa.ParternAttentionColVersion_V2(G)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    outs = []
+    saved = pa.OVERLAP_TEXT
+    try:
+        for overlap in (True, False, True):
+            pa.OVERLAP_TEXT = overlap
+            pa._CACHE.clear()
+            bsak._ORDER_CACHE.clear()
+            outs.append(proc(qd, kd, vd, index_k=idx))
+    finally:
+        pa.OVERLAP_TEXT = saved
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(outs[2], outs[1])
+
+
 def _directed(a=2.5):
     # Frame f's queries boost the keys of frame f+1 and carry a per-frame slope g_f on a
     # position channel (first-frame rows also a per-row text component); v is one direction
@@ -261,6 +285,18 @@ def test_constrained_mod_factor_matches_oracle(dev):
     want = opat.constrained_mod_factor(x.double(), 0.05, 100.0)
     assert torch.allclose(got, want, rtol=2e-5, atol=1e-6), (got - want).abs().max()
     assert torch.equal(got[1, 7], torch.full_like(got[1, 7], 0.5))
+    # more heads than a workgroup's threads, the only out-of-range head past the first 256
+    x = torch.rand(2, 200, 300, 1, generator=g) + 0.5
+    assert torch.equal(constrained_mod_factor(x.to(dev), 0.01, 50.0).cpu(), x)
+    x[1, 190, 7] = 0.001
+    got = constrained_mod_factor(x.to(dev), 0.01, 50.0).cpu().double()
+    want = opat.constrained_mod_factor(x.double(), 0.01, 50.0)
+    assert torch.allclose(got, want, rtol=2e-5, atol=1e-6), (got - want).abs().max()
+    assert got[1, 190].min().item() == torch.tensor(0.01).item()  # remapped and clamped to fp32(0.01)
+    # other float dtypes come back in their own dtype (equal values when nothing changes)
+    xb = (torch.rand(1, 4, 700, 1, generator=g) + 0.5).bfloat16()
+    yb = constrained_mod_factor(xb.to(dev), 0.01, 50.0)
+    assert yb.dtype == torch.bfloat16 and torch.equal(yb.cpu(), xb)
 
 
 def test_get_softmax_probabilities(dev):
