@@ -11,9 +11,11 @@ Matching, merge/unmerge and the biased attention are HIP kernels (`sa_tome_*`,
 `sa_block_sparse_fwd` with every key block and a key bias).
 
 Default `merge_config` is BASELINE config 4: head-averaged k metric (metric="head_mean_k"),
-2x2 spatial stride, no temporal stride, r = 4000, full merge. The reference's own setting
-(metric cat(k, |k|, v, |v|) per head, 3x3x4 stride, r = 9000, k/v-only merge) is
-`MergeAttention(REFERENCE_MERGE_CONFIG, full_merge=False, metric="kv_norm")`.
+2x2 spatial stride, no temporal stride, r = 4000, full merge, the top-left token of each
+cell as its dst (no_rand=True). The reference's own setting (metric cat(k, |k|, v, |v|) per
+head, 3x3x4 stride, r = 9000, k/v-only merge, a random dst per cell drawn at every re-match
+from a generator made at construction, :16-20, :30) is `MergeAttention.reference()`, i.e.
+`MergeAttention(REFERENCE_MERGE_CONFIG, full_merge=False, metric="kv_norm", no_rand=False)`.
 """
 from __future__ import annotations
 
@@ -24,6 +26,7 @@ import torch
 from . import _tome
 from .block_mask_attn import dense_kv_list
 from .utils.block_sparse_attn_kernel import block_sparse_attention
+from .utils.merge_unmerge import draw_cell_choice, init_generator
 
 CONFIG4_MERGE_CONFIG = {"w": 45, "h": 30, "t": 13, "sx": 2, "sy": 2, "st": 1, "r": 4000}
 REFERENCE_MERGE_CONFIG = {"w": 45, "h": 30, "t": 13, "sx": 3, "sy": 3, "st": 4, "r": 9000}
@@ -39,7 +42,8 @@ def _global_count():
 
 class MergeAttention:
     def __init__(self, merge_config=None, full_merge: bool = True, gap: int = 1, metric: str = "head_mean_k",
-                 text_len: int = 226, sm_scale: float = None):
+                 text_len: int = 226, sm_scale: float = None, no_rand: bool = True,
+                 generator: torch.Generator = None):
         if metric not in ("head_mean_k", "kv_norm"):
             raise ValueError("metric must be 'head_mean_k' or 'kv_norm'")
         self.merge_config = dict(merge_config or CONFIG4_MERGE_CONFIG)
@@ -48,9 +52,23 @@ class MergeAttention:
         self.metric = metric
         self.text_len = text_len
         self.sm_scale = sm_scale
+        self.no_rand = no_rand
+        # The reference seeds its generator from the global RNG of the GPU (the CPU without
+        # one) when the processor is built (:19, merge_unmerge.py:8-22).
+        if generator is None and not no_rand:
+            generator = init_generator(torch.device("cuda" if torch.cuda.is_available() else "cpu"))
+        self.generator = generator
+        self.cell_choice = None  # dst offsets of the last re-match (None: top-left)
         self.maps = None
         self.calls = 0
         self._kv_cache = {}
+
+    @classmethod
+    def reference(cls, **kwargs):
+        """The reference's configuration (MergeAttention.py:16-48)."""
+        args = dict(merge_config=REFERENCE_MERGE_CONFIG, full_merge=False, metric="kv_norm", no_rand=False)
+        args.update(kwargs)
+        return cls(**args)
 
     def _count(self):
         c = _global_count()
@@ -60,7 +78,12 @@ class MergeAttention:
         cfg = self.merge_config
         mode = 0 if self.metric == "head_mean_k" else 1
         metric = _tome.metric_from_qkv(k, v if mode == 1 else None, self.text_len, mode)
-        a_idx, b_idx = _tome.partition(cfg["t"], cfg["h"], cfg["w"], cfg["sx"], cfg["sy"], cfg["st"], k.device)
+        # One dst per cell: the top-left token, or a draw from the generator at every re-match
+        # (merge_unmerge.py:66-70).
+        self.cell_choice = None if self.no_rand else draw_cell_choice(
+            cfg["t"], cfg["h"], cfg["w"], cfg["sx"], cfg["sy"], cfg["st"], self.generator)
+        a_idx, b_idx = _tome.partition(cfg["t"], cfg["h"], cfg["w"], cfg["sx"], cfg["sy"], cfg["st"], k.device,
+                                       cell_choice=self.cell_choice)
         return _tome.match(metric, a_idx, b_idx, cfg["r"], self.text_len)
 
     def _heads_per_group(self, H):

@@ -140,19 +140,38 @@ def match(metric: torch.Tensor, a_idx: torch.Tensor, b_idx: torch.Tensor, r: int
     return maps
 
 
+# Device index -> event recorded on the stream of the last sa_tome_match_noalloc call.
+_NOALLOC_LAST = {}
+
+
 def match_noalloc(metric: torch.Tensor, a_idx: torch.Tensor, b_idx: torch.Tensor, r: int, text_len: int) -> TomeMaps:
     """match() through `sa_tome_match_noalloc`: the library allocates nothing and no workspace
     is passed (its partials live in a fixed 16 MiB device array per GPU; larger problems raise
-    ValueError). The maps themselves are caller buffers, allocated here."""
+    ValueError). The maps themselves are caller buffers, allocated here.
+
+    Calls on one GPU share that array, so their kernels must not overlap. Calls from this
+    function are ordered: each call's stream waits for an event recorded after the previous
+    call on the same GPU (whatever its stream). Under graph capture no event is waited for or
+    recorded (the capture's own stream order applies)."""
     _lib.require_gpu(metric, a_idx, b_idx)
     G, N, C = metric.shape
     r = max(0, min(int(r), a_idx.numel()))
     maps = TomeMaps(G, N, text_len, a_idx, b_idx, r, metric.device)
     metric = metric.contiguous()
-    with torch.cuda.device(metric.device):
-        rc = _lib.load().sa_tome_match_noalloc(metric.data_ptr(), C, ctypes.byref(maps.struct),
-                                               _lib.stream_of(metric))
+    dev = metric.device
+    stream = torch.cuda.current_stream(dev)
+    capturing = torch.cuda.is_current_stream_capturing()
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    prev = _NOALLOC_LAST.get(key)
+    if prev is not None and not capturing:
+        stream.wait_event(prev)
+    with torch.cuda.device(dev):
+        rc = _lib.load().sa_tome_match_noalloc(metric.data_ptr(), C, ctypes.byref(maps.struct), stream.cuda_stream)
     _lib.check(rc, "sa_tome_match_noalloc")
+    if not capturing:
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        _NOALLOC_LAST[key] = ev
     return maps
 
 

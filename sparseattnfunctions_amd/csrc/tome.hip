@@ -764,7 +764,9 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
     a.n_src = m.n_src; a.n_dst = m.n_dst; a.splits = splits;
     a.dst_per_split = match_tiles_per_split(m.n_dst) * kMTile;
     a.part_max = part_max; a.part_idx = part_idx;
-    if (C == kMfC)
+    // match_mfma_kernel stages dst rows with 16-byte loads; a metric base that is not 16-byte
+    // aligned takes match_kernel (scalar metric loads, the same fixed-order sums and maps).
+    if (C == kMfC && reinterpret_cast<uintptr_t>(metric) % 16 == 0)
       hipLaunchKernelGGL(match_mfma_kernel, dim3((m.n_src + kMfSrc - 1) / kMfSrc, m.G, splits), dim3(256), 0, s, a);
     else
       hipLaunchKernelGGL(match_kernel, dim3((m.n_src + kMTile - 1) / kMTile, m.G, splits), dim3(256), 0, s, a);

@@ -42,6 +42,16 @@ def init_generator(device: torch.device, fallback: torch.Generator = None):
     return init_generator(torch.device("cpu")) if fallback is None else fallback
 
 
+def draw_cell_choice(t: int, h: int, w: int, sx: int, sy: int, st: int, generator: torch.Generator = None):
+    """The dst offset of each (st, sy, sx) cell of frames 1..t-1, drawn as the reference draws
+    it (merge_unmerge.py:69: `torch.randint(sy*sx*st, (tst, hsy, wsx, 1))` on the generator's
+    device, the same values in the same order); int32 [tst, hsy, wsx] on the CPU."""
+    tst, hsy, wsx = (t - 1) // st, h // sy, w // sx
+    dev = generator.device if generator is not None else torch.device("cpu")
+    return torch.randint(sy * sx * st, size=(tst, hsy, wsx, 1), device=dev, generator=generator).reshape(
+        tst, hsy, wsx).to(device="cpu", dtype=torch.int32)
+
+
 def bipartite_soft_matching_video(metric: torch.Tensor, w: int, h: int, t: int, sx: int, sy: int, st: int, r: int,
                                   no_rand: bool = False, generator: torch.Generator = None,
                                   text_len: int = 226) -> Tuple[Callable, Callable]:
@@ -51,11 +61,7 @@ def bipartite_soft_matching_video(metric: torch.Tensor, w: int, h: int, t: int, 
         return do_nothing, do_nothing
     if N != t * h * w:
         raise ValueError(f"metric has {N} tokens, expected t*h*w = {t * h * w}")
-    choice = None
-    if not no_rand:
-        tst, hsy, wsx = (t - 1) // st, h // sy, w // sx
-        dev = generator.device if generator is not None else torch.device("cpu")
-        choice = torch.randint(sy * sx * st, size=(tst, hsy, wsx), device=dev, generator=generator).cpu()
+    choice = None if no_rand else draw_cell_choice(t, h, w, sx, sy, st, generator)
     a_idx, b_idx = _tome.partition(t, h, w, sx, sy, st, metric.device, cell_choice=choice)
     maps = _tome.match(_tome.normalize(metric), a_idx, b_idx, r, text_len)
     counter = maps.sizes.to(torch.int64).reshape(G, maps.n_dst, 1)

@@ -2,10 +2,12 @@
 the C oracle; MergeAttention outputs within the bf16 tolerances of the fp64 oracle."""
 import math
 
+import numpy as np
 import pytest
 import torch
 
 from conftest import case
+from tome_adversarial import adversarial_metric
 from oracle import native
 from oracle.attention import masked_attention
 from sparseattnfunctions_amd import _tome
@@ -66,6 +68,57 @@ def test_small_pipeline_bit_exact(dev, mode):
             assert torch.equal(_tome.unmerge(xm, maps, hpg).cpu(), native.tome_unmerge(xm.cpu(), want, hpg))
 
 
+def _misaligned(x):
+    """A copy of x whose base is 4 bytes past a 16-byte boundary (contiguous)."""
+    buf = torch.empty(x.numel() + 4, dtype=x.dtype, device=x.device)
+    y = buf[1: 1 + x.numel()].view(x.shape)
+    y.copy_(x)
+    assert y.is_contiguous() and y.data_ptr() % 16 == 4
+    return y
+
+
+@pytest.mark.parametrize("kind", ["exponents", "subnormal", "cancel", "ties"])
+def test_match_kernels_adversarial_bit_exact(dev, kind):
+    # The 64-channel matching runs on the matrix cores on the assumption that
+    # v_mfma_f32_16x16x4_f32 adds its four products to the accumulator as an in-order fmaf
+    # chain. On metrics built to separate summation orders, the MFMA path (aligned metric), the
+    # VALU match_kernel (the same metric at a base that is not 16-byte aligned) and the C
+    # oracle's fmaf chain must give the same maps bit for bit, scores included.
+    geom = Geometry(text_len=226, T=6, Hp=12, Wp=20)
+    G, N = 2, geom.n_video
+    case(f"tome match adversarial metric: {kind}")
+    a, b = _tome.partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1, dev)
+    oa, ob = native.tome_partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1)
+    x = adversarial_metric(kind, a, b, G, N)
+    assert torch.isfinite(x).all()
+    r = oa.numel()
+    want = native.tome_match(x, oa, ob, r, geom.text_len)
+    md = x.to(dev)
+    assert md.data_ptr() % 16 == 0
+    mfma = _tome.match(md, a, b, r, geom.text_len)
+    valu = _tome.match(_misaligned(md), a, b, r, geom.text_len)
+    torch.cuda.synchronize()
+    _maps_equal(valu, want)
+    _maps_equal(mfma, want)
+    if kind == "subnormal":
+        nm = want["node_max"].abs()
+        assert ((nm > 0) & (nm < 2.0 ** -126)).any()  # subnormal scores were compared
+
+
+def test_match_misaligned_metric(dev):
+    # A metric whose base is not 16-byte aligned gives the same maps (C4-sized head-sum metric).
+    case("tome match misaligned metric")
+    geom = Geometry()
+    _, k, _ = cogvideox_qkv(8, B=2, H=4, geom=geom)
+    metric = _tome.metric_from_qkv(k.to(dev), None, geom.text_len, 0)
+    a, b = _tome.partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1, dev)
+    want = _tome.match(metric, a, b, 4000, geom.text_len)
+    got = _tome.match(_misaligned(metric), a, b, 4000, geom.text_len)
+    torch.cuda.synchronize()
+    for f in ("node_idx", "node_max", "edge", "dst_idx", "dst_cnt", "row_of_token", "key_bias"):
+        assert torch.equal(getattr(got, f), getattr(want, f)), f
+
+
 @pytest.fixture(scope="module")
 def c4_oracle():
     """Config 4 inputs (seed 3) and every matching map computed by the C oracle alone: the
@@ -120,6 +173,23 @@ def test_merge_attention_config4(dev, c4_oracle):
                               1 / 8, key_bias=bias)
         want = native.tome_unmerge(om, sub, 1)[0, 0]
         _check(out[bb, hh], want)
+    # Every (b, h): its text rows, 32 random video rows and the last row, each through the
+    # merged row it is unmerged from, against the fp64 oracle on the oracle's merged tensors.
+    g = torch.Generator().manual_seed(4)
+    L = q.shape[2]
+    for bb in range(q.shape[0]):
+        sub = {f: t[bb:bb + 1] for f, t in want_maps.items()}
+        bias = sub["key_bias"].reshape(1, 1, -1).double()
+        rot = sub["row_of_token"][0].long()
+        for hh in range(q.shape[1]):
+            sel = lambda x: x[bb:bb + 1, hh:hh + 1]
+            qm, km, vm = (native.tome_merge(sel(x), sub, a, b, 4000, 226, 1) for x in (q, k, v))
+            rows = torch.unique(torch.cat([torch.arange(226), torch.randint(226, L, (32,), generator=g),
+                                           torch.tensor([L - 1])]))
+            mrows, inv = torch.unique(rot[rows], return_inverse=True)
+            om = masked_attention(qm, km, vm, torch.ones(1, 1, 1, 1, dtype=torch.bool).expand(1, 1, 216, 216),
+                                  1 / 8, key_bias=bias, rows=mrows)[0, 0]
+            _check(out[bb, hh, rows], om[inv])
 
 
 def test_merge_attention_reference_setting(dev):
@@ -147,6 +217,40 @@ def test_merge_attention_reference_setting(dev):
     proc.gap = 2
     proc(q.to(dev), k.to(dev), v.to(dev))
     assert proc.maps is not maps or proc.calls % 2 == 0
+
+
+def test_merge_attention_random_dst_choice(dev):
+    # The reference draws one dst per (st, sy, sx) cell from the processor's generator at every
+    # re-match (MergeAttention.py:20, :30; merge_unmerge.py:66-70). The partition follows the
+    # reference's steps (test_oracle_tome's numpy restatement) on the same draws, the maps
+    # match the C oracle on that partition, and the next re-match draws again.
+    from test_oracle_tome import _reference_partition
+    case("MergeAttention reference setting, generator-driven dst choice")
+    geom = Geometry(text_len=226, T=5, Hp=6, Wp=9)
+    q, k, v = cogvideox_qkv(9, B=2, H=2, geom=geom)
+    cfg = dict(REFERENCE_MERGE_CONFIG, w=9, h=6, t=5, r=60)
+    proc = MergeAttention.reference(merge_config=cfg, generator=torch.Generator(device=dev).manual_seed(7))
+    assert (proc.full_merge, proc.metric, proc.no_rand) == (False, "kv_norm", False)
+    twin = torch.Generator(device=dev).manual_seed(7)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    seen = []
+    for call in range(3):
+        proc(qd, kd, vd)
+        draws = torch.randint(3 * 3 * 4, size=((5 - 1) // 4, 6 // 3, 9 // 3, 1), device=dev, generator=twin)
+        choice = draws.cpu().reshape(-1)
+        assert torch.equal(proc.cell_choice.reshape(-1).long(), choice)
+        ra, rb = _reference_partition(5, 6, 9, 3, 3, 4, choice)
+        maps = proc.maps
+        assert np.array_equal(maps.a_idx.cpu().numpy(), ra) and np.array_equal(maps.b_idx.cpu().numpy(), rb)
+        want = native.tome_match(native.tome_metric(k, v, 226, 1), maps.a_idx.cpu(), maps.b_idx.cpu(), 60, 226)
+        _maps_equal(maps, want)
+        seen.append(tuple(choice.tolist()))
+    assert len(set(seen)) > 1  # each re-match draws anew
+    # no_rand keeps the top-left token of every cell
+    top = MergeAttention(cfg, full_merge=False, metric="kv_norm")
+    top(qd, kd, vd)
+    ra, rb = _reference_partition(5, 6, 9, 3, 3, 4)
+    assert top.cell_choice is None and np.array_equal(top.maps.b_idx.cpu().numpy(), rb)
 
 
 def test_reference_api_closures(dev):

@@ -148,3 +148,79 @@ def test_library_partition_matches_oracle():
         a, b = _tome.partition(*geo, device="cpu")
         oa, ob = native.tome_partition(*geo)
         assert torch.equal(a, oa) and torch.equal(b, ob)
+
+
+def _chain_node_max(metric, a_idx, b_idx, order, ftz=False):
+    """Best score per src with the C channels added in `order` (fp64 product and sum, rounded
+    to fp32 after each step: an fmaf chain up to rare double roundings). `ftz` flushes
+    subnormal fp32 results to zero after each step."""
+    out = []
+    for gi in range(metric.shape[0]):
+        A = metric[gi, a_idx.long()].numpy().astype(np.float64)
+        B = metric[gi, b_idx.long()].numpy().astype(np.float64)
+        acc = np.zeros((A.shape[0], B.shape[0]), dtype=np.float32)
+        for c in order:
+            acc = (acc.astype(np.float64) + A[:, c:c + 1] * B[None, :, c]).astype(np.float32)
+            if ftz:
+                acc[np.abs(acc) < np.float32(2.0 ** -126)] = 0
+        out.append(acc.max(-1))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("kind", ["exponents", "cancel"])
+def test_adversarial_metrics_separate_summation_orders(kind):
+    # The metrics of the GPU test of the matching kernels can tell an in-order fmaf chain over
+    # the channels from the reverse order and from a four-wide interleaved order: the best
+    # score of some src differs between them.
+    from tome_adversarial import adversarial_metric
+    T, Hp, Wp = 6, 12, 20
+    a, b = native.tome_partition(T, Hp, Wp, 2, 2, 1)
+    x = adversarial_metric(kind, a, b, 2, T * Hp * Wp)
+    assert torch.isfinite(x).all()
+    maps = native.tome_match(x, a, b, a.numel(), 226)
+    fwd = _chain_node_max(x, a, b, range(64))
+    # the emulation follows the oracle's in-order chain
+    assert (fwd == maps["node_max"].numpy()).mean() > 0.99
+    rev = _chain_node_max(x, a, b, range(63, -1, -1))
+    assert (rev != maps["node_max"].numpy()).mean() > 0.01
+    # four interleaved chains over channels c = 4j + i, then added in i order
+    g4 = _chain_node_max(x, a, b, [c for i in range(4) for c in range(i, 64, 4)])
+    assert (g4 != maps["node_max"].numpy()).mean() > 0.01
+
+
+def test_adversarial_subnormal_metric_needs_subnormals():
+    # In the subnormal metric most best scores are subnormal fp32 values (sums on the uniform
+    # 2^-149 grid, where the order of additions does not matter), and flushing subnormal
+    # results to zero at each step changes them: it tells a chain that keeps subnormals from
+    # one that flushes them.
+    from tome_adversarial import adversarial_metric
+    T, Hp, Wp = 6, 12, 20
+    a, b = native.tome_partition(T, Hp, Wp, 2, 2, 1)
+    x = adversarial_metric("subnormal", a, b, 2, T * Hp * Wp)
+    maps = native.tome_match(x, a, b, a.numel(), 226)
+    nm = maps["node_max"].abs()
+    assert ((nm > 0) & (nm < 2.0 ** -126)).float().mean() > 0.5
+    assert (_chain_node_max(x, a, b, range(64)) == maps["node_max"].numpy()).mean() > 0.99
+    ftz = _chain_node_max(x, a, b, range(64), ftz=True)
+    assert (ftz != maps["node_max"].numpy()).mean() > 0.5
+
+
+def test_adversarial_ties_are_ties():
+    # The ties metric has exactly equal best scores (small integers: exact sums) on several dst
+    # per src, and equal node_max across srcs; the oracle keeps the lower dst and src.
+    from tome_adversarial import adversarial_metric
+    T, Hp, Wp = 6, 12, 20
+    a, b = native.tome_partition(T, Hp, Wp, 2, 2, 1)
+    x = adversarial_metric("ties", a, b, 2, T * Hp * Wp)
+    maps = native.tome_match(x, a, b, a.numel(), 226)
+    for gi in range(2):
+        s = x[gi, a.long()].double() @ x[gi, b.long()].double().T
+        best = s.max(-1).values
+        n_best = (s == best[:, None]).sum(-1)
+        assert (n_best > 1).sum() > 50
+        first = (s == best[:, None]).float().argmax(-1)
+        assert torch.equal(maps["node_idx"][gi].long(), first)
+        assert torch.equal(maps["node_max"][gi].double(), best)
+        nm = maps["node_max"][gi].numpy()
+        assert len(np.unique(nm)) < nm.size // 2
+        assert np.array_equal(maps["edge"][gi].numpy(), np.argsort(-nm, kind="stable"))

@@ -64,3 +64,28 @@ def test_match_noalloc_rejects_oversized(dev):
     assert b"scratch" in _lib.load().sa_last_error()
     with pytest.raises(ValueError):
         _tome.match_noalloc(metric, a, b, 4000, geom.text_len)
+
+
+def test_match_noalloc_calls_on_two_streams(dev):
+    # Calls on one GPU share its scratch array; match_noalloc orders its calls across streams
+    # (each waits for an event after the previous call), so two calls issued back to back on
+    # two streams, with no synchronisation between them, both give the workspace entry's maps.
+    case("tome match noalloc on two streams")
+    geom = Geometry(T=6, Hp=12, Wp=20)
+    a, b = _tome.partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1, dev)
+    metrics, wants = [], []
+    for seed in (11, 12):
+        _, k, _ = cogvideox_qkv(seed, B=2, H=4, geom=geom)
+        m = _tome.metric_from_qkv(k.to(dev), None, geom.text_len, 0)
+        metrics.append(m)
+        wants.append(_tome.match(m, a, b, 300, geom.text_len))
+    main = torch.cuda.current_stream(dev)
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    got = []
+    for s, m in zip(streams, metrics):
+        s.wait_stream(main)
+        with torch.cuda.stream(s):
+            got.append(_tome.match_noalloc(m, a, b, 300, geom.text_len))
+    torch.cuda.synchronize()
+    for g, w in zip(got, wants):
+        _same(g, w)
