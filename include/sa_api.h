@@ -121,7 +121,7 @@ int sa_block_sparse_fwd_v32(const uint16_t* q, const int64_t q_strides[3], const
 /*
  * sa_block_sparse_fwd for fp32 q, k, v and out (the reference kernel also runs on fp32 tiles,
  * :52-209, with P cast to v's dtype, :107, so kept in fp32): same arguments and list contract,
- * head dim 64, key_bias must be NULL (SA_ERR_UNSUPPORTED otherwise). fp32 MFMA
+ * head dim 64 or 128 (:231), key_bias must be NULL (SA_ERR_UNSUPPORTED otherwise). fp32 MFMA
  * (v_mfma_f32_16x16x4_f32), running row maximum, P and row sums in fp32. Strides in elements,
  * multiples of 4; bases 16-byte aligned.
  */
@@ -212,6 +212,22 @@ int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         int D, int causal, float sm_scale, int block_size, float* po,
                         const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
                         void* stream);
+
+/*
+ * sa_attn_pooling_fwd for fp32 q, k, v and out, in fp32 arithmetic as the reference computes
+ * (:230-240 casts bf16 inputs to fp32 and runs the kernel on fp32 tiles, P kept in fp32):
+ * the attention of sa_block_sparse_fwd_f32 (fp32 MFMA, running row maximum) over every key
+ * block (causal: up to the diagonal, the diagonal tile masked to keys <= query), grouped key
+ * heads as there; the rows' column maxima and log-sum-exps go to the workspace and a reduce
+ * kernel forms Po for every block size. D = 64 or 128; same workspace
+ * (sa_attn_pooling_workspace), strides in elements, multiples of 4.
+ */
+int sa_attn_pooling_fwd_f32(const float* q, const int64_t q_strides[3], const float* k,
+                            const int64_t k_strides[3], const float* v, const int64_t v_strides[3],
+                            float* out, const int64_t out_strides[3], int B, int H, int H_kv, int L,
+                            int D, int causal, float sm_scale, int block_size, float* po,
+                            const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                            void* stream);
 
 /*
  * sa_attn_pooling_fwd for fp16 q, k, v and out (the reference also takes fp16, :230-289):

@@ -88,6 +88,11 @@ _PROTOTYPES = {
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,
          ctypes.c_int64, _P],
     ),
+    "sa_attn_pooling_fwd_f32": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,
+         ctypes.c_int64, _P],
+    ),
     "sa_attn_pooling_fwd_f16": (
         _I,
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _I, _F, _I, _P, _I64P, _P,

@@ -1382,6 +1382,20 @@ extern "C" int sa_attn_pooling_workspace(int B, int H, int L, int block_size, in
 
 namespace {
 
+// Po from the stored row maxima and log-sum-exps (pool_reduce_kernel).
+int launch_pool_reduce(const PoolLayout& p, const float* r, const float* lse, int B, int H, int L, int block_size,
+                       int causal, float* po, const int64_t po_strides[3], hipStream_t s, const char* fn) {
+  const int nd = sa::cdiv(L, block_size);
+  PoolReduceArgs ra;
+  ra.r = r; ra.nqb = p.nqb; ra.ncol_alloc = p.ncol_alloc; ra.lpad = p.lpad; ra.lse = lse;
+  ra.L = L; ra.bs = block_size; ra.G = p.G; ra.nd = nd; ra.ncol = sa::cdiv(L, p.G); ra.causal = causal ? 1 : 0;
+  ra.H = H; ra.po = po; ra.po_sb = po_strides[0]; ra.po_sh = po_strides[1]; ra.po_si = po_strides[2];
+  ra.total = (int64_t)B * H * nd;
+  SA_REQUIRE(ra.total < (1LL << 31), "%s: grid too large", fn);
+  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)ra.total), dim3(256), (unsigned)(nd * sizeof(float)), s, ra);
+  return sa::check_launch(fn);
+}
+
 int attn_pooling(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3],
                  const uint16_t* v, const int64_t v_strides[3], uint16_t* out, const int64_t out_strides[3], int B,
                  int H, int H_kv, int L, int D, int causal, float sm_scale, int block_size, float* po,
@@ -1425,14 +1439,45 @@ int attn_pooling(const uint16_t* q, const int64_t q_strides[3], const uint16_t* 
                           sm_scale, nullptr, 0, nullptr, 0, nullptr, 0, stream, fn, H / H_kv, p.G, r, lse, nullptr,
                           fp16))
     return rc;
-  PoolReduceArgs ra;
-  ra.r = r; ra.nqb = p.nqb; ra.ncol_alloc = p.ncol_alloc; ra.lpad = p.lpad; ra.lse = lse;
-  ra.L = L; ra.bs = block_size; ra.G = p.G; ra.nd = nd; ra.ncol = sa::cdiv(L, p.G); ra.causal = la.causal;
-  ra.H = H; ra.po = po; ra.po_sb = po_strides[0]; ra.po_sh = po_strides[1]; ra.po_si = po_strides[2];
-  ra.total = (int64_t)B * H * nd;
-  SA_REQUIRE(ra.total < (1LL << 31), "%s: grid too large", fn);
-  hipLaunchKernelGGL(pool_reduce_kernel, dim3((unsigned)ra.total), dim3(256), (unsigned)(nd * sizeof(float)), s, ra);
-  return sa::check_launch(fn);
+  return launch_pool_reduce(p, r, lse, B, H, L, block_size, causal, po, po_strides, s, fn);
+}
+
+// fp32 q, k, v (the reference's own arithmetic for attn_with_pooling, which computes in fp32):
+// the fp32 kernel in pooling mode stores the row maxima and log-sum-exps, the reduce kernel
+// forms Po for every block size.
+int attn_pooling_f32(const float* q, const int64_t q_strides[3], const float* k, const int64_t k_strides[3],
+                     const float* v, const int64_t v_strides[3], float* out, const int64_t out_strides[3], int B,
+                     int H, int H_kv, int L, int D, int causal, float sm_scale, int block_size, float* po,
+                     const int64_t po_strides[3], void* workspace, int64_t workspace_bytes, void* stream,
+                     const char* fn) {
+  SA_REQUIRE(po && po_strides && workspace, "%s: null pointer", fn);
+  SA_REQUIRE(B > 0 && H > 0 && L > 0, "%s: bad shape B=%d H=%d L=%d", fn, B, H, L);
+  SA_REQUIRE(H_kv > 0 && H % H_kv == 0, "%s: H_kv=%d must divide H=%d", fn, H_kv, H);
+  SA_REQUIRE(block_size == 32 || block_size == 64 || block_size == 128, "%s: block_size %d not in {32, 64, 128}",
+             fn, block_size);
+  const PoolLayout p = pool_layout(B, H, L, block_size);
+  const int nd = sa::cdiv(L, block_size);
+  if (nd > kPoolMaxNd) return sa::fail(SA_ERR_UNSUPPORTED, "%s: %d blocks per row > %d", fn, nd, kPoolMaxNd);
+  SA_REQUIRE(workspace_bytes >= (int64_t)p.total, "%s: workspace of %lld bytes < %lld", fn,
+             (long long)workspace_bytes, (long long)p.total);
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s: workspace not 256-byte aligned", fn);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  PoolListArgs la;
+  la.idx = reinterpret_cast<int32_t*>(ws + p.idx);
+  la.cnt = reinterpret_cast<int32_t*>(ws + p.cnt);
+  la.slot = reinterpret_cast<int32_t*>(ws + p.slot);
+  la.mask = reinterpret_cast<uint64_t*>(ws + p.mask);
+  la.nqb = p.nqb; la.nkb = p.nkb; la.causal = causal ? 1 : 0;
+  hipStream_t s = sa::as_stream(stream);
+  const int64_t n_list = std::max<int64_t>((int64_t)p.nqb * p.nkb, kBlock);
+  hipLaunchKernelGGL(pool_lists_kernel, dim3((unsigned)((n_list + 255) / 256)), dim3(256), 0, s, la);
+  if (int rc = sa::check_launch(fn)) return rc;
+  float* r = reinterpret_cast<float*>(ws + p.r);
+  float* lse = reinterpret_cast<float*>(ws + p.lse);
+  if (int rc = sa::attn_f32_pooling(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, L, D, la.idx,
+                                    la.cnt, p.nkb, H / H_kv, causal != 0, sm_scale, p.G, r, lse, stream, fn))
+    return rc;
+  return launch_pool_reduce(p, r, lse, B, H, L, block_size, causal, po, po_strides, s, fn);
 }
 
 }  // namespace
@@ -1445,6 +1490,17 @@ extern "C" int sa_attn_pooling_fwd(const uint16_t* q, const int64_t q_strides[3]
                                    void* stream) {
   return attn_pooling(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, H_kv, L, D, causal, sm_scale,
                       block_size, po, po_strides, workspace, workspace_bytes, stream, false, "sa_attn_pooling_fwd");
+}
+
+extern "C" int sa_attn_pooling_fwd_f32(const float* q, const int64_t q_strides[3], const float* k,
+                                       const int64_t k_strides[3], const float* v, const int64_t v_strides[3],
+                                       float* out, const int64_t out_strides[3], int B, int H, int H_kv, int L, int D,
+                                       int causal, float sm_scale, int block_size, float* po,
+                                       const int64_t po_strides[3], void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  return attn_pooling_f32(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, H_kv, L, D, causal,
+                          sm_scale, block_size, po, po_strides, workspace, workspace_bytes, stream,
+                          "sa_attn_pooling_fwd_f32");
 }
 
 extern "C" int sa_attn_pooling_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,

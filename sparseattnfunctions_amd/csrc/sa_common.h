@@ -41,6 +41,13 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// fp32 attention in pooling mode (attn_f32.hip), for the pooled-map entry point.
+int attn_f32_pooling(const float* q, const int64_t q_strides[3], const float* k, const int64_t k_strides[3],
+                     const float* v, const int64_t v_strides[3], float* out, const int64_t out_strides[3], int B,
+                     int H, int L, int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt, int kv_rep,
+                     bool causal, float sm_scale, int pool_cols, float* pool_r, float* pool_lse, void* stream,
+                     const char* fn);
+
 }  // namespace sa
 
 #define SA_REQUIRE(cond, ...)                                   \

@@ -14,14 +14,17 @@ its rows: Po = max over the block's rows of exp2(R - lse), normalised. For block
 rows' log-sum-exps are stored too, and a reduce kernel does this over two waves' rows. The
 probability matrix itself is never written.
 
-q, k and v are bf16 or fp16 (one dtype), head_dim 64 or 128. Po is fp32 for bf16 inputs and
-fp16 for fp16 inputs, the dtypes the reference returns (it computes bf16 inputs in fp32 and
-fp16 inputs in fp16, storing Po in that dtype).
+q, k and v are bf16, fp16 or fp32 (one dtype), head_dim 64 or 128. Po is fp32 for bf16 and
+fp32 inputs and fp16 for fp16 inputs, the dtypes the reference returns (it computes bf16 inputs
+in fp32 and fp16 inputs in fp16, storing Po in that dtype).
 
-Differences from the reference: fp32 inputs raise TypeError (the reference also runs fp32;
-this build's fp32 attention kernel has no pooling mode); bf16 inputs are computed with bf16
-products where the reference casts them up to fp32 first. The rows of a last, partial query block that lie
-past L take no part in its maximum; the reference reads them without bounds checks.
+Arithmetic. fp32 inputs run the fp32 kernel (fp32 MFMA, P and row sums in fp32), as the
+reference does. bf16 and fp16 inputs run, by default, the 16-bit kernel: bf16 (fp16) products
+with fp32 accumulation and P rounded to the input dtype before P.V, where the reference casts
+bf16 inputs up to fp32 first (:235-240); `attn_with_pooling(..., precision="fp32")` does what
+the reference does (inputs cast to fp32, the fp32 kernel, the output cast back to the input
+dtype), at the fp32 MFMA rate (1/16 of bf16's). The rows of a last, partial query block that
+lie past L take no part in its maximum; the reference reads them without bounds checks.
 """
 from __future__ import annotations
 
@@ -39,13 +42,19 @@ class _attention_pooling(torch.autograd.Function):
     (:230-287); like the reference it has no backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, sm_scale, block_size):
+    def forward(ctx, q, k, v, causal, sm_scale, block_size, precision=None):
         assert block_size in {32, 64, 128}
-        half = (torch.bfloat16, torch.float16)
-        q, k, v = _prep_qkv(q, half), _prep_qkv(k, half), _prep_qkv(v, half)
+        if precision not in (None, "fp32"):
+            raise ValueError(f"precision must be None or 'fp32', got {precision!r}")
+        types = (torch.bfloat16, torch.float16, torch.float32)
+        q, k, v = _prep_qkv(q, types), _prep_qkv(k, types), _prep_qkv(v, types)
         if not q.dtype == k.dtype == v.dtype:
             raise TypeError(f"q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+        orig_dtype = q.dtype
+        if precision == "fp32" and q.dtype != torch.float32:
+            q, k, v = q.float(), k.float(), v.float()
         fp16 = q.dtype == torch.float16
+        fp32 = q.dtype == torch.float32
         _lib.require_gpu(q, k, v)
         B, H, L, D = q.shape
         Hk = k.shape[1]
@@ -61,17 +70,20 @@ class _attention_pooling(torch.autograd.Function):
         _lib.check(lib.sa_attn_pooling_workspace(B, H, L, block_size, ctypes.byref(ws_bytes)),
                    "sa_attn_pooling_workspace")
         ws = torch.empty(ws_bytes.value, dtype=torch.uint8, device=q.device)
-        fn = "sa_attn_pooling_fwd_f16" if fp16 else "sa_attn_pooling_fwd"
+        fn = "sa_attn_pooling_fwd_f16" if fp16 else ("sa_attn_pooling_fwd_f32" if fp32 else "sa_attn_pooling_fwd")
         with torch.cuda.device(q.device):
             _lib.check(getattr(lib, fn)(
                 q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
                 v.data_ptr(), _lib.i64(*v.stride()[:3]), o.data_ptr(), _lib.i64(*o.stride()[:3]),
                 B, H, Hk, L, D, 1 if causal else 0, float(sm_scale), block_size, po.data_ptr(),
                 _lib.i64(*po.stride()[:3]), ws.data_ptr(), ws.numel(), _lib.stream_of(q)), fn)
-        return o, (po.to(torch.float16) if fp16 else po)
+        return o.to(orig_dtype), (po.to(torch.float16) if fp16 else po)
 
 
-attn_with_pooling = _attention_pooling.apply
+def attn_with_pooling(q, k, v, causal, sm_scale, block_size, precision=None):
+    """(o, Po) as the reference's `attn_with_pooling = _attention_pooling.apply` (:289); the
+    optional `precision="fp32"` computes 16-bit inputs in fp32 as the reference does."""
+    return _attention_pooling.apply(q, k, v, causal, sm_scale, block_size, precision)
 
 
 def is_hip() -> bool:

@@ -12,10 +12,9 @@ libsa_hip.so (`sa_mask_to_kv_list` + `sa_block_sparse_fwd`), not Triton.
 Inputs are bf16 or fp16 (all three the same), head_dim 64 or 128 as the reference asserts
 (:231); P is rounded to the input dtype before P.V as the reference rounds it to v's (:107).
 fp32 inputs run the fp32 kernel (`sa_block_sparse_fwd_f32`: fp32 MFMA, P kept in fp32, as the
-reference's cast to v's dtype leaves it), head_dim 64.
+reference's cast to v's dtype leaves it), head_dim 64 or 128.
 
 Differences from the reference, by design:
-  * fp32 inputs need head_dim 64 (the reference also takes 128);
   * a query block whose mask row is empty yields 0 instead of NaN (:201-203);
   * sm_scale must be > 0.
 """
@@ -96,7 +95,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128, or fp32
-    with D = 64 (plain lists only: fp32 MFMA, P kept in fp32 as the reference's kernel does);
+    (plain lists only: fp32 MFMA, P kept in fp32 as the reference's kernel does);
     key_bias optional fp32 [B,H,Lk] (any strides with a contiguous key axis, stride 0 to
     broadcast). `n_text_blocks` only affects scheduling (those block rows are dispatched
     first).

@@ -353,8 +353,8 @@ def test_mixed_or_fp64_dtypes_rejected(dev):
         block_sparse_triton_fn(q.float(), q.float(), q, m, 1 / 8)
     with pytest.raises(TypeError):
         block_sparse_triton_fn(q.double(), q.double(), q.double(), m, 1 / 8)
-    with pytest.raises(NotImplementedError):  # fp32 kernel: head dim 64
-        qq = torch.randn(1, 1, 64, 128, device=dev)
+    with pytest.raises(AssertionError):  # head dims the reference asserts: 64 or 128
+        qq = torch.randn(1, 1, 64, 96, device=dev)
         block_sparse_triton_fn(qq, qq, qq, m, 1 / 8)
 
 
@@ -399,6 +399,25 @@ def test_fp32_random_masks(dev, Lq, Lk, seed):
     out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125)
     _check_f32(out, masked_attention(q, k, v, mask, 0.125))
     assert torch.all(out[1, 2, :64] == 0)
+
+
+@pytest.mark.parametrize("Lq,Lk,seed", [(257, 257, 11), (130, 385, 12), (700, 700, 13)])
+def test_fp32_head_dim_128(dev, Lq, Lk, seed):
+    # head dim 128 (the reference accepts 64 and 128 for any dtype, :230-231): two 64-wide
+    # halves of d in the scores, eight 16-row d blocks of the output
+    case(f"fp32 d=128 Lq={Lq} Lk={Lk}")
+    B, H = 1, 3
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, n, 128, generator=g) for n in (Lq, Lk, Lk))
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.5
+    mask[..., 0] = True
+    mask[0, 1, 1] = False  # an empty row writes 0
+    scale = 1 / math.sqrt(128)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+    assert out.shape == q.shape
+    _check_f32(out, masked_attention(q, k, v, mask, scale))
+    assert torch.all(out[0, 1, 64:128].cpu() == 0)
 
 
 def test_fp32_strided_and_large_scores(dev):

@@ -101,11 +101,63 @@ def test_pooled_attention_fp16_and_head_dim_128(dev, dtype, D, bs, causal):
     assert torch.allclose(po.cpu().double(), want_po, rtol=6e-3, atol=1e-7), (po.cpu().double() - want_po).abs().max()
 
 
-def test_pooled_attention_fp32_rejected(dev):
-    case("attn_with_pooling fp32 inputs")
-    q, k, v = _qkv(3, 1, 1, 1, 64, dtype=torch.float32)
-    with pytest.raises(TypeError):
-        attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), False, 0.125, 64)
+# fp32 arithmetic, as the reference computes attn_with_pooling (bf16 inputs cast to fp32,
+# :235-240): fp32 inputs always, 16-bit inputs with precision="fp32". The bar is fp32
+# accuracy against the fp64 oracle on the same inputs: out max-abs 2e-5 / mean-abs 2e-6, Po
+# relative 2e-5 (+1e-9 absolute).
+F32_MAX, F32_MEAN = 2e-5, 2e-6
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D,Hk", [(64, 4), (64, 2), (128, 2)])
+def test_pooled_attention_fp32(dev, bs, causal, D, Hk):
+    case(f"attn_with_pooling fp32 bs={bs} causal={causal} D={D} Hk={Hk}")
+    q, k, v = _qkv(bs + 3 * Hk + causal + D, 1, 4, Hk, 600, scale=1.5, D=D, dtype=torch.float32)
+    scale = 1 / math.sqrt(D)
+    o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, scale, bs)
+    assert o.dtype == torch.float32 and po.dtype == torch.float32
+    want_o, want_po = pooled_attention(q, k, v, causal, scale, bs)
+    err = (o.cpu().double() - want_o).abs()
+    assert err.max().item() <= F32_MAX and err.mean().item() <= F32_MEAN, (err.max().item(), err.mean().item())
+    assert po.shape == want_po.shape
+    assert torch.allclose(po.cpu().double(), want_po, rtol=2e-5, atol=1e-9), (po.cpu().double() - want_po).abs().max()
+    if causal:
+        nd = po.shape[-1]
+        up = torch.ones(nd, nd, dtype=torch.bool).triu(1)
+        assert torch.all(po.cpu()[..., up] == 0)
+
+
+@pytest.mark.parametrize("L", [40, 130])
+def test_pooled_attention_fp32_short(dev, L):
+    case(f"attn_with_pooling fp32 L={L}")
+    q, k, v = _qkv(L, 2, 2, 2, L, dtype=torch.float32)
+    for bs in (32, 64, 128):
+        for causal in (False, True):
+            o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, 0.125, bs)
+            want_o, want_po = pooled_attention(q, k, v, causal, 0.125, bs)
+            assert (o.cpu().double() - want_o).abs().max().item() <= F32_MAX
+            assert torch.allclose(po.cpu().double(), want_po, rtol=2e-5, atol=1e-9)
+
+
+def test_pooled_attention_bf16_in_fp32_arithmetic(dev):
+    # precision="fp32": bf16 inputs computed as the reference computes them (cast to fp32);
+    # Po at the fp32 bar against the oracle on the bf16 values, out rounded once to bf16.
+    case("attn_with_pooling bf16 inputs, precision fp32")
+    q, k, v = _qkv(77, 1, 4, 2, 900, scale=1.5)
+    for bs, causal in ((64, False), (128, True), (32, True)):
+        o, po = attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), causal, 0.125, bs, precision="fp32")
+        assert o.dtype == torch.bfloat16 and po.dtype == torch.float32
+        want_o, want_po = pooled_attention(q, k, v, causal, 0.125, bs)
+        assert torch.allclose(po.cpu().double(), want_po, rtol=2e-5, atol=1e-9)
+        # the only rounding of out is the final one to bf16: within half a bf16 ulp of the oracle
+        # (plus the fp32 bar), and equal to the fp32 result of the same inputs rounded once
+        err = (o.cpu().double() - want_o).abs()
+        assert torch.all(err <= want_o.abs() * 2.0 ** -8 + 2e-5)
+        o32, _ = attn_with_pooling(q.float().to(dev), k.float().to(dev), v.float().to(dev), causal, 0.125, bs)
+        assert torch.equal(o, o32.to(torch.bfloat16))
+    with pytest.raises(ValueError):
+        attn_with_pooling(q.to(dev), k.to(dev), v.to(dev), False, 0.125, 64, precision="fp64")
 
 
 @pytest.mark.parametrize("causal", [False, True])
