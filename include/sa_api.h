@@ -62,6 +62,32 @@ int sa_mask_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B
                        void* stream);
 
 /*
+ * Block mask of another block shape -> 64 x 64 tile lists with token-level cuts.
+ * Serves sparse_attention_factory(BLOCK_M, BLOCK_N) (utils/block_sparse_attn_kernel.py:
+ * 283-291): mask row m covers query rows [m*BLOCK_M, (m+1)*BLOCK_M), column n keys
+ * [n*BLOCK_N, (n+1)*BLOCK_N) (:139-155). block_m, block_n: powers of two in 16..1024.
+ *   mask      uint8/bool [B, H, >= ceil(Lq/block_m), >= ceil(Lk/block_n)], element strides.
+ *   kv_idx/kv_cnt  lists of the 64-row tiles (rows B*H*ceil(Lq/64), max_cnt >= ceil(Lk/64)):
+ *             a 64-key tile is listed when a mask cell it covers is set (cells past Lq or Lk
+ *             neither keep nor cut a tile).
+ *   kv_slot   [rows][max_cnt]: -1 when every cell of the tile is set, else the pattern of set
+ *             cells, an index into sa_cell_tile_masks(block_m, block_n); may be NULL when both
+ *             block sizes are >= 64 (then every listed tile is whole).
+ * The lists and slots go to sa_block_sparse_fwd_tilemask / _mapped(_f16) unchanged.
+ */
+int sa_mask_cells_to_kv_list(const uint8_t* mask, const int64_t mask_strides[4], int B, int H,
+                             int Lq, int Lk, int block_m, int block_n, int32_t* kv_idx,
+                             int32_t* kv_slot, int max_cnt, int32_t* kv_cnt, void* stream);
+
+/*
+ * Host. Token masks of every cell pattern of a 64 x 64 tile for sa_mask_cells_to_kv_list:
+ * masks[p][r] bit k is set when the cell holding (query r, key k) of the tile is set in
+ * pattern p. *n_patterns = 2^(cells per tile) (at most 65 536, for 16 x 16 blocks);
+ * masks = NULL: count only.
+ */
+int sa_cell_tile_masks(int block_m, int block_n, uint64_t* masks, int64_t* n_patterns);
+
+/*
  * Block-sparse attention forward: out = softmax(q k^T * sm_scale [+ key_bias]) v restricted,
  * for each 64-row query block, to the 64-key blocks in its kv list.
  * Replaces `block_sparse_triton_fn` / `_forward` / `_fwd_kernel`

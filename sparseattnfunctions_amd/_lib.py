@@ -32,6 +32,8 @@ _PROTOTYPES = {
     "sa_abi_version": (_I, []),
     "sa_last_error": (ctypes.c_char_p, []),
     "sa_mask_to_kv_list": (_I, [_P, _I64P, _I, _I, _I, _I, _P, _I, _P, _P]),
+    "sa_mask_cells_to_kv_list": (_I, [_P, _I64P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),
+    "sa_cell_tile_masks": (_I, [_I, _I, _P, _I64P]),
     "sa_block_pool": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "sa_block_topk_kv_list": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P]),
     "sa_block_sparse_fwd": (

@@ -592,7 +592,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
           for (int g = 0; g < 2; ++g) {
             const float m_new = fmaxf(m[g], cand[g]);
-            const float alpha = fast_exp2(m[g] - m_new);  // 0 when m = -inf
+            // 0 when m = -inf; a row with no key yet (m_new = -inf: every key so far masked, while
+            // another row of the wave raised its maximum) has nothing to rescale.
+            const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m[g] - m_new);
             m[g] = m_new;
             l[g] *= alpha;
 #pragma unroll

@@ -4,7 +4,9 @@ Mirrors special_attentions/utils/block_sparse_attn_kernel.py of xiaolong-li1/Spa
   * `block_sparse_triton_fn(q, k, v, block_sparse_mask, sm_scale)` (:293) -- same arguments,
     same asserts (:226-231), output allocated like `torch.empty_like(q)` (:228), forward only
     (backward raises NotImplementedError, :278-281);
-  * `sparse_attention_factory` (:283-291), `get_sparse_attn_mask_from_topk` (:31-39) and
+  * `sparse_attention_factory` (:283-291; any power-of-two BLOCK_M x BLOCK_N from 16 to 1024,
+    mapped onto 64 x 64 tiles with token-level masks where a tile is cut),
+    `get_sparse_attn_mask_from_topk` (:31-39) and
     `get_sparse_attn_mask_from_threshold` (:42-47).
 The name keeps "triton" for source compatibility; the work runs in the HIP kernels of
 libsa_hip.so (`sa_mask_to_kv_list` + `sa_block_sparse_fwd`), not Triton.
@@ -207,17 +209,63 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     return out
 
 
+_CELL_MASKS = {}
+
+
+def cell_tile_masks(block_m: int, block_n: int, device) -> torch.Tensor:
+    """Device table of the 64 x 64 token masks of every cell pattern (`sa_cell_tile_masks`),
+    cached per block shape."""
+    key = (block_m, block_n, str(device))
+    t = _CELL_MASKS.get(key)
+    if t is None:
+        lib = _lib.load()
+        n = ctypes.c_int64(0)
+        _lib.check(lib.sa_cell_tile_masks(block_m, block_n, None, ctypes.byref(n)), "sa_cell_tile_masks")
+        host = torch.empty(n.value, 64, dtype=torch.int64)
+        _lib.check(lib.sa_cell_tile_masks(block_m, block_n, host.data_ptr(), ctypes.byref(n)), "sa_cell_tile_masks")
+        t = _CELL_MASKS[key] = host.to(device)
+    return t
+
+
+def cell_kv_list(mask: torch.Tensor, B: int, H: int, Lq: int, Lk: int, block_m: int, block_n: int):
+    """(KVList of 64 x 64 tiles, kv_slot or None) for a block mask of block_m x block_n cells
+    (`sa_mask_cells_to_kv_list`)."""
+    _lib.require_gpu(mask)
+    nM, nN = math.ceil(Lq / block_m), math.ceil(Lk / block_n)
+    if mask.dim() != 4 or mask.shape[-2] < nM or mask.shape[-1] < nN:
+        raise ValueError(f"block mask of shape {tuple(mask.shape)} for {nM} x {nN} blocks of {block_m} x {block_n}")
+    m = mask.to(torch.bool).expand(B, H, mask.shape[-2], mask.shape[-1]).view(torch.uint8)
+    nqb, nkb = math.ceil(Lq / BLOCK), math.ceil(Lk / BLOCK)
+    kv = KVList.empty(B, H, nqb, nkb, mask.device)
+    slot = None if (block_m >= BLOCK and block_n >= BLOCK) else torch.empty_like(kv.idx)
+    with torch.cuda.device(mask.device):
+        _lib.check(_lib.load().sa_mask_cells_to_kv_list(
+            m.data_ptr(), _lib.i64(*m.stride()), B, H, Lq, Lk, block_m, block_n, kv.idx.data_ptr(), _lib.ptr(slot),
+            kv.max_cnt, kv.cnt.data_ptr(), _lib.stream_of(m)), "sa_mask_cells_to_kv_list")
+    return kv, slot
+
+
 def _forward(ctx, q, k, v, block_sparse_mask, sm_scale, BLOCK_M=64, BLOCK_N=64, num_warps=None,
              num_stages=1, out=None):
-    """Reference host wrapper semantics (block_sparse_attn_kernel.py:211-265)."""
+    """Reference host wrapper semantics (block_sparse_attn_kernel.py:211-265). BLOCK_M x BLOCK_N
+    other than 64 x 64 (powers of two, 16..1024): mask row m covers query rows m*BLOCK_M..,
+    column n keys n*BLOCK_N.. (:139-155); the kernel runs 64 x 64 tiles, a tile cut by the mask
+    with token-level masks (`sa_mask_cells_to_kv_list`)."""
     assert q.shape[-1] == k.shape[-1] == v.shape[-1]
     assert k.shape[2] == v.shape[2]
     assert q.shape[-1] in [64, 128]
-    if BLOCK_M != BLOCK or BLOCK_N != BLOCK:
-        raise NotImplementedError("the MI355X kernel uses 64x64 blocks")
     B, H, Lq, _ = q.shape
-    kv = kv_list_from_mask(block_sparse_mask, B, H, math.ceil(Lq / BLOCK), math.ceil(k.shape[2] / BLOCK))
-    return block_sparse_attention(q, k, v, kv, sm_scale, out=out)
+    Lk = k.shape[2]
+    if BLOCK_M == BLOCK and BLOCK_N == BLOCK:
+        kv = kv_list_from_mask(block_sparse_mask, B, H, math.ceil(Lq / BLOCK), math.ceil(Lk / BLOCK))
+        return block_sparse_attention(q, k, v, kv, sm_scale, out=out)
+    kv, slot = cell_kv_list(block_sparse_mask, B, H, Lq, Lk, int(BLOCK_M), int(BLOCK_N))
+    if slot is None:
+        return block_sparse_attention(q, k, v, kv, sm_scale, out=out)
+    if q.dtype == torch.float32:
+        raise NotImplementedError("fp32 inputs with blocks smaller than 64: the fp32 kernel has no token masks")
+    return block_sparse_attention(q, k, v, kv, sm_scale, out=out,
+                                  tile_masks=(slot, cell_tile_masks(int(BLOCK_M), int(BLOCK_N), q.device), False))
 
 
 class _sparse_attention(torch.autograd.Function):

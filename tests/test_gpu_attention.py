@@ -268,8 +268,8 @@ def test_factory_and_backward(dev):
     m = torch.ones(1, 1, 1, 1, dtype=torch.bool, device=dev)
     out = fn(q, k, v, m, 0.125)
     assert out.shape == q.shape
-    with pytest.raises(NotImplementedError):
-        sparse_attention_factory(128, 64)(q, k, v, m, 0.125)
+    with pytest.raises(ValueError):  # BLOCK_M must be a power of two from 16 to 1024
+        sparse_attention_factory(96, 64)(q, k, v, m, 0.125)
     qg = q.clone().requires_grad_(True)
     o = block_sparse_triton_fn(qg, k, v, m, 0.125)
     with pytest.raises(NotImplementedError):
@@ -632,3 +632,63 @@ def test_key_range_split_caller_workspace(dev):
         B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, 0.125, None, 0, None, 0, parts,
         ws.data_ptr(), nbytes - 4, _lib.stream_of(qd))
     assert rc == _lib.SA_ERR_INVALID
+
+
+def _token_mask(mask, Lq, Lk, bm, bn):
+    """Token-level [B, H, Lq, Lk] expansion of a block mask of bm x bn blocks."""
+    rows = torch.arange(Lq) // bm
+    cols = torch.arange(Lk) // bn
+    return mask[:, :, rows][:, :, :, cols]
+
+
+@pytest.mark.parametrize("bm,bn,Lq,Lk", [
+    (32, 32, 300, 300), (16, 64, 200, 333), (64, 16, 257, 190), (128, 128, 500, 500),
+    (128, 64, 300, 450), (32, 128, 260, 515), (16, 16, 150, 170), (256, 32, 600, 300),
+])
+def test_factory_block_shapes(dev, bm, bn, Lq, Lk):
+    # sparse_attention_factory(BLOCK_M, BLOCK_N) (block_sparse_attn_kernel.py:283-291): mask row
+    # m covers query rows m*BLOCK_M.., column n keys n*BLOCK_N.. (:139-155). Against the fp64
+    # oracle on the token-level expansion of the mask; rows whose cells are all off write 0.
+    case(f"factory BLOCK_M={bm} BLOCK_N={bn} Lq={Lq} Lk={Lk}")
+    B, H = 1, 2
+    g = torch.Generator().manual_seed(bm * 13 + bn + Lq)
+    q, k, v = _rand((B, H, Lq, 64), 600 + bm), _rand((B, H, Lk, 64), 601 + bn), _rand((B, H, Lk, 64), 602)
+    nM, nN = math.ceil(Lq / bm), math.ceil(Lk / bn)
+    mask = torch.rand(B, H, nM, nN, generator=g) < 0.35
+    mask[0, 0, 0] = False  # an empty row of cells
+    mask[0, 1, -1] = True  # a full row of cells, last (partial) one included
+    fn = sparse_attention_factory(BLOCK_M=bm, BLOCK_N=bn)
+    out = fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125)
+    tok = _token_mask(mask, Lq, Lk, bm, bn)
+    want = masked_attention(q, k, v, tok, 0.125, block=1)
+    _check(out, want)
+    assert torch.all(out[0, 0, :min(bm, Lq)].cpu() == 0)
+    # the same mask at 64 x 64 granularity where it is one: bit-identical to the 64 path
+    if bm == 64 and bn == 64:
+        assert torch.equal(out, block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125))
+
+
+def test_factory_block_shapes_fp16_and_d128(dev):
+    case("factory 32 x 32, fp16 and head dim 128")
+    g = torch.Generator().manual_seed(71)
+    for dtype, D in ((torch.float16, 64), (torch.bfloat16, 128)):
+        q, k, v = (torch.randn(1, 2, 230, D, generator=g).to(dtype) for _ in range(3))
+        mask = torch.rand(1, 2, 8, 8, generator=g) < 0.4
+        mask[..., 0] = True
+        out = sparse_attention_factory(32, 32)(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 1 / math.sqrt(D))
+        _check(out, masked_attention(q, k, v, _token_mask(mask, 230, 230, 32, 32), 1 / math.sqrt(D), block=1))
+
+
+def test_factory_block_shapes_fp32(dev):
+    # fp32 inputs: whole-tile shapes (multiples of 64) run the fp32 kernel on the expanded
+    # lists; smaller blocks need token masks, which the fp32 kernel does not have.
+    case("factory fp32")
+    g = torch.Generator().manual_seed(72)
+    q, k, v = (torch.randn(1, 2, 300, 64, generator=g) for _ in range(3))
+    mask = torch.rand(1, 2, 3, 5, generator=g) < 0.5
+    mask[..., 0] = True
+    out = sparse_attention_factory(128, 64)(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125)
+    _check_f32(out, masked_attention(q, k, v, _token_mask(mask, 300, 300, 128, 64), 0.125, block=1))
+    with pytest.raises(NotImplementedError):
+        sparse_attention_factory(32, 64)(q.to(dev), k.to(dev), v.to(dev), torch.ones(1, 2, 10, 5, dtype=torch.bool,
+                                                                                    device=dev), 0.125)
