@@ -286,8 +286,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // Bias rows: three 64-key slots per wave (list positions of even and odd index, and a slot
   // for the copies issued past the end of the list, which nothing reads).
   __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * 3 * kBlock : 4];
-  // Vector-memory operations per tile, in issue order: group K = [mask rows (2)] [K (8 per
-  // half)], group V = [bias of the next tile (1)] [V (8 per half)]. The waits below count them.
+  // Vector-memory operations per tile, in issue order: group K = [mask rows (2, cut tiles
+  // only)] [K (8 per half)], group V = [bias of the next tile (1)] [V (8 per half)]. The
+  // waits below count them.
   constexpr int kGroupK = 8 * kHalves + (kMask ? 2 : 0);
   constexpr int kGroupV = 8 * kHalves + (kBias ? 1 : 0);
 
@@ -414,9 +415,11 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
     if (kMask) {
       mslot = it < cnt ? slots[it] : -1;
-      const uint64_t* mrow = a.tile_masks + (int64_t)max(mslot, 0) * kBlock;
-      mw[0] = mrow[col];
-      mw[1] = mrow[32 + col];
+      if (mslot >= 0) {  // rows of a cut tile only (mslot is wave-uniform)
+        const uint64_t* mrow = a.tile_masks + (int64_t)mslot * kBlock;
+        mw[0] = mrow[col];
+        mw[1] = mrow[32 + col];
+      }
     }
     if (kD == 64 && c128) {
       dma_tile_c128(khead, kbytes, kb0 * krow, kgo, kl);
@@ -620,7 +623,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
           }
 
       // ---- V^T operands of this tile, then request the next tile's V.
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
+      // The next tile's group K holds its two mask-row loads only if that tile is cut.
+      if (kMask && mslot < 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK - 2));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
       // The reads are issued in the order the P·V MFMAs consume them, and each MFMA pair
       // waits only for its own two reads (LDS reads return in order; the full wait first
       // leaves no scalar load outstanding, so the counts are exact). The next tile's V
