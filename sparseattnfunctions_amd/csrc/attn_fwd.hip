@@ -12,7 +12,9 @@
 // workgroup holds 4 independent waves (no workgroup barriers) and two workgroups share a
 // CU (2 waves per SIMD). Per 64-key tile a wave computes S^T = K Q^T and O^T = V^T P^T
 // with v_mfma_f32_32x32x16_bf16 (16 + 16 MFMAs = 1 MFLOP); each lane holds one query
-// column of S^T, so row statistics need one cross-half exchange.
+// column of S^T, so row statistics need one cross-half exchange. Plain lists at head dim 128
+// run bsa_fwd_pair_kernel instead: two waves of 32 query rows share each block's tiles, so
+// that two waves fit a SIMD.
 //
 // Data movement. An MFMA operand load straight from global memory puts a different row in
 // every lane, so each 1 KB load costs the address unit ~64 cache-line lookups; that, not
@@ -265,8 +267,10 @@ constexpr int kWaitLgkm0 = 0xC07F;
 
 // T: bf16 or fp16 operands (and output). kD: head dim 64 or 128. A 128-dim row is staged as
 // two 128-byte half rows in two half tiles with the 64-dim layout, so every read pattern of
-// the 64-dim kernel applies per half; at 128 dims a wave holds ~420 registers, so one
-// workgroup (one wave per SIMD) runs per CU.
+// the 64-dim kernel applies per half; at 128 dims a wave holds ~350 registers, so one
+// workgroup (one wave per SIMD) runs per CU. (Plain head-dim-128 lists without key-range
+// parts run bsa_fwd_pair_kernel; this kernel serves their bias, tile-mask, pooling and split
+// launches.)
 // kDV: value columns that enter P.V and the output, kD or 32 (head dim 64: v tiles are
 // copied as usual and only their first 32 columns are read; out has 32 columns).
 template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64, int kDV = kD>
@@ -805,6 +809,296 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   }
 }
 
+
+// Workgroup barrier with no memory fence: the waits before it are explicit (a fence would
+// also wait for the copies in flight). The clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Head dim 128, plain lists: one query block per workgroup of two waves (a wave pair). Wave g
+// holds query rows 32g .. 32g + 31 of the block: its Q^T operands, O^T accumulators and S^T
+// take half the registers of a 64-row wave (216 VGPRs against ~350), so two waves run per
+// SIMD where bsa_fwd_kernel fits one. The pair shares one K and one V tile in LDS, and wave g
+// copies the 128-byte half rows of d half g of each (the half tiles of bsa_fwd_kernel). Four
+// workgroup barriers per tile order the copies and the reads: K landed, K read (the K buffer
+// may be refilled), V landed, V read. Same operations per sum in the same order as
+// bsa_fwd_kernel: bit-identical outputs. (At head dim 64 the same scheme, three waves per
+// SIMD, was slower than bsa_fwd_kernel's two 64-row waves.)
+// Slots: the four slots of dispatch group w (the work order's unit, placed on XCD w % 8)
+// go to the workgroups x = 32 (w / 8) + 8 i + w % 8, i = 0..3, which the dispatcher places
+// on the same XCD.
+template <typename T>
+__global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
+  typedef Elem<T> E;
+  constexpr int kD = 128;
+  constexpr int kDS = kD / 16;        // 16-wide d steps of S = K Q^T
+  constexpr int kDC = kD / 32;        // 32-row d chunks of O^T
+  constexpr int kHalves = kD / 64;    // 128-byte half tiles per K or V tile
+  constexpr int kCopies = 8;          // copy instructions per wave and tile, each of K and V
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kHalves * kTileBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kHalves * kTileBytes];
+  __shared__ int redo_lds[2];
+
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // query rows 32g .. 32g + 31
+  const int col = lane & 31;
+  const int hh = lane >> 5;
+  const int x = blockIdx.x;
+  const int slot = 4 * (8 * (x >> 5) + (x & 7)) + ((x >> 3) & 3);
+  int item = -1;
+  if (slot < a.n_slots) item = __builtin_amdgcn_readfirstlane(a.order ? a.order[slot] : slot);
+  // Both waves take the same branch: no barrier is left unmatched.
+  if (item < 0 || item >= a.n_items) return;
+  const int bh = item / a.nqb;
+  const int qb = item - bh * a.nqb;
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int64_t list_row = (int64_t)bh * a.list_bh_stride + qb;
+  int cnt = a.kv_cnt[list_row];
+  cnt = cnt < 0 ? 0 : (cnt > a.max_cnt ? a.max_cnt : cnt);
+  const __attribute__((address_space(4))) int32_t* list =
+      (const __attribute__((address_space(4))) int32_t*)(a.kv_idx + list_row * a.max_cnt);
+
+  const uint16_t* qbase = a.q + b * a.q_sb + h * a.q_sh;
+  const int hk = a.kv_rep > 1 ? h / a.kv_rep : h;
+  const uint16_t* khead = a.k + b * a.k_sb + hk * a.k_sh;
+  const uint16_t* vhead = a.v + b * a.v_sb + hk * a.v_sh;
+  const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
+  const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
+  const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
+  lds_u8* const kl = (lds_u8*)k_lds;
+  lds_u8* const vl = (lds_u8*)v_lds;
+
+  uint32_t kgo[2], vgo[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int r = 8 * p + (lane >> 3);
+    const int chunk = (lane & 7) ^ swz(r);
+    kgo[p] = (lane >> 3) * krow + 16 * chunk;
+    vgo[p] = (lane >> 3) * vrow + 16 * chunk;
+  }
+  int kro[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) kro[s] = 128 * col + 16 * ((2 * s + hh) ^ swz(col));
+  int vro[2][2];
+  {
+    const int i = lane & 15, g4 = lane >> 4;
+    const int hq = g4 >> 1, dg = g4 & 1;
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int r = 8 * t + 4 * hq + (i >> 2);
+        const int chunk = 4 * dc + 2 * dg + ((i & 3) >> 1);
+        vro[dc][t] = 128 * r + 16 * (chunk ^ swz(r)) + 8 * (i & 1);
+      }
+  }
+
+  // Q^T B operands of query row qb * 64 + 32g + col (clamped into Lq; clamped rows are never
+  // stored; with a row map, q row q_rows[i], zeros outside q).
+  typename E::v8 qf[kDS];
+  {
+    int row = min(qb * kBlock + 32 * g + col, a.Lq - 1);
+    bool zero = false;
+    if (a.q_rows) {
+      row = a.q_rows[row];
+      zero = (unsigned)row >= (unsigned)a.q_src_rows;
+      row = zero ? 0 : row;
+    }
+    const uint16_t* p = qbase + (int64_t)row * a.q_sl + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < kDS; ++s) {
+      const uint4 w = *reinterpret_cast<const uint4*>(p + 16 * s);
+      qf[s] = __builtin_bit_cast(typename E::v8, zero ? make_uint4(0u, 0u, 0u, 0u) : w);
+    }
+  }
+  // The Q operands have landed before the first copy is issued, so that no load issued
+  // before the loop is pending inside it.
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+
+  sa_f32x16 acc[kDC];
+  float m = -INFINITY, l = 0.f;
+
+  auto block_ok = [&](int kb) { return (unsigned)kb < (unsigned)a.nkb; };
+  // This wave's share of the copy of tile kb: the half tile of d half g (all 64 rows).
+  auto copy_share = [&](const uint16_t* head, uint32_t bytes, uint32_t row, const uint32_t (&go)[2], lds_u8* dst,
+                        int kb) {
+    const uint32_t off = (block_ok(kb) ? (uint32_t)kb * kBlock : 0u) * row;
+    dma_tile(head + 64 * g, bytes, off, row, go, dst + g * kTileBytes);
+  };
+  auto issue_k = [&](int kb) { copy_share(khead, kbytes, krow, kgo, kl, kb); };
+  auto issue_v = [&](int kb) { copy_share(vhead, vbytes, vrow, vgo, vl, kb); };
+
+  // One pass over the list. Fast pass (kSafe = false): P = exp2(S) with no max, checked by
+  // the caller; safe pass: running max with lazy rescale.
+  auto run = [&](auto safe_tag) {
+    constexpr bool kSafe = decltype(safe_tag)::value;
+#pragma unroll
+    for (int dc = 0; dc < kDC; ++dc) acc[dc] = sa_f32x16{};
+    m = -INFINITY;
+    l = 0.f;
+    int kb = cnt > 0 ? list[0] : -1;
+    if (cnt > 0) {
+      issue_k(kb);
+      issue_v(kb);
+    }
+    for (int it = 0; it < cnt; ++it) {
+      // Past the end of the list the copies re-load the current block, so every iteration
+      // has the same copies in flight.
+      const int kb_next = it + 1 < cnt ? list[it + 1] : kb;
+      // ---- K landed (own share: the wait; the partner's: the barrier).
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+      wg_barrier();
+      sa_u32x4v kop[2][kDS];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < kDS; ++s) kop[c][s] = lds_read_b128(kl + (s >> 2) * kTileBytes + kro[s & 3] + 4096 * c);
+      sa_f32x16 S[2];  // S^T of keys 32c + ..., query row 32g + col
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        sa_f32x16 t = {};
+#pragma unroll
+        for (int s = 0; s < kDS; ++s) t = E::mfma(E::as8(kop[c][s]), qf[s], t);
+        S[c] = t;
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+      // ---- Both waves hold their K operands: refill the K buffer.
+      wg_barrier();
+      issue_k(kb_next);
+      const int nvalid = block_ok(kb) ? min(kBlock, a.Lk - kb * kBlock) : 0;
+      if (nvalid < kBlock) {  // keys past Lk, or an entry outside the grid
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (32 * c + 8 * (e >> 2) + 4 * hh + (e & 3) >= nvalid) S[c][e] = -INFINITY;
+      }
+      const float sc = a.scale_log2;
+      float mu = 0.f;
+      if (kSafe) {
+        float mx = fmaxf(fmaxf(S[0][0], S[0][1]), S[0][2]);
+#pragma unroll
+        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[0][e]), S[0][e + 1]);
+        mx = fmaxf(fmaxf(mx, S[0][15]), S[1][0]);
+#pragma unroll
+        for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[1][e]), S[1][e + 1]);
+        mx = fmaxf(mx, S[1][15]);
+        const float cand = xhalf_max(mx) * sc;  // sc > 0
+        if (__ballot(cand > m + kRescaleLog2) != 0) {
+          const float m_new = fmaxf(m, cand);
+          // A row with no key yet (m_new = -inf) has nothing to rescale.
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+          m = m_new;
+          l *= alpha;
+#pragma unroll
+          for (int dc = 0; dc < kDC; ++dc) acc[dc] *= alpha;
+        }
+        mu = m == -INFINITY ? 0.f : m;
+      }
+      uint32_t P[2][8];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) {
+          const float p0 = fast_exp2(kSafe ? fmaf(S[c][e], sc, -mu) : S[c][e] * sc);
+          const float p1 = fast_exp2(kSafe ? fmaf(S[c][e + 1], sc, -mu) : S[c][e + 1] * sc);
+          P[c][e >> 1] = E::pack(p0, p1);
+          l = E::dot2_ones(P[c][e >> 1], l);
+        }
+      // ---- V landed (own share: the wait; the partner's: the barrier).
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+      wg_barrier();
+#pragma unroll
+      for (int hp = 0; hp < kHalves; ++hp) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        sa_u32x2v vr[2][2][2][2];  // [c][u][dc][t]
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+              for (int t = 0; t < 2; ++t) {
+                const uint32_t base = (uint32_t)(uintptr_t)(vl + hp * kTileBytes + vro[dc][t]);
+                vr[c][u][dc][t] = (c == 0 ? (u == 0 ? lds_read_tr16_asm<0>(base) : lds_read_tr16_asm<2048>(base))
+                                          : (u == 0 ? lds_read_tr16_asm<4096>(base) : lds_read_tr16_asm<6144>(base)));
+              }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int dc = 0; dc < 2; ++dc) {
+              const int done = 2 * ((c * 2 + u) * 2 + dc) + 2;  // reads this MFMA needs
+              lgkm_wait_pair(16 - done, vr[c][u][dc][0], vr[c][u][dc][1]);
+              const sa_u32x4v vop = {vr[c][u][dc][0].x, vr[c][u][dc][0].y, vr[c][u][dc][1].x, vr[c][u][dc][1].y};
+              acc[2 * hp + dc] = E::mfma(
+                  E::as8(vop), E::as8(sa_u32x4v{P[c][4 * u], P[c][4 * u + 1], P[c][4 * u + 2], P[c][4 * u + 3]}),
+                  acc[2 * hp + dc]);
+            }
+      }
+      // ---- Both waves hold their V operands: refill the V buffer.
+      wg_barrier();
+      issue_v(kb_next);
+      kb = kb_next;
+    }
+    // The copies requested after the last tile land in LDS: wait for them before the LDS
+    // is written again or the wave ends.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  };
+
+  constexpr bool kFast = std::is_same<T, __bf16>::value;
+  if (kFast) {
+    run(std::false_type{});
+    // The fast pass is exact unless a row's sum left [2^-90, 2^90] or an accumulator
+    // overflowed; then the pair redoes its block with the safe pass. Both waves decide
+    // together (their barriers must match).
+    bool bad = false;
+    if (cnt > 0) {
+      const float l_tot = xhalf_sum(l);
+      bad = !(l_tot >= 0x1p-90f && l_tot <= 0x1p90f);
+      float amax = 0.f;
+#pragma unroll
+      for (int dc = 0; dc < kDC; ++dc)
+#pragma unroll
+        for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][e])), fabsf(acc[dc][e + 1]));
+      bad |= !(amax <= 3.0e38f);
+    }
+    const int wave_bad = __ballot(bad) != 0;
+    if (lane == 0) redo_lds[g] = wave_bad;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    wg_barrier();
+    const bool redo = (redo_lds[0] | redo_lds[1]) != 0;
+    if (redo) run(std::true_type{});
+  } else {
+    run(std::true_type{});
+  }
+
+  // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
+  const float l_tot = xhalf_sum(l);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  int row = qb * kBlock + 32 * g + col;
+  bool store = row < a.Lq;
+  if (store && a.o_rows) {  // remapped layout: query i goes to out row o_rows[i]
+    row = a.o_rows[row];
+    store = (unsigned)row < (unsigned)a.o_dst_rows;
+  }
+  if (store) {
+    uint16_t* orow = a.o + b * a.o_sb + h * a.o_sh + (int64_t)row * a.o_sl;
+#pragma unroll
+    for (int dc = 0; dc < kDC; ++dc)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const sa_f32x16& A = acc[dc];
+        // element 4q4 + j is d = 32dc + 8q4 + 4hh + j
+        *reinterpret_cast<uint2*>(orow + 32 * dc + 8 * q4 + 4 * hh) =
+            make_uint2(E::pack(A[4 * q4] * inv, A[4 * q4 + 1] * inv), E::pack(A[4 * q4 + 2] * inv, A[4 * q4 + 3] * inv));
+      }
+  }
+}
+
 }  // namespace
 
 
@@ -934,6 +1228,15 @@ void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask
     if (v32) {  // 32 value columns (the caller has rejected tile masks and pooling)
       if (bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, T, kD, 32>), g, blk, 0, s, a);
       else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, 32>), g, blk, 0, s, a);
+      return;
+    }
+  }
+  if constexpr (kD == 128) {
+    if (!mask && !bias && pool_cols == 0 && a.n_parts == 1) {  // plain lists: wave pairs
+      // Workgroup x runs slot 4 (8 (x / 32) + x % 8) + (x / 8) % 4: the four slots of each
+      // dispatch group on that group's XCD.
+      const int64_t groups = a.n_slots / kWaves;
+      hipLaunchKernelGGL((bsa_fwd_pair_kernel<T>), dim3((unsigned)((groups + 7) / 8 * 32)), dim3(128), 0, s, a);
       return;
     }
   }

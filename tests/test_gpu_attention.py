@@ -93,11 +93,12 @@ def test_empty_rows_write_zero(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125))
 
 
-def test_strided_and_broadcast(dev):
+@pytest.mark.parametrize("D", [64, 128])
+def test_strided_and_broadcast(dev, D):
     # q/k/v as views of a [B, L, H, D] buffer (non-contiguous heads) and a [1,1,n,n] mask.
-    case("strided BLHD views + broadcast mask")
+    case(f"strided BLHD views + broadcast mask D={D}")
     B, L, H = 2, 300, 4
-    base = [_rand((B, L, H, 64), 50 + i) for i in range(3)]
+    base = [_rand((B, L, H, D), 50 + i) for i in range(3)]
     q, k, v = (t.to(dev).permute(0, 2, 1, 3) for t in base)
     nb = math.ceil(L / 64)
     g = torch.Generator().manual_seed(5)
@@ -171,20 +172,41 @@ def test_key_bias_short_lists(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125, key_bias=bias.double()))
 
 
-def test_large_scores_redo_with_running_max(dev):
+@pytest.mark.parametrize("D", [64, 128])
+def test_large_scores_redo_with_running_max(dev, D):
     # Head 0 has scores of several hundred (exp2 overflows without the max subtraction),
     # head 1 ordinary ones: the kernel must redo exactly the items whose sums left range.
-    case("large scores on one head")
+    case(f"large scores on one head D={D}")
     B, H, L = 1, 2, 300
-    q, k, v = (_rand((B, H, L, 64), 130 + i) for i in range(3))
+    q, k, v = (_rand((B, H, L, D), 130 + i) for i in range(3))
     q[:, 0] *= 16
     k[:, 0] *= 16
     nb = math.ceil(L / 64)
     g = torch.Generator().manual_seed(13)
     mask = torch.rand(B, H, nb, nb, generator=g) < 0.6
     mask[..., 0] = True
-    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 0.125)
-    _check(out, masked_attention(q, k, v, mask, 0.125))
+    scale = 1 / math.sqrt(D)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+    _check(out, masked_attention(q, k, v, mask, scale))
+
+
+def test_head_dim_128_redo_when_one_half_overflows(dev):
+    # At head dim 128 a query block is computed by two waves of 32 rows each. Here only rows
+    # 0-31 of each block of head 0 have scores of several hundred: one wave's row sums leave
+    # range, the other's do not, and the pair must redo the block together (the two waves'
+    # barriers must match) and still give both halves exactly.
+    case("head dim 128, large scores in rows 0-31 of each block")
+    B, H, L, D = 1, 2, 320, 128
+    q, k, v = (_rand((B, H, L, D), 530 + i) for i in range(3))
+    rows = (torch.arange(L) % 64) < 32
+    q[:, 0, rows] *= 48  # log2-domain scores up to ~330 in rows 0-31; rows 32-63 stay below 10
+    nb = math.ceil(L / 64)
+    g = torch.Generator().manual_seed(531)
+    mask = torch.rand(B, H, nb, nb, generator=g) < 0.6
+    mask[..., 0] = True
+    scale = 1 / math.sqrt(D)
+    out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), scale)
+    _check(out, masked_attention(q, k, v, mask, scale))
 
 
 def test_uniform_negative_bias_is_shift_invariant(dev):
@@ -200,7 +222,8 @@ def test_uniform_negative_bias_is_shift_invariant(dev):
     _check(out, masked_attention(q, k, v, mask, 0.125))
 
 
-@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float16, 64), (torch.float16, 128)])
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float16, 64), (torch.bfloat16, 128),
+                                     (torch.float16, 128)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_row_mapped_queries_and_outputs(dev, with_bias, dtype, D):
     # Logical query i reads q row q_rows[i] (-1: zero padding) and is written to out row
