@@ -290,9 +290,11 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // Bias rows: three 64-key slots per wave (list positions of even and odd index, and a slot
   // for the copies issued past the end of the list, which nothing reads).
   __shared__ __attribute__((aligned(16))) float b_lds[kBias ? kWaves * 3 * kBlock : 4];
-  // Vector-memory operations per tile, in issue order: group K = [mask rows (2, cut tiles
-  // only)] [K (8 per half)], group V = [bias of the next tile (1)] [V (8 per half)]. The
-  // waits below count them.
+  // Tile-mask rows of the tile in flight (64 words per wave), copied like K and V.
+  __shared__ __attribute__((aligned(16))) uint64_t m_lds[kMask ? kWaves * kBlock : 2];
+  // Vector-memory operations per tile, in issue order: group K = [mask rows (2 copies into
+  // LDS, cut tiles only)] [K (8 per half)], group V = [bias of the next tile (1)] [V (8 per
+  // half)]. The waits below count them.
   constexpr int kGroupK = 8 * kHalves + (kMask ? 2 : 0);
   constexpr int kGroupV = 8 * kHalves + (kBias ? 1 : 0);
 
@@ -412,17 +414,18 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // An entry outside [0, nkb) copies block 0 and is masked out entirely.
   auto entry = [&](int it) -> int { return it < cnt ? list[it] : -1; };
   auto block_ok = [&](int kb) { return (unsigned)kb < (unsigned)a.nkb; };
-  uint64_t mw[2] = {~0ull, ~0ull};  // tile-mask rows 32g + col of the tile in flight
-  int mslot = -1;
+  int mslot = -1;  // mask slot of the tile in flight (-1: not cut)
   // Group K of tile `kb` (list position it): mask rows, K copy.
   auto issue_k = [&](int kb, int it) {
     const uint32_t kb0 = block_ok(kb) ? (uint32_t)kb * kBlock : 0u;
     if (kMask) {
       mslot = it < cnt ? slots[it] : -1;
-      if (mslot >= 0) {  // rows of a cut tile only (mslot is wave-uniform)
-        const uint64_t* mrow = a.tile_masks + (int64_t)mslot * kBlock;
-        mw[0] = mrow[col];
-        mw[1] = mrow[32 + col];
+      if (mslot >= 0) {  // the 512 bytes of a cut tile's rows, two 4-byte copies per lane
+        const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint64_t*>(a.tile_masks + (int64_t)mslot * kBlock), (short)0, kBlock * 8, 0x00020000);
+        lds_u8* md = (lds_u8*)(m_lds + (kMask ? wave * kBlock : 0));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, md, 4, lane * 4, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, md, 4, lane * 4, 0, 256, 0);
       }
     }
     if (kD == 64 && c128) {
@@ -477,17 +480,37 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       issue_k(kb, beg);
       issue_v(kb, beg);
     }
+    if constexpr (kMask) {
+      // The group K size varies with the tiles (mask rows of cut tiles only), and the
+      // compiler's wait analysis then carries the Q operand loads into the loop, where it
+      // would wait for every copy in flight before the first MFMA of each tile. Wait for them
+      // here (everything older than the prologue's copies) and redefine the Q registers
+      // after the wait, so that the loop sees no load behind them.
+      if (cnt > beg) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK - 2 + kGroupV));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int s = 0; s < kDS; ++s) asm volatile("" : "+v"(qf[g][s]));
+    }
     while (it < cnt) {
       // Past the end of the list the copies re-load the current block, so every iteration
       // has the same operations in flight.
       const int it_next = it + 1 < cnt ? it + 1 : it;
       const int kb_next = entry(it_next);
       const int nvalid = block_ok(kb) ? min(kBlock, a.Lk - kb * kBlock) : 0;
-      const uint64_t mw_cur[2] = {mw[0], mw[1]};
       const int mslot_cur = mslot;
 
       // ---- K operands of this tile, then request the next tile's group K.
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupV));
+      // This tile's mask rows (group K, landed by the wait above), read before the next
+      // tile's group K reuses the buffer.
+      uint64_t mw_cur[2] = {~0ull, ~0ull};
+      if (kMask && mslot_cur >= 0) {
+        const uint64_t* mr = m_lds + (kMask ? wave * kBlock : 0);
+        mw_cur[0] = mr[col];
+        mw_cur[1] = mr[32 + col];
+      }
       sa_u32x4v kop[2][kDS];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
@@ -627,7 +650,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
           }
 
       // ---- V^T operands of this tile, then request the next tile's V.
-      // The next tile's group K holds its two mask-row loads only if that tile is cut.
+      // The next tile's group K holds its two mask-row copies only if that tile is cut.
       if (kMask && mslot < 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK - 2));
       else __builtin_amdgcn_s_waitcnt(waitcnt_vm(kGroupK));
       // The reads are issued in the order the P·V MFMAs consume them, and each MFMA pair
