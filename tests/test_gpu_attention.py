@@ -110,21 +110,22 @@ def test_strided_and_broadcast(dev, D):
 
 
 @pytest.mark.parametrize("Lk", [20, 33, 57, 100, 300, 1000])
-@pytest.mark.parametrize("with_bias", [False, True])
-def test_contiguous_and_strided_key_rows_agree(dev, Lk, with_bias):
+@pytest.mark.parametrize("with_bias,D", [(False, 64), (True, 64), (False, 128)])
+def test_contiguous_and_strided_key_rows_agree(dev, Lk, with_bias, D):
     # Contiguous 64-element K/V rows are copied through per-tile buffer descriptors based at
     # the tile's rows 0 and 32 (sized to the head's last row; empty when row 32 is past it);
     # strided rows through per-load offsets. Same values, same arithmetic: bit-identical
     # outputs, including the partial last tile and Lk < 32 (an empty second descriptor).
-    case(f"contiguous vs strided K/V Lk={Lk} bias={with_bias}")
+    # Head dim 128 (wave pairs, each copying one 128-byte half of every row) likewise.
+    case(f"contiguous vs strided K/V Lk={Lk} bias={with_bias} D={D}")
     B, H, Lq = 2, 3, 130
-    q = _rand((B, H, Lq, 64), 160).to(dev)
-    kc, vc = _rand((B, H, Lk, 64), 161).to(dev), _rand((B, H, Lk, 64), 162).to(dev)
-    ks = torch.empty(B, Lk, H, 64, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
-    vs = torch.empty(B, Lk, H, 64, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+    q = _rand((B, H, Lq, D), 160).to(dev)
+    kc, vc = _rand((B, H, Lk, D), 161).to(dev), _rand((B, H, Lk, D), 162).to(dev)
+    ks = torch.empty(B, Lk, H, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+    vs = torch.empty(B, Lk, H, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
     ks.copy_(kc)
     vs.copy_(vc)
-    assert ks.stride(2) == H * 64 and kc.stride(2) == 64
+    assert ks.stride(2) == H * D and kc.stride(2) == D
     nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
     g = torch.Generator().manual_seed(Lk)
     mask = torch.rand(B, H, nqb, nkb, generator=g) < 0.7
