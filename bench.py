@@ -37,10 +37,15 @@ def _events():
 
 
 def time_fn(fn, iters=20, warmup=5):
-    """Median ms per call over `iters` back-to-back calls after `warmup` untimed ones; each
-    call is bracketed by its own HIP events on the current stream."""
-    for _ in range(warmup):
+    """Median ms per call over `iters` back-to-back calls after `warmup` untimed ones (continued
+    until at least 0.2 s of back-to-back calls, so the engine clock has settled after the
+    previous measurement); each call is bracketed by its own HIP events on the current stream."""
+    n, t0 = 0, time.perf_counter()
+    while n < warmup or (time.perf_counter() - t0 < 0.2 and n < warmup + 1000):
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     ev = [_events() for _ in range(iters)]
     torch.cuda.synchronize()
     for e0, e1 in ev:
