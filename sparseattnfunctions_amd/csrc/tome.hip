@@ -617,18 +617,12 @@ __device__ inline void add_u4(float* s, uint4 w) {
   s[4] += bf16lo(w.z); s[5] += bf16hi(w.z); s[6] += bf16lo(w.w); s[7] += bf16hi(w.w);
 }
 
-// kR merged rows per thread, rows 32 r + lane / 8 of the workgroup's 32 kR rows: the index
-// and first loads of a thread's rows are in flight together, so that one tensor keeps more
-// loads in flight per index chain (C4, one tensor, inputs larger than the last-level cache:
-// 63.4 us with one row per thread, 58.3 us with two, 68.3 us with four, where the member
-// chains of a thread's dst rows run one after the other).
-template <int kN>
-constexpr int kMergeRows = kN == 1 ? 2 : 1;
-
+// Two or three tensors: one merged row per 8 lanes; a dst row's members are loaded only
+// once its member range is known, kU at a time (clamped to the last member).
 template <int kN>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   constexpr int kU = 4;  // member loads in flight
-  constexpr int kR = kMergeRows<kN>;
+  constexpr int kR = 1;
   const sa_tome_maps& m = a.m;
   const int c8 = threadIdx.x & 7;
   const int64_t n_rows = (int64_t)a.B * a.H * m.Lm;
@@ -720,6 +714,103 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   for (int t = 0; t < kN; ++t)
     *reinterpret_cast<uint4*>(a.out[t] + b * a.o_sb[t] + h * a.o_sh[t] + (int64_t)j * a.o_sl[t] + 8 * c8) = res[t];
   }
+}
+
+// One tensor (the reference closure's merge of a single tensor): one merged row per 8 lanes,
+// with the loads in three dependent levels: (1) merged_src[j] and, for a dst row, its member
+// range from dst_ptr; (2) the row's own token and its first kU member indices; (3) those
+// members' rows, loaded only by the lanes of rows that have them. Members past the first kU
+// follow in batches of kU. C4, inputs larger than the last-level cache: 53.8 us, against
+// 58.6 us with merge_kernel's member loads (which wait for the member range inside the
+// row's branch). With three tensors this form is 2 % slower than merge_kernel.
+template <int kN>
+__global__ __launch_bounds__(256) void merge_early_kernel(MergeArgs a) {
+  constexpr int kU = 4;  // member loads in flight
+  const sa_tome_maps& m = a.m;
+  const int c8 = threadIdx.x & 7;
+  const int64_t n_rows = (int64_t)a.B * a.H * m.Lm;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+  if (row >= n_rows) return;
+  const int64_t bh = row / m.Lm;
+  const int j = (int)(row - bh * m.Lm);
+  const int64_t g = bh / a.heads_per_group;
+  const int d0 = m.text_len + m.n_src - m.r;  // first dst row
+  const int src = m.merged_src[g * m.Lm + j];
+  int lo = 0, hi = 0;
+  if (j >= d0) {
+    const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1) + (j - d0);
+    lo = ptr[0];
+    hi = ptr[1];
+  }
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const uint16_t* xb[kN];
+  uint4 w0[kN];
+#pragma unroll
+  for (int t = 0; t < kN; ++t) {
+    xb[t] = a.x[t] + b * a.x_sb[t] + h * a.x_sh[t] + 8 * c8;
+    w0[t] = *reinterpret_cast<const uint4*>(xb[t] + (int64_t)src * a.x_sl[t]);
+  }
+  const int32_t* mr = m.member_rows + g * m.r;
+  int rr[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) rr[u] = lo + u < hi ? mr[lo + u] : -1;
+  uint4 w[kU][kN];
+#pragma unroll
+  for (int u = 0; u < kU; ++u)
+#pragma unroll
+    for (int t = 0; t < kN; ++t)
+      w[u][t] = rr[u] >= 0 ? *reinterpret_cast<const uint4*>(xb[t] + (int64_t)rr[u] * a.x_sl[t])
+                           : make_uint4(0, 0, 0, 0);
+  uint4 res[kN];
+  if (lo == hi) {
+#pragma unroll
+    for (int t = 0; t < kN; ++t) res[t] = w0[t];
+  } else {
+    float s[kN][8];
+#pragma unroll
+    for (int t = 0; t < kN; ++t) {
+      const uint4 x = w0[t];
+      s[t][0] = bf16lo(x.x); s[t][1] = bf16hi(x.x); s[t][2] = bf16lo(x.y); s[t][3] = bf16hi(x.y);
+      s[t][4] = bf16lo(x.z); s[t][5] = bf16hi(x.z); s[t][6] = bf16lo(x.w); s[t][7] = bf16hi(x.w);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (lo + u < hi) {
+#pragma unroll
+        for (int t = 0; t < kN; ++t) add_u4(s[t], w[u][t]);
+      }
+    for (int p = lo + kU; p < hi; p += kU) {  // members in edge order, kU at a time
+      int rq[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) rq[u] = mr[min(p + u, hi - 1)];  // clamped: always a member
+      uint4 wq[kU][kN];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int t = 0; t < kN; ++t) wq[u][t] = *reinterpret_cast<const uint4*>(xb[t] + (int64_t)rq[u] * a.x_sl[t]);
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (p + u < hi) {
+#pragma unroll
+          for (int t = 0; t < kN; ++t) add_u4(s[t], wq[u][t]);
+        }
+    }
+    const float n = (float)(1 + hi - lo);
+#pragma unroll
+    for (int t = 0; t < kN; ++t) {
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t lo16 = __float_as_uint(round_bf16(s[t][2 * q] / n)) >> 16;
+        const uint32_t hi16 = __float_as_uint(round_bf16(s[t][2 * q + 1] / n)) & 0xffff0000u;
+        o[q] = lo16 | hi16;
+      }
+      res[t] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kN; ++t)
+    *reinterpret_cast<uint4*>(a.out[t] + b * a.o_sb[t] + h * a.o_sh[t] + (int64_t)j * a.o_sl[t] + 8 * c8) = res[t];
 }
 
 // Unmerge: out[b, h, t] = xm[b, h, row_of_token[t]].
@@ -961,12 +1052,11 @@ int launch_merge(bool unmerge, int n, const uint16_t* const* x, const int64_t* x
   SA_REQUIRE(rows * 8 / 256 < (1LL << 31), "%s: grid too large", fn);
   hipStream_t s = sa::as_stream(stream);
   const dim3 grid(grid256(rows * 8)), blk(256);
-  // merge_kernel<n>: 32 kMergeRows<n> rows per workgroup
-  auto mgrid = [&](int kr) { return dim3((unsigned)((rows + 32 * kr - 1) / (32 * kr))); };
+  // 8 lanes per merged row, 32 rows per workgroup
   if (unmerge) hipLaunchKernelGGL(unmerge_kernel, grid, blk, 0, s, a);
-  else if (n == 1) hipLaunchKernelGGL(merge_kernel<1>, mgrid(kMergeRows<1>), blk, 0, s, a);
-  else if (n == 2) hipLaunchKernelGGL(merge_kernel<2>, mgrid(kMergeRows<2>), blk, 0, s, a);
-  else hipLaunchKernelGGL(merge_kernel<3>, mgrid(kMergeRows<3>), blk, 0, s, a);
+  else if (n == 1) hipLaunchKernelGGL(merge_early_kernel<1>, grid, blk, 0, s, a);
+  else if (n == 2) hipLaunchKernelGGL(merge_kernel<2>, grid, blk, 0, s, a);
+  else hipLaunchKernelGGL(merge_kernel<3>, grid, blk, 0, s, a);
   return sa::check_launch(fn);
 }
 }  // namespace
