@@ -30,8 +30,10 @@
 // Softmax economy: the running max is only raised when a tile exceeds it by more than
 // kRescaleLog2 (then p <= 2^kRescaleLog2), so the accumulator rescale is rare; row sums
 // accumulate the bf16-rounded P pairs with v_dot2c_f32_bf16; maxima use v_max3_f32. A
-// first pass skips the max entirely (P = exp2(S * scale), exact while the row sums stay in
-// range, which is checked); items whose sums leave range are redone with the running max.
+// first pass skips the max entirely (bf16: P = exp2(S * scale); fp16, whose P has 5 exponent
+// bits: P = exp2(S * scale - m0) with m0 the row's maximum in the item's first tile), exact
+// while the row sums stay in range, which is checked; items whose sums leave range are
+// redone with the running max.
 //
 // Scheduling: a host-built work order maps dispatch slots to items so that each XCD
 // (workgroups round-robin over 8 XCDs) processes a contiguous range of heads, longest
@@ -467,6 +469,8 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // (running max, lazy rescale) otherwise.
   auto run = [&](auto safe_tag) {
     constexpr bool kSafe = decltype(safe_tag)::value;
+    // fp16 P keeps 5 exponent bits, so its fast pass subtracts a fixed per-row offset.
+    constexpr bool kOffset = !kSafe && !std::is_same<T, __bf16>::value;
 #pragma unroll
     for (int dc = 0; dc < kDC; ++dc)
 #pragma unroll
@@ -601,6 +605,26 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         }
       }
       float mu[2] = {0.f, 0.f};
+      // Row max of this tile's scaled scores (sc > 0: max(S) * sc = max(S * sc)).
+      auto tile_row_max = [&](int g) {
+        float mx = fmaxf(fmaxf(S[g][0][0], S[g][0][1]), S[g][0][2]);
+#pragma unroll
+        for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][0][e]), S[g][0][e + 1]);
+        mx = fmaxf(fmaxf(mx, S[g][0][15]), S[g][1][0]);
+#pragma unroll
+        for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][1][e]), S[g][1][e + 1]);
+        mx = fmaxf(mx, S[g][1][15]);
+        return xhalf_max(mx) * sc;
+      };
+      if (kOffset) {
+        // fp16 fast pass: the first tile's row maxima are the exp2 offsets of the whole item.
+        if (it == beg) {
+#pragma unroll
+          for (int g = 0; g < 2; ++g) m[g] = tile_row_max(g);
+        }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) mu[g] = (m[g] == -INFINITY) ? 0.f : m[g];
+      }
       if (kSafe) {
         // Row max; the running max is raised only when this tile exceeds it by more than
         // the threshold (always on the first tile, where m = -inf).
@@ -608,14 +632,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         bool raise = false;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          float mx = fmaxf(fmaxf(S[g][0][0], S[g][0][1]), S[g][0][2]);
-#pragma unroll
-          for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][0][e]), S[g][0][e + 1]);
-          mx = fmaxf(fmaxf(mx, S[g][0][15]), S[g][1][0]);
-#pragma unroll
-          for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[g][1][e]), S[g][1][e + 1]);
-          mx = fmaxf(mx, S[g][1][15]);
-          cand[g] = xhalf_max(mx) * sc;  // sc > 0
+          cand[g] = tile_row_max(g);
           raise |= cand[g] > m[g] + kRescaleLog2;
         }
         if (__ballot(raise) != 0) {
@@ -643,8 +660,8 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         for (int g = 0; g < 2; ++g)
 #pragma unroll
           for (int e = 0; e < 16; e += 2) {
-            const float p0 = fast_exp2(kSafe ? fmaf(S[g][c][e], sc, -mu[g]) : S[g][c][e] * sc);
-            const float p1 = fast_exp2(kSafe ? fmaf(S[g][c][e + 1], sc, -mu[g]) : S[g][c][e + 1] * sc);
+            const float p0 = fast_exp2(kSafe || kOffset ? fmaf(S[g][c][e], sc, -mu[g]) : S[g][c][e] * sc);
+            const float p1 = fast_exp2(kSafe || kOffset ? fmaf(S[g][c][e + 1], sc, -mu[g]) : S[g][c][e + 1] * sc);
             P[g][c][e >> 1] = E::pack(p0, p1);
             l[g] = E::dot2_ones(P[g][c][e >> 1], l[g]);
           }
@@ -704,13 +721,12 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
 
-  // fp16 P has a narrow exponent range: fp16 launches run the safe pass only.
-  constexpr bool kFast = std::is_same<T, __bf16>::value;
-  if (kFast) run(std::false_type{});
-  else run(std::true_type{});
-  // The fast pass is exact unless a row's sum left [2^-90, 2^90] (scores far from 0, where
-  // exp2 would lose range) or an accumulator overflowed; then redo the item safely.
-  if (kFast && cnt > beg) {
+  run(std::false_type{});
+  // The fast pass is exact unless a row's sum left [2^-90, 2^90] (bf16: scores far from 0,
+  // where exp2 would lose range; fp16: a later tile's score more than 2^16 times the first
+  // tile's maximum, where P rounds to inf) or an accumulator overflowed; then redo the item
+  // safely.
+  if (cnt > beg) {
     bool bad = false;
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
@@ -952,10 +968,12 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
   auto issue_k = [&](int kb) { copy_share(khead, kbytes, krow, kgo, kl, kb); };
   auto issue_v = [&](int kb) { copy_share(vhead, vbytes, vrow, vgo, vl, kb); };
 
-  // One pass over the list. Fast pass (kSafe = false): P = exp2(S) with no max, checked by
-  // the caller; safe pass: running max with lazy rescale.
+  // One pass over the list. Fast pass (kSafe = false): P = exp2(S) with no max (fp16: minus
+  // the row's maximum over the first tile), checked by the caller; safe pass: running max
+  // with lazy rescale.
   auto run = [&](auto safe_tag) {
     constexpr bool kSafe = decltype(safe_tag)::value;
+    constexpr bool kOffset = !kSafe && !std::is_same<T, __bf16>::value;
 #pragma unroll
     for (int dc = 0; dc < kDC; ++dc) acc[dc] = sa_f32x16{};
     m = -INFINITY;
@@ -999,7 +1017,8 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
       }
       const float sc = a.scale_log2;
       float mu = 0.f;
-      if (kSafe) {
+      // Row max of this tile's scaled scores (sc > 0: max(S) * sc = max(S * sc)).
+      auto tile_row_max = [&]() {
         float mx = fmaxf(fmaxf(S[0][0], S[0][1]), S[0][2]);
 #pragma unroll
         for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[0][e]), S[0][e + 1]);
@@ -1007,7 +1026,14 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
 #pragma unroll
         for (int e = 1; e < 15; e += 2) mx = fmaxf(fmaxf(mx, S[1][e]), S[1][e + 1]);
         mx = fmaxf(mx, S[1][15]);
-        const float cand = xhalf_max(mx) * sc;  // sc > 0
+        return xhalf_max(mx) * sc;
+      };
+      if (kOffset) {  // fp16 fast pass: the first tile's row max is the item's exp2 offset
+        if (it == 0) m = tile_row_max();
+        mu = m == -INFINITY ? 0.f : m;
+      }
+      if (kSafe) {
+        const float cand = tile_row_max();
         if (__ballot(cand > m + kRescaleLog2) != 0) {
           const float m_new = fmaxf(m, cand);
           // A row with no key yet (m_new = -inf) has nothing to rescale.
@@ -1024,8 +1050,8 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int e = 0; e < 16; e += 2) {
-          const float p0 = fast_exp2(kSafe ? fmaf(S[c][e], sc, -mu) : S[c][e] * sc);
-          const float p1 = fast_exp2(kSafe ? fmaf(S[c][e + 1], sc, -mu) : S[c][e + 1] * sc);
+          const float p0 = fast_exp2(kSafe || kOffset ? fmaf(S[c][e], sc, -mu) : S[c][e] * sc);
+          const float p1 = fast_exp2(kSafe || kOffset ? fmaf(S[c][e + 1], sc, -mu) : S[c][e + 1] * sc);
           P[c][e >> 1] = E::pack(p0, p1);
           l = E::dot2_ones(P[c][e >> 1], l);
         }
@@ -1072,12 +1098,11 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
 
-  constexpr bool kFast = std::is_same<T, __bf16>::value;
-  if (kFast) {
+  {
     run(std::false_type{});
-    // The fast pass is exact unless a row's sum left [2^-90, 2^90] or an accumulator
-    // overflowed; then the pair redoes its block with the safe pass. Both waves decide
-    // together (their barriers must match).
+    // The fast pass is exact unless a row's sum left [2^-90, 2^90] (fp16: P rounded to inf)
+    // or an accumulator overflowed; then the pair redoes its block with the safe pass. Both
+    // waves decide together (their barriers must match).
     bool bad = false;
     if (cnt > 0) {
       const float l_tot = xhalf_sum(l);
@@ -1095,8 +1120,6 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
     wg_barrier();
     const bool redo = (redo_lds[0] | redo_lds[1]) != 0;
     if (redo) run(std::true_type{});
-  } else {
-    run(std::true_type{});
   }
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).

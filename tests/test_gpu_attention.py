@@ -356,8 +356,9 @@ def test_fp16_and_head_dim_128_key_bias(dev, dtype, D):
 
 
 def test_fp16_large_scores_use_running_max(dev):
-    # fp16 P cannot hold exp2 of raw scores of several hundred: fp16 launches always subtract
-    # the running row maximum (the bf16 fast pass would overflow fp16).
+    # fp16 P cannot hold exp2 of raw scores of several hundred: the fp16 fast pass subtracts
+    # each row's maximum over the first tile, and rows whose later tiles exceed it by more
+    # than 2^16 are redone with the running maximum.
     case("fp16 large scores")
     q = (_rand((1, 1, 128, 64), 140) * 6).half()
     k = (_rand((1, 1, 128, 64), 141) * 6).half()
@@ -365,6 +366,34 @@ def test_fp16_large_scores_use_running_max(dev):
     mask = torch.ones(1, 1, 2, 2, dtype=torch.bool)
     out = block_sparse_triton_fn(q.to(dev), k.to(dev), v.to(dev), mask.to(dev), 1 / 8)
     _check(out, masked_attention(q, k, v, mask, 1 / 8))
+
+
+@pytest.mark.parametrize("large_first", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_fp16_offset_from_first_tile(dev, large_first, D):
+    # Key block 0 small, key block 1 with scores ~35 (log2 units) higher: with the large block
+    # first, its row maxima make every exp2 argument <= 0; with the small block first, the
+    # second tile's P exceeds fp16's range (P = inf, row sum inf) and the item is redone
+    # with the running maximum. Both must match the fp64 oracle.
+    case(f"fp16 first-tile offset large_first={large_first} D={D}")
+    q = _rand((1, 2, 128, D), 150)
+    k = _rand((1, 2, 128, D), 151)
+    small, large = slice(0, 64), slice(64, 128)
+    if large_first:
+        small, large = large, small
+    k[:, :, small] *= 0.01
+    k[:, :, large] *= 10.0 * math.sqrt(64 / D)
+    q, k = q.half(), k.half()
+    v = _rand((1, 2, 128, D), 152, torch.float16)
+    mask = torch.ones(1, 2, 2, 2, dtype=torch.bool)
+    # Lists hold key block 0 then 1, so the small block is the first tile unless large_first.
+    out = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), dense_kv_list(1, 2, 2, 2, dev), 1 / 8)
+    _check(out, masked_attention(q, k, v, mask, 1 / 8))
+    if D == 128:  # plain lists at head dim 128 run the wave-pair kernel; the key-bias variant does not
+        zero = torch.zeros(1, 2, 128, dtype=torch.float32, device=dev)
+        outb = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), dense_kv_list(1, 2, 2, 2, dev), 1 / 8,
+                                      key_bias=zero)
+        _check(outb, masked_attention(q, k, v, mask, 1 / 8))
 
 
 def test_mixed_or_fp64_dtypes_rejected(dev):
