@@ -498,7 +498,7 @@ def _split_parts(n_items, max_cnt, D=64):
     (1, 2, 200, 8192, 64, torch.bfloat16, 1.0),   # partial last query block
     (2, 3, 64, 4500, 64, torch.bfloat16, 1.0),    # partial last key block
     (1, 2, 64, 4096, 128, torch.bfloat16, 1.0),   # head dim 128
-    (1, 2, 100, 4096, 64, torch.float16, 1.0),    # fp16 (running maximum in every part)
+    (1, 2, 100, 4096, 64, torch.float16, 1.0),    # fp16 (each part offsets by its first tile's row maxima)
     (1, 2, 128, 6000, 64, torch.bfloat16, 8.0),   # scores of several hundred: parts redo safely
 ])
 def test_key_range_split_dense(dev, B, H, Lq, Lk, D, dtype, amp):
