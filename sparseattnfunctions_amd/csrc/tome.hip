@@ -622,51 +622,29 @@ __device__ inline void add_u4(float* s, uint4 w) {
 template <int kN>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   constexpr int kU = 4;  // member loads in flight
-  constexpr int kR = 1;
   const sa_tome_maps& m = a.m;
   const int c8 = threadIdx.x & 7;
   const int64_t n_rows = (int64_t)a.B * a.H * m.Lm;
-  const int d0 = m.text_len + m.n_src - m.r;  // first dst row
-  int64_t rows[kR], bhs[kR];
-  int js[kR], srcs[kR], los[kR], his[kR];
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    rows[r] = ((int64_t)blockIdx.x * kR + r) * 32 + (threadIdx.x >> 3);
-    const int64_t rc = rows[r] < n_rows ? rows[r] : n_rows - 1;
-    bhs[r] = rc / m.Lm;
-    js[r] = (int)(rc - bhs[r] * m.Lm);
-    const int64_t gr = bhs[r] / a.heads_per_group;
-    srcs[r] = m.merged_src[gr * m.Lm + js[r]];
-    los[r] = his[r] = 0;
-    if (js[r] >= d0) {
-      const int32_t* ptr = m.dst_ptr + gr * (m.n_dst + 1) + (js[r] - d0);
-      los[r] = ptr[0];
-      his[r] = ptr[1];
-    }
-  }
-  uint4 w0s[kR][kN];
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    const int64_t b = bhs[r] / a.H, h = bhs[r] - b * a.H;
-#pragma unroll
-    for (int t = 0; t < kN; ++t)
-      w0s[r][t] = *reinterpret_cast<const uint4*>(a.x[t] + b * a.x_sb[t] + h * a.x_sh[t] + 8 * c8 +
-                                                   (int64_t)srcs[r] * a.x_sl[t]);
-  }
-#pragma unroll
-  for (int r = 0; r < kR; ++r) {
-  if (rows[r] >= n_rows) break;
-  const int64_t bh = bhs[r];
-  const int j = js[r];
-  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+  if (row >= n_rows) return;
+  const int64_t bh = row / m.Lm;
+  const int j = (int)(row - bh * m.Lm);
   const int64_t g = bh / a.heads_per_group;
-  const int lo = los[r], hi = his[r];
+  const int d0 = m.text_len + m.n_src - m.r;  // first dst row
+  const int src = m.merged_src[g * m.Lm + j];
+  int lo = 0, hi = 0;
+  if (j >= d0) {
+    const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1) + (j - d0);
+    lo = ptr[0];
+    hi = ptr[1];
+  }
+  const int64_t b = bh / a.H, h = bh - b * a.H;
   const uint16_t* xb[kN];
   uint4 w0[kN];
 #pragma unroll
   for (int t = 0; t < kN; ++t) {
     xb[t] = a.x[t] + b * a.x_sb[t] + h * a.x_sh[t] + 8 * c8;
-    w0[t] = w0s[r][t];
+    w0[t] = *reinterpret_cast<const uint4*>(xb[t] + (int64_t)src * a.x_sl[t]);
   }
   uint4 res[kN];
   if (lo == hi) {
@@ -713,7 +691,6 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 #pragma unroll
   for (int t = 0; t < kN; ++t)
     *reinterpret_cast<uint4*>(a.out[t] + b * a.o_sb[t] + h * a.o_sh[t] + (int64_t)j * a.o_sl[t] + 8 * c8) = res[t];
-  }
 }
 
 // One tensor (the reference closure's merge of a single tensor): one merged row per 8 lanes,
