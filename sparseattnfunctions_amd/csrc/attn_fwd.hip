@@ -1098,29 +1098,27 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
 
-  {
-    run(std::false_type{});
-    // The fast pass is exact unless a row's sum left [2^-90, 2^90] (fp16: P rounded to inf)
-    // or an accumulator overflowed; then the pair redoes its block with the safe pass. Both
-    // waves decide together (their barriers must match).
-    bool bad = false;
-    if (cnt > 0) {
-      const float l_tot = xhalf_sum(l);
-      bad = !(l_tot >= 0x1p-90f && l_tot <= 0x1p90f);
-      float amax = 0.f;
+  run(std::false_type{});
+  // The fast pass is exact unless a row's sum left [2^-90, 2^90] (fp16: P rounded to inf)
+  // or an accumulator overflowed; then the pair redoes its block with the safe pass. Both
+  // waves decide together (their barriers must match).
+  bool bad = false;
+  if (cnt > 0) {
+    const float l_tot = xhalf_sum(l);
+    bad = !(l_tot >= 0x1p-90f && l_tot <= 0x1p90f);
+    float amax = 0.f;
 #pragma unroll
-      for (int dc = 0; dc < kDC; ++dc)
+    for (int dc = 0; dc < kDC; ++dc)
 #pragma unroll
-        for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][e])), fabsf(acc[dc][e + 1]));
-      bad |= !(amax <= 3.0e38f);
-    }
-    const int wave_bad = __ballot(bad) != 0;
-    if (lane == 0) redo_lds[g] = wave_bad;
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-    wg_barrier();
-    const bool redo = (redo_lds[0] | redo_lds[1]) != 0;
-    if (redo) run(std::true_type{});
+      for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][e])), fabsf(acc[dc][e + 1]));
+    bad |= !(amax <= 3.0e38f);
   }
+  const int wave_bad = __ballot(bad) != 0;
+  if (lane == 0) redo_lds[g] = wave_bad;
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  wg_barrier();
+  const bool redo = (redo_lds[0] | redo_lds[1]) != 0;
+  if (redo) run(std::true_type{});
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
   const float l_tot = xhalf_sum(l);

@@ -371,18 +371,22 @@ __global__ __launch_bounds__(256, 2) void match_mfma_kernel(MatchArgs a) {
         for (int sb = 0; sb < 4; ++sb)
           acc[db][sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aop[db], bop[sb][j], acc[db][sb], 0, 0, 0);
     }
+    // A lane meets its dst rows in ascending order (tiles ascending, d = d0 + 16 db + 4 kg + i
+    // within a tile), so a tie never replaces the lower index: `better` reduces to v > best.
+    // Rows past d_hi exist only in the range's last tile.
+    const bool full = d0 + kMfDst <= d_hi;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = d0 + 16 * db + 4 * kg + i;
-        if (d < d_hi) {
+        if (full || d < d_hi) {
 #pragma unroll
-          for (int sb = 0; sb < 4; ++sb)
-            if (better(acc[db][sb][i], d, best[sb], bidx[sb])) {
-              best[sb] = acc[db][sb][i];
-              bidx[sb] = d;
-            }
+          for (int sb = 0; sb < 4; ++sb) {
+            const bool gt = acc[db][sb][i] > best[sb];
+            best[sb] = gt ? acc[db][sb][i] : best[sb];
+            bidx[sb] = gt ? d : bidx[sb];
+          }
         }
       }
     if (more) store_tile(buf ^ 1);
