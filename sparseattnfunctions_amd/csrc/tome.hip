@@ -576,28 +576,72 @@ __global__ void fill_kernel(sa_tome_maps m) {
   m.members[g * m.r + m.dst_ptr[g * (m.n_dst + 1) + d] + p] = e;
 }
 
-// Members of each dst in ascending edge order (insertion sort of its short segment), then
-// the token row of each member (member_rows): the merge reads one index per member.
-__global__ void sort_kernel(sa_tome_maps m) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Members of each dst in ascending edge order, then the token row of each member
+// (member_rows): the merge reads one index per member. One wave per dst: the members are
+// distinct edge positions, so each one's place is the number of smaller members, counted
+// against the whole segment in 64-member chunks (broadcast with readlane); a segment of more
+// than kSortMaxMembers (64 chunks' ranks in registers) is insertion-sorted by lane 0.
+constexpr int kSortChunks = 16;
+constexpr int kSortMaxMembers = 64 * kSortChunks;
+
+__global__ __launch_bounds__(256) void sort_kernel(sa_tome_maps m) {
+  const int lane = threadIdx.x & 63;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;  // (group, dst) of this wave
   if (i >= (int64_t)m.G * m.n_dst) return;
   const int64_t g = i / m.n_dst;
   const int d = (int)(i - g * m.n_dst);
   const int32_t* ptr = m.dst_ptr + g * (m.n_dst + 1);
   int32_t* mem = m.members + g * m.r;
-  const int lo = ptr[d], hi = ptr[d + 1];
-  for (int x = lo + 1; x < hi; ++x) {
-    const int v = mem[x];
-    int y = x - 1;
-    while (y >= lo && mem[y] > v) {
-      mem[y + 1] = mem[y];
-      --y;
-    }
-    mem[y + 1] = v;
-  }
+  const int lo = __builtin_amdgcn_readfirstlane(ptr[d]), hi = __builtin_amdgcn_readfirstlane(ptr[d + 1]);
+  const int n = hi - lo;
+  if (n <= 0) return;
   const int32_t* edge = m.edge + g * m.n_src;
   int32_t* rows = m.member_rows + g * m.r;
-  for (int x = lo; x < hi; ++x) rows[x] = m.text_len + m.a_idx[edge[mem[x]]];
+  if (n > kSortMaxMembers) {
+    if (lane == 0) {
+      for (int x = lo + 1; x < hi; ++x) {
+        const int v = mem[x];
+        int y = x - 1;
+        while (y >= lo && mem[y] > v) {
+          mem[y + 1] = mem[y];
+          --y;
+        }
+        mem[y + 1] = v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    for (int x = lo + lane; x < hi; x += 64) rows[x] = m.text_len + m.a_idx[edge[mem[x]]];
+    return;
+  }
+  const int nc = (n + 63) >> 6;  // chunks of the segment (wave-uniform)
+  int val[kSortChunks], rank[kSortChunks];
+#pragma unroll
+  for (int c = 0; c < kSortChunks; ++c) {
+    val[c] = c < nc && 64 * c + lane < n ? mem[lo + 64 * c + lane] : INT_MAX;
+    rank[c] = 0;
+  }
+#pragma unroll
+  for (int cj = 0; cj < kSortChunks; ++cj) {
+    if (cj < nc) {
+      const int nj = min(64, n - 64 * cj);
+      for (int j = 0; j < nj; ++j) {
+        const int u = __builtin_amdgcn_readlane(val[cj], j);
+#pragma unroll
+        for (int c = 0; c < kSortChunks; ++c)
+          if (c < nc) rank[c] += u < val[c];
+      }
+    }
+  }
+  // Every member was read into val before any store below (the stores depend on the ranks,
+  // which depend on every lane's value).
+#pragma unroll
+  for (int c = 0; c < kSortChunks; ++c) {
+    if (c < nc && 64 * c + lane < n) {
+      mem[lo + rank[c]] = val[c];
+      rows[lo + rank[c]] = m.text_len + m.a_idx[edge[val[c]]];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -931,7 +975,7 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
   hipLaunchKernelGGL(scan_kernel, dim3(m.G), dim3(1024), 0, s, m);
   if (m.r > 0) {
     hipLaunchKernelGGL(fill_kernel, dim3(grid256((int64_t)m.G * m.r)), dim3(256), 0, s, m);
-    hipLaunchKernelGGL(sort_kernel, dim3(grid256((int64_t)m.G * m.n_dst)), dim3(256), 0, s, m);
+    hipLaunchKernelGGL(sort_kernel, dim3(grid256((int64_t)m.G * m.n_dst * 64)), dim3(256), 0, s, m);  // a wave per dst
   }
   return sa::check_launch(fn);
 }
