@@ -484,8 +484,10 @@ __global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, int splits) {
       keys[e] = j < j_hi ? ((uint64_t)order_bits(nm[j]) << 32) | (uint32_t)~j : 0ull;
     }
     __syncthreads();
-    const int n = min(kRankTile, j_hi - t0);
-    for (int e = 0; e < n; e += 2) count += (keys[e] > mine) + (keys[e + 1] > mine);
+    // The whole tile: padding keys are 0 and never count. Unrolled so that many LDS reads
+    // are in flight per wait.
+#pragma unroll 16
+    for (int e = 0; e < kRankTile; e += 2) count += (keys[e] > mine) + (keys[e + 1] > mine);
   }
   if (s < m.n_src && count) atomicAdd(&m.rank[(int64_t)g * m.n_src + s], count);
 }
@@ -967,7 +969,8 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
   const int64_t n0 = (int64_t)m.G * std::max(m.n_src, m.n_dst);
   hipLaunchKernelGGL(combine_kernel, dim3(grid256(n0)), dim3(256), 0, s, ma);
   if (m.n_src > 0) {
-    const int rsplit = std::max(1, std::min(16, m.n_src / 1024));
+    // Key ranges of at most one staged tile each (the rank loop always runs a whole tile).
+    const int rsplit = std::max(1, std::min(64, (m.n_src + kRankTile - 1) / kRankTile));
     hipLaunchKernelGGL(rank_kernel, dim3((m.n_src + 255) / 256, m.G, rsplit), dim3(256), 0, s, m, rsplit);
     hipLaunchKernelGGL(edge_kernel, dim3(grid256((int64_t)m.G * m.n_src)), dim3(256), 0, s, m);
   }
