@@ -354,41 +354,36 @@ __global__ __launch_bounds__(256, 2) void match_mfma_kernel(MatchArgs a) {
   for (int d0 = d_lo; d0 < d_hi; d0 += kMfDst) {  // workgroup-uniform trip count
     const bool more = d0 + kMfDst < d_hi;
     if (more) load_tile(d0 + kMfDst);
-    sa_f32x4 acc[4][4];  // [dst block][src block]
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int sb = 0; sb < 4; ++sb) acc[db][sb] = sa_f32x4{0.f, 0.f, 0.f, 0.f};
-    const float* t = dl[buf] + m16 * kMfLd + kg;
-#pragma unroll
-    for (int j = 0; j < kMfC / 4; ++j) {
-      float aop[4];
-#pragma unroll
-      for (int db = 0; db < 4; ++db) aop[db] = t[16 * db * kMfLd + 4 * j];
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int sb = 0; sb < 4; ++sb)
-          acc[db][sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aop[db], bop[sb][j], acc[db][sb], 0, 0, 0);
-    }
     // A lane meets its dst rows in ascending order (tiles ascending, d = d0 + 16 db + 4 kg + i
     // within a tile), so a tie never replaces the lower index: `better` reduces to v > best.
-    // Rows past d_hi exist only in the range's last tile.
+    // Rows past d_hi exist only in the range's last tile. Dst block db's maxima are taken
+    // while block db + 1's MFMAs run (they do not depend on each other).
     const bool full = d0 + kMfDst <= d_hi;
+    const float* t = dl[buf] + m16 * kMfLd + kg;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db) {
+      sa_f32x4 acc[4];  // [src block]
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) acc[sb] = sa_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kMfC / 4; ++j) {
+        const float aop = t[16 * db * kMfLd + 4 * j];
+#pragma unroll
+        for (int sb = 0; sb < 4; ++sb) acc[sb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aop, bop[sb][j], acc[sb], 0, 0, 0);
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = d0 + 16 * db + 4 * kg + i;
         if (full || d < d_hi) {
 #pragma unroll
           for (int sb = 0; sb < 4; ++sb) {
-            const bool gt = acc[db][sb][i] > best[sb];
-            best[sb] = gt ? acc[db][sb][i] : best[sb];
+            const bool gt = acc[sb][i] > best[sb];
+            best[sb] = gt ? acc[sb][i] : best[sb];
             bidx[sb] = gt ? d : bidx[sb];
           }
         }
       }
+    }
     if (more) store_tile(buf ^ 1);
     __syncthreads();
     buf ^= 1;
