@@ -68,6 +68,38 @@ def test_small_pipeline_bit_exact(dev, mode):
             assert torch.equal(_tome.unmerge(xm, maps, hpg).cpu(), native.tome_unmerge(xm.cpu(), want, hpg))
 
 
+def test_crowded_dsts_bit_exact(dev):
+    # Every src row equals one of two unit vectors u, w and every dst row is u except one
+    # that is w: all u-srcs pick the first dst (ties go to the lowest index), all w-srcs the
+    # w dst. With every src merged, one dst holds 7 860 members (more than 1 024: the member
+    # sort's serial path) and the other 300 (several 64-member chunks).
+    case("tome crowded dsts")
+    geom = Geometry(text_len=226, T=9, Hp=30, Wp=45)
+    a, b = _tome.partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1, dev)
+    oa, ob = native.tome_partition(geom.T, geom.Hp, geom.Wp, 2, 2, 1)
+    n_video = geom.T * geom.Hp * geom.Wp
+    g = torch.Generator().manual_seed(11)
+    u, w = torch.randn(2, 64, generator=g)
+    u, w = u / u.norm(), w / w.norm()
+    metric = u.repeat(1, n_video, 1)  # [1, N, 64]
+    w_src = oa[torch.randperm(oa.numel(), generator=g)[:300]].long()
+    metric[0, w_src] = w
+    metric[0, ob[5].long()] = w
+    r = oa.numel()
+    maps = _tome.match(metric.to(dev), a, b, r, geom.text_len)
+    want = native.tome_match(metric, oa, ob, r, geom.text_len)
+    _maps_equal(maps, want)
+    cnt = maps.dst_cnt.cpu()[0]
+    assert cnt[0].item() == oa.numel() - 300 and cnt[5].item() == 300
+    ptr, mem, dst = maps.dst_ptr.cpu(), maps.members.cpu(), maps.dst_idx.cpu()
+    for d in (0, 5):
+        seg = mem[0, ptr[0, d]:ptr[0, d + 1]]
+        assert torch.equal(seg, (dst[0, :r] == d).nonzero().flatten().int()), d
+    q = cogvideox_qkv(6, B=1, H=1, geom=geom)[0]
+    xm = _tome.merge(q.to(dev), maps, 1)
+    assert torch.equal(xm.cpu(), native.tome_merge(q, want, oa, ob, r, geom.text_len, 1))
+
+
 def _misaligned(x):
     """A copy of x whose base is 4 bytes past a 16-byte boundary (contiguous)."""
     buf = torch.empty(x.numel() + 4, dtype=x.dtype, device=x.device)
