@@ -663,7 +663,7 @@ int sa_tome_metric(const uint16_t* k, const int64_t k_strides[3], const uint16_t
  * the same arithmetic as sa_tome_metric's last step. */
 int sa_tome_normalize(const float* metric, int64_t rows, int C, float* out, void* stream);
 
-/* Workspace bytes needed by sa_tome_match. */
+/* Workspace bytes needed by sa_tome_match (the workspace must be 8-byte aligned). */
 int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes);
 
 /*
@@ -678,10 +678,11 @@ int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, void* workspac
 /*
  * sa_tome_match without a workspace argument and without any allocation. No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops). The split partials live in a device array inside the library
- * (one 16 MiB copy per GPU, held until the process ends); calls whose partials,
- * G * splits * max(n_src, 1) * 8 bytes with splits <= 16 (sa_tome_match_workspace), exceed it
- * fail with SA_ERR_INVALID. Every call on one GPU shares that array: calls that overlap on
+ * capture, tight serving loops). The match's split partials and the rank's sorted key tiles
+ * live in a device array inside the library (one 16 MiB copy per GPU, held until the process
+ * ends); calls that need more than that -- max(G * splits * max(n_src, 1), G * n_src rounded
+ * up to 1024) * 8 bytes with splits <= 16, the figure sa_tome_match_workspace returns -- fail
+ * with SA_ERR_INVALID. Every call on one GPU shares that array: calls that overlap on
  * one GPU (on different streams or host threads) race and must be serialised by the caller.
  * Results are identical to sa_tome_match's.
  */

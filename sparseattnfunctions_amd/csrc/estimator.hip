@@ -267,42 +267,9 @@ __global__ __launch_bounds__(256) void energy_list_kernel(EnergyArgs a) {
   }
   int rank[NCH];  // rank path: position of this lane's entry e in the order
   if constexpr (kSort) {
-    // Bitonic network, descending. Element i = 64 e + lane of the padded row sits in
-    // register e of lane `lane`: partners in the same lane (i ^ j, j >= 64) are exchanged
-    // in registers, partners in other lanes (j < 64) through shuffles. Sorted position p
-    // then holds the p-th key, and the key gives back its value and column.
-#pragma unroll
-    for (int k = 2; k <= NSORT; k <<= 1) {
-#pragma unroll
-      for (int j = k >> 1; j > 0; j >>= 1) {
-        if (j >= 64) {
-          const int je = j >> 6;
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            if (e & je) continue;
-            // pair (i, i + j) in one lane; descending block when (i & k) == 0 (k > 64 here)
-            const bool desc = ((64 * e) & k) == 0;
-            const uint64_t x = key[e], y = key[e | je];
-            const bool first_x = (x > y) == desc;
-            key[e] = first_x ? x : y;
-            key[e | je] = first_x ? y : x;
-          }
-        } else {
-          const bool lower = (lane & j) == 0;
-#pragma unroll
-          for (int e = 0; e < E; ++e) {
-            const bool desc = (((64 * e) | lane) & k) == 0;
-            const uint64_t x = key[e];
-            const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, j);
-            const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j);
-            const uint64_t y = ((uint64_t)yhi << 32) | ylo;
-            // the lower index of a descending pair (or the upper of an ascending one) takes
-            // the larger key
-            key[e] = (lower == desc) == (x > y) ? x : y;
-          }
-        }
-      }
-    }
+    // Bitonic network, descending (sa_wave_bitonic_desc): sorted position p then holds the
+    // p-th key, and the key gives back its value and column.
+    sa_wave_bitonic_desc<E>(key, lane);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int p = 64 * e + lane;

@@ -61,3 +61,44 @@ typedef float sa_f32x16 __attribute__((ext_vector_type(16)));
 typedef float sa_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint16_t sa_u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t sa_u16x4 __attribute__((ext_vector_type(4)));
+
+// Bitonic sort, descending, of the 64 * E keys of one wave: element i = 64 e + lane sits in
+// register e of lane `lane`. Partners in the same lane (i ^ j, j >= 64) are exchanged in
+// registers, partners in other lanes (j < 64) through shuffles; afterwards sorted position p
+// holds the p-th largest key. E is a power of two.
+template <int E>
+__device__ inline void sa_wave_bitonic_desc(uint64_t (&key)[E], int lane) {
+  constexpr int N = 64 * E;
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+        const int je = j >> 6;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if (e & je) continue;
+          // pair (i, i + j) in one lane; descending block when (i & k) == 0 (k > 64 here)
+          const bool desc = ((64 * e) & k) == 0;
+          const uint64_t x = key[e], y = key[e | je];
+          const bool first_x = (x > y) == desc;
+          key[e] = first_x ? x : y;
+          key[e | je] = first_x ? y : x;
+        }
+      } else {
+        const bool lower = (lane & j) == 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const bool desc = (((64 * e) | lane) & k) == 0;
+          const uint64_t x = key[e];
+          const uint32_t ylo = (uint32_t)__shfl_xor((int)(uint32_t)x, j);
+          const uint32_t yhi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j);
+          const uint64_t y = ((uint64_t)yhi << 32) | ylo;
+          // the lower index of a descending pair (or the upper of an ascending one) takes the
+          // larger key
+          key[e] = (lower == desc) == (x > y) ? x : y;
+        }
+      }
+    }
+  }
+}

@@ -38,7 +38,7 @@ constexpr int kMTile = 128;      // src rows per match workgroup, dst columns pe
 constexpr int kMChunk = 16;      // channels staged in LDS per step
 constexpr int kMLd = kMTile + 4;  // channel-major LDS row (16-byte aligned; 4-bank offset per row)
 constexpr int kMMaxSplits = 16;  // dst splits of the match grid
-constexpr int kRankTile = 1024;  // keys staged per rank step
+constexpr int kRankTile = 256;   // keys per sorted rank tile
 
 __device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -435,7 +435,7 @@ struct MapArgs {
 };
 
 // Combine dst splits in ascending order (ties keep the lower split = lower dst) and zero
-// the counters of the later passes.
+// the dst counters of the later passes.
 __global__ void combine_kernel(MapArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const sa_tome_maps& m = a.m;
@@ -452,7 +452,6 @@ __global__ void combine_kernel(MapArgs a) {
     }
     m.node_max[i] = bv;
     m.node_idx[i] = bi;
-    m.rank[i] = 0;
   }
   if (i < (int64_t)m.G * m.n_dst) {
     m.dst_cnt[i] = 0;
@@ -462,29 +461,68 @@ __global__ void combine_kernel(MapArgs a) {
 
 // rank[s] = #{s' : node_max[s'] ranks before node_max[s]} (descending value, then position).
 // Composite keys (order_bits << 32 | ~position) are distinct and larger exactly when earlier
-// in that order, so each comparison is one unsigned 64-bit compare; padding keys are 0.
-__global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, int splits) {
-  __shared__ __attribute__((aligned(16))) uint64_t keys[kRankTile];
+// in that order; keys of positions past n_src are 0, below every real key. The keys of each
+// group are cut into tiles of kRankTile, each sorted descending by one wave
+// (rank_sort_kernel); a key's rank is then the sum over the tiles of the number of larger
+// keys, a binary search in each sorted tile (rank_kernel).
+constexpr int kRankE = kRankTile / 64;   // keys per lane of a tile sort
+constexpr int kRankChunkTiles = 32;       // sorted tiles staged in LDS at once (64 KB)
+
+__device__ inline uint64_t rank_key(const float* nm, int j, int n) {
+  return j < n ? ((uint64_t)order_bits(nm[j]) << 32) | (uint32_t)~j : 0ull;
+}
+
+__global__ __launch_bounds__(64) void rank_sort_kernel(sa_tome_maps m, uint64_t* sorted) {
+  const int lane = threadIdx.x, t = blockIdx.x, g = blockIdx.y;
+  const float* nm = m.node_max + (int64_t)g * m.n_src;
+  uint64_t key[kRankE];
+#pragma unroll
+  for (int e = 0; e < kRankE; ++e) key[e] = rank_key(nm, t * kRankTile + 64 * e + lane, m.n_src);
+  sa_wave_bitonic_desc<kRankE>(key, lane);
+  uint64_t* out = sorted + ((int64_t)g * gridDim.x + t) * kRankTile;
+#pragma unroll
+  for (int e = 0; e < kRankE; ++e) out[64 * e + lane] = key[e];
+}
+
+// The keys above `mine` form a prefix of a descending tile; its length by binary search.
+__device__ inline int rank_prefix(const uint64_t* tile, uint64_t mine) {
+  int p = 0;
+#pragma unroll
+  for (int step = kRankTile / 2; step > 0; step >>= 1)
+    if (tile[p + step - 1] > mine) p += step;
+  return p == kRankTile - 1 && tile[kRankTile - 1] > mine ? kRankTile : p;
+}
+
+__global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, const uint64_t* sorted, int n_tiles) {
+  __shared__ __attribute__((aligned(16))) uint64_t keys[kRankChunkTiles * kRankTile];
   const int g = blockIdx.y;
   const int s = blockIdx.x * 256 + threadIdx.x;
-  const float* nm = m.node_max + (int64_t)g * m.n_src;
-  const uint64_t mine = s < m.n_src ? ((uint64_t)order_bits(nm[s]) << 32) | (uint32_t)~s : ~0ull;
-  const int per = (m.n_src + splits - 1) / splits;
-  const int j_lo = blockIdx.z * per, j_hi = min(m.n_src, j_lo + per);
+  const uint64_t mine = rank_key(m.node_max + (int64_t)g * m.n_src, s, m.n_src);
+  const uint64_t* src = sorted + (int64_t)g * n_tiles * kRankTile;
   int count = 0;
-  for (int t0 = j_lo; t0 < j_hi; t0 += kRankTile) {
+  for (int t0 = 0; t0 < n_tiles; t0 += kRankChunkTiles) {
+    const int nt = min(kRankChunkTiles, n_tiles - t0);
     __syncthreads();
-    for (int e = threadIdx.x; e < kRankTile; e += 256) {
-      const int j = t0 + e;
-      keys[e] = j < j_hi ? ((uint64_t)order_bits(nm[j]) << 32) | (uint32_t)~j : 0ull;
+    // Tiles past n_tiles are staged as 0 keys (they count nothing), so the searches below
+    // need no guard: one independent search per staged tile, their LDS reads overlapping.
+    {
+      // kPer 16-byte loads (two keys each) per thread, all in flight before the stores.
+      constexpr int kPer = kRankChunkTiles * kRankTile / 2 / 256;  // key pairs per thread
+      const uint4* src4 = reinterpret_cast<const uint4*>(src + (int64_t)t0 * kRankTile);
+      uint4 w[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int e2 = threadIdx.x + 256 * u;  // key pair e2 = keys 2 e2, 2 e2 + 1
+        w[u] = 2 * e2 < nt * kRankTile ? src4[e2] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) reinterpret_cast<uint4*>(keys)[threadIdx.x + 256 * u] = w[u];
     }
     __syncthreads();
-    // The whole tile: padding keys are 0 and never count. Unrolled so that many LDS reads
-    // are in flight per wait.
-#pragma unroll 16
-    for (int e = 0; e < kRankTile; e += 2) count += (keys[e] > mine) + (keys[e + 1] > mine);
+#pragma unroll
+    for (int t = 0; t < kRankChunkTiles; ++t) count += rank_prefix(keys + t * kRankTile, mine);
   }
-  if (s < m.n_src && count) atomicAdd(&m.rank[(int64_t)g * m.n_src + s], count);
+  if (s < m.n_src) m.rank[(int64_t)g * m.n_src + s] = count;
 }
 
 // edge[g][rank[s]] = s.
@@ -964,9 +1002,11 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
   const int64_t n0 = (int64_t)m.G * std::max(m.n_src, m.n_dst);
   hipLaunchKernelGGL(combine_kernel, dim3(grid256(n0)), dim3(256), 0, s, ma);
   if (m.n_src > 0) {
-    // Key ranges of at most one staged tile each (the rank loop always runs a whole tile).
-    const int rsplit = std::max(1, std::min(64, (m.n_src + kRankTile - 1) / kRankTile));
-    hipLaunchKernelGGL(rank_kernel, dim3((m.n_src + 255) / 256, m.G, rsplit), dim3(256), 0, s, m, rsplit);
+    // The sorted tiles reuse the workspace: the split partials are dead after combine_kernel.
+    const int n_tiles = (m.n_src + kRankTile - 1) / kRankTile;
+    uint64_t* sorted = reinterpret_cast<uint64_t*>(partials);
+    hipLaunchKernelGGL(rank_sort_kernel, dim3(n_tiles, m.G), dim3(64), 0, s, m, sorted);
+    hipLaunchKernelGGL(rank_kernel, dim3((m.n_src + 255) / 256, m.G), dim3(256), 0, s, m, sorted, n_tiles);
     hipLaunchKernelGGL(edge_kernel, dim3(grid256((int64_t)m.G * m.n_src)), dim3(256), 0, s, m);
   }
   hipLaunchKernelGGL(assign_kernel, dim3(grid256((int64_t)m.G * m.L)), dim3(256), 0, s, m);
@@ -978,8 +1018,12 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
   return sa::check_launch(fn);
 }
 
+// The workspace holds the split partials of the match (8 bytes per group, split and src),
+// then the rank's sorted key tiles (8 bytes per group and padded src).
 int64_t match_partial_bytes(int G, int n_src, int n_dst) {
-  return (int64_t)G * match_splits(n_dst) * std::max(n_src, 1) * 8;
+  const int64_t partials = (int64_t)G * match_splits(n_dst) * std::max(n_src, 1) * 8;
+  const int64_t tiles = (int64_t)G * ((n_src + kRankTile - 1) / kRankTile) * kRankTile * 8;
+  return std::max(partials, tiles);
 }
 
 // ---- allocation-free matching ---------------------------------------------------------
@@ -1023,6 +1067,7 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
   int rc = check_maps(maps, "sa_tome_match");
   if (rc) return rc;
   SA_REQUIRE(metric && workspace, "sa_tome_match: null metric/workspace");
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 8 == 0, "sa_tome_match: workspace not 8-byte aligned");
   SA_REQUIRE(C > 0 && C <= kMaxC, "sa_tome_match: C=%d outside [1, %d]", C, kMaxC);
   const sa_tome_maps& m = *maps;
   const int64_t need = match_partial_bytes(m.G, m.n_src, m.n_dst);
