@@ -522,16 +522,12 @@ __global__ __launch_bounds__(256) void rank_kernel(sa_tome_maps m, const uint64_
 #pragma unroll
     for (int t = 0; t < kRankChunkTiles; ++t) count += rank_prefix(keys + t * kRankTile, mine);
   }
-  if (s < m.n_src) m.rank[(int64_t)g * m.n_src + s] = count;
+  if (s < m.n_src) {
+    m.rank[(int64_t)g * m.n_src + s] = count;
+    m.edge[(int64_t)g * m.n_src + count] = s;  // the edge order: edge[rank[s]] = s
+  }
 }
 
-// edge[g][rank[s]] = s.
-__global__ void edge_kernel(sa_tome_maps m) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)m.G * m.n_src) return;
-  const int64_t g = i / m.n_src;
-  m.edge[g * m.n_src + m.rank[i]] = (int32_t)(i - g * m.n_src);
-}
 
 // dst_idx, dst counts, the unmerge map for every token and the source row of every
 // merged row (merged_src).
@@ -1007,7 +1003,6 @@ int tome_match_impl(const float* metric, int C, const sa_tome_maps& m, void* par
     uint64_t* sorted = reinterpret_cast<uint64_t*>(partials);
     hipLaunchKernelGGL(rank_sort_kernel, dim3(n_tiles, m.G), dim3(64), 0, s, m, sorted);
     hipLaunchKernelGGL(rank_kernel, dim3((m.n_src + 255) / 256, m.G), dim3(256), 0, s, m, sorted, n_tiles);
-    hipLaunchKernelGGL(edge_kernel, dim3(grid256((int64_t)m.G * m.n_src)), dim3(256), 0, s, m);
   }
   hipLaunchKernelGGL(assign_kernel, dim3(grid256((int64_t)m.G * m.L)), dim3(256), 0, s, m);
   hipLaunchKernelGGL(scan_kernel, dim3(m.G), dim3(1024), 0, s, m);
