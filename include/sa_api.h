@@ -118,8 +118,10 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
 /*
  * sa_block_sparse_fwd for fp16 q, k, v and out (the reference kernel runs on either 16-bit
  * type: P is rounded to v's dtype, :107): same arguments and contract, D = 64 or 128, with the
- * fp16 MFMA and P rounded to fp16. Every item runs with the running row maximum (fp16 P has
- * too little exponent range for the unshifted exp2 that bf16 launches try first).
+ * fp16 MFMA and P rounded to fp16. fp16 P has too little exponent range for the unshifted
+ * exp2 that bf16 launches try first, so an item's first pass subtracts, from every score of a
+ * row, the row's maximum over the item's first tile; an item in which a later score exceeds
+ * that by 2^16 or more (P rounds to inf) is redone with the running row maximum.
  */
 int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                             const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
@@ -204,7 +206,7 @@ int sa_block_sparse_fwd_mapped(const uint16_t* q, const int64_t q_strides[3], co
 
 /*
  * sa_block_sparse_fwd_mapped for fp16 q, k, v and out: same arguments and contract, computed
- * as sa_block_sparse_fwd_f16 (fp16 MFMA, P rounded to fp16, running row maximum).
+ * as sa_block_sparse_fwd_f16 (fp16 MFMA, P rounded to fp16, first-tile row offsets).
  */
 int sa_block_sparse_fwd_mapped_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                                    const int64_t k_strides[3], const uint16_t* v,
@@ -323,7 +325,8 @@ int sa_block_sparse_fwd_split(const uint16_t* q, const int64_t q_strides[3], con
                               const int32_t* o_rows, int o_dst_rows, int parts, void* workspace,
                               int64_t workspace_bytes, void* stream);
 
-/* sa_block_sparse_fwd_split for fp16 q, k, v and out (P rounded to fp16, running row maximum). */
+/* sa_block_sparse_fwd_split for fp16 q, k, v and out (P rounded to fp16; each part offsets its
+ * rows by their maxima over the part's first tile, as sa_block_sparse_fwd_f16). */
 int sa_block_sparse_fwd_split_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                                   const int64_t k_strides[3], const uint16_t* v,
                                   const int64_t v_strides[3], uint16_t* out,
