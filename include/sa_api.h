@@ -666,7 +666,7 @@ int sa_tome_metric(const uint16_t* k, const int64_t k_strides[3], const uint16_t
  * the same arithmetic as sa_tome_metric's last step. */
 int sa_tome_normalize(const float* metric, int64_t rows, int C, float* out, void* stream);
 
-/* Workspace bytes needed by sa_tome_match (the workspace must be 8-byte aligned). */
+/* Workspace bytes needed by sa_tome_match (the workspace must be 16-byte aligned). */
 int sa_tome_match_workspace(int G, int n_src, int n_dst, int64_t* bytes);
 
 /*

@@ -611,7 +611,8 @@ __global__ void fill_kernel(sa_tome_maps m) {
 // (member_rows): the merge reads one index per member. One wave per dst: the members are
 // distinct edge positions, so each one's place is the number of smaller members, counted
 // against the whole segment in 64-member chunks (broadcast with readlane); a segment of more
-// than kSortMaxMembers (64 chunks' ranks in registers) is insertion-sorted by lane 0.
+// than kSortMaxMembers (the ranks of kSortChunks chunks, kept in registers) is insertion-sorted
+// by lane 0.
 constexpr int kSortChunks = 16;
 constexpr int kSortMaxMembers = 64 * kSortChunks;
 
@@ -1062,7 +1063,7 @@ extern "C" int sa_tome_match(const float* metric, int C, sa_tome_maps* maps, voi
   int rc = check_maps(maps, "sa_tome_match");
   if (rc) return rc;
   SA_REQUIRE(metric && workspace, "sa_tome_match: null metric/workspace");
-  SA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 8 == 0, "sa_tome_match: workspace not 8-byte aligned");
+  SA_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "sa_tome_match: workspace not 16-byte aligned");
   SA_REQUIRE(C > 0 && C <= kMaxC, "sa_tome_match: C=%d outside [1, %d]", C, kMaxC);
   const sa_tome_maps& m = *maps;
   const int64_t need = match_partial_bytes(m.G, m.n_src, m.n_dst);

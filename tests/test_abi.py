@@ -157,3 +157,21 @@ def test_library_allocates_no_device_memory():
     for f in names:
         hits = pat.findall(open(os.path.join(csrc, f)).read())
         assert not hits, (f, hits)
+
+
+def test_tome_match_workspace_checks(lib):
+    # Sizes and alignment of the caller's workspace are checked before any GPU work (the map
+    # pointers are placeholders that the validation never dereferences).
+    from sparseattnfunctions_amd._tome import _MapsStruct
+    G, ns, nd, r, T = 2, 12240, 5310, 4000, 226
+    N = ns + nd
+    maps = _MapsStruct(G, N, T, ns, nd, r, T + N, T + N - r, *([4096] * 15))
+    need = ctypes.c_int64(0)
+    assert lib.sa_tome_match_workspace(G, ns, nd, ctypes.byref(need)) == 0
+    splits = 14  # 42 dst tiles of 128 in splits of 3
+    assert need.value == max(G * splits * ns * 8, G * ((ns + 255) // 256) * 256 * 8)
+    metric = ctypes.c_void_p(4096)
+    rc = lib.sa_tome_match(metric, 64, ctypes.byref(maps), ctypes.c_void_p(4096 + 8), need.value, None)
+    assert rc == _lib.SA_ERR_INVALID and b"16-byte aligned" in lib.sa_last_error()
+    rc = lib.sa_tome_match(metric, 64, ctypes.byref(maps), ctypes.c_void_p(4096), need.value - 1, None)
+    assert rc == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
