@@ -723,9 +723,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 
   run(std::false_type{});
   // The fast pass is exact unless a row's sum left [2^-90, 2^90] (bf16: scores far from 0,
-  // where exp2 would lose range; fp16: a later tile's score more than 2^16 times the first
-  // tile's maximum, where P rounds to inf) or an accumulator overflowed; then redo the item
-  // safely.
+  // where exp2 would lose range; fp16: a later tile's P at or above 2^16 times the largest P of
+  // the first tile, where fp16 P rounds to inf) or an accumulator overflowed; then redo the
+  // item safely.
   if (cnt > beg) {
     bool bad = false;
 #pragma unroll
