@@ -116,6 +116,35 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
                         const int32_t* work_order, int64_t n_slots, void* stream);
 
 /*
+ * sa_block_sparse_fwd with the scores in fp16 (same block_sparse_attn_kernel.py:52-209 work,
+ * bf16 q, k, v and out, head dim 64, no key_bias). The workspace holds an fp16 copy of k (round
+ * to nearest even: exact for 2^-17 <= |k| < 65504, on fp16's subnormal grid below, an absolute
+ * error of at most 2^-25) and the largest squared key-row norm of each 64-row key block,
+ * written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16 (or by this call first, with
+ * prepared = 0). Each query block forms its operands fp16(q * sm_scale * log2(e)) in registers,
+ * so that S = q k^T lands in the exp2 domain and the softmax takes no multiply per score. A
+ * query block uses these operands when its largest row norm of q * sm_scale * log2(e) times the
+ * head's largest key-row norm is at most 32, with both squared norms below 4e9: that bounds
+ * every |S * sm_scale * log2(e)| by 32 (Cauchy-Schwarz), and the 2^-11 relative rounding of each
+ * q element then moves a score by at most 2^-6 in the exp2 domain. Any other query block (or
+ * one with a NaN norm) runs exactly as in sa_block_sparse_fwd. Row sums, P (bf16) and P.V are
+ * as there. The fp16 operands have no counterpart in the reference, whose kernel scales the
+ * fp32 scores (:84-85).
+ *   workspace  256-byte aligned, >= sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64) bytes; with
+ *              prepared = 1 it must hold this k's preparation, done earlier in stream order
+ *              (another stream: the caller orders the two).
+ */
+int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int64_t* bytes);
+int sa_block_sparse_fwd_k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int Lk,
+                                    int D, void* workspace, int64_t workspace_bytes, void* stream);
+int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                            const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                            uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                            int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt, float sm_scale,
+                            const int32_t* work_order, int64_t n_slots, int prepared, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
  * sa_block_sparse_fwd for fp16 q, k, v and out (the reference kernel runs on either 16-bit
  * type: P is rounded to v's dtype, :107): same arguments and contract, D = 64 or 128, with the
  * fp16 MFMA and P rounded to fp16. fp16 P has too little exponent range for the unshifted
@@ -349,6 +378,17 @@ int sa_block_sparse_fwd_split_f16(const uint16_t* q, const int64_t q_strides[3],
 int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                   const int64_t k_strides[3], int B, int H, int L, int D, int block,
                   float* q_pooled, float* k_pooled, void* stream);
+
+/*
+ * sa_block_pool with block = 64 whose k pass also writes the workspace of
+ * sa_block_sparse_fwd_k16 for this k (the fp16 copy and the per-block key norms, the same
+ * bits as sa_block_sparse_fwd_k16_prepare), so that the attention call can pass prepared = 1
+ * (this pass reads k anyway). No counterpart in the reference.
+ *   workspace  256-byte aligned, >= sa_block_sparse_fwd_k16_workspace(B, H, L, 64) bytes.
+ */
+int sa_block_pool_k16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                      const int64_t k_strides[3], int B, int H, int L, int D, float* q_pooled,
+                      float* k_pooled, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Per-row top-k block selection -> kv lists.

@@ -23,6 +23,7 @@ class KVList:
     H: int
     nqb: int
     nkb: int
+    dense: bool = False  # every row lists every key block (set by the dense-list builders)
 
     @property
     def rows(self) -> int:

@@ -35,6 +35,7 @@ _PROTOTYPES = {
     "sa_mask_cells_to_kv_list": (_I, [_P, _I64P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P]),
     "sa_cell_tile_masks": (_I, [_I, _I, _P, _I64P]),
     "sa_block_pool": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "sa_block_pool_k16": (_I, [_P, _I64P, _P, _I64P, _I, _I, _I, _I, _P, _P, _P, ctypes.c_int64, _P]),
     "sa_block_topk_kv_list": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P]),
     "sa_block_sparse_fwd": (
         _I,
@@ -74,6 +75,13 @@ _PROTOTYPES = {
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
     "sa_attn_split_parts": (_I, [ctypes.c_int64, _I, _I, _I, ctypes.POINTER(_I)]),
     "sa_attn_split_workspace": (_I, [ctypes.c_int64, _I, _I, _I64P]),
+    "sa_block_sparse_fwd_k16_workspace": (_I, [_I, _I, _I, _I, _I64P]),
+    "sa_block_sparse_fwd_k16_prepare": (_I, [_P, _I64P, _I, _I, _I, _I, _P, ctypes.c_int64, _P]),
+    "sa_block_sparse_fwd_k16": (
+        _I,
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P, ctypes.c_int64, _I,
+         _P, ctypes.c_int64, _P],
+    ),
     "sa_block_sparse_fwd_split": (
         _I,
         [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P, _I, _P, _I, _I, _P,
@@ -185,6 +193,19 @@ def i64(*vals: int):
 
 def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+_SIDE = {}
+
+
+def side_stream(device) -> "torch.cuda.Stream":
+    """The package's second stream on `device` (default priority), created once: work that
+    runs beside the current stream's, ordered with it by wait_stream / events."""
+    key = str(torch.device(device))
+    s = _SIDE.get(key)
+    if s is None:
+        s = _SIDE[key] = torch.cuda.Stream(device=device)
+    return s
 
 
 def stream_of(t: torch.Tensor) -> int:

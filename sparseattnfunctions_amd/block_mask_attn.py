@@ -33,7 +33,7 @@ def dense_kv_list(B: int, H: int, nqb: int, nkb: int, device) -> KVList:
     """Every key block for every query block (dense attention through the same kernel)."""
     idx = torch.arange(nkb, dtype=torch.int32, device=device).expand(B * H * nqb, nkb).contiguous()
     cnt = torch.full((B * H * nqb,), nkb, dtype=torch.int32, device=device)
-    return KVList(idx, cnt, B, H, nqb, nkb)
+    return KVList(idx, cnt, B, H, nqb, nkb, dense=True)
 
 
 class BlockSparseAttention:
@@ -50,15 +50,17 @@ class BlockSparseAttention:
     def n_text_blocks(self) -> int:
         return math.ceil(self.geometry.text_len / self.block_size)
 
-    def build_kv_list(self, q: torch.Tensor, k: torch.Tensor) -> KVList:
+    def build_kv_list(self, q: torch.Tensor, k: torch.Tensor, with_fp16_keys: bool = False):
+        """kv lists of the mean-pool top-k rule; with `with_fp16_keys`, (kv, fp16 keys made beside
+        the top-k kernel) for block_sparse_attention(..., k16=...)."""
         nb = math.ceil(q.shape[2] / self.block_size)
         return meanpool_topk_kv_list(q, k, topk_count(self.keep_ratio, nb), self.n_text_blocks(),
-                                     block=self.block_size)
+                                     block=self.block_size, with_fp16_keys=with_fp16_keys)
 
     def forward(self, q, k, v):
-        kv = self.build_kv_list(q, k)
+        kv, k16 = self.build_kv_list(q, k, with_fp16_keys=True)
         self.last_kv = kv
-        return block_sparse_attention(q, k, v, kv, self.sm_scale, n_text_blocks=self.n_text_blocks())
+        return block_sparse_attention(q, k, v, kv, self.sm_scale, n_text_blocks=self.n_text_blocks(), k16=k16)
 
     def forward_dense(self, q, k, v):
         B, H, L, _ = q.shape

@@ -28,8 +28,11 @@ def _prep(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
-def pool_blocks(q: torch.Tensor, k: Optional[torch.Tensor] = None, block: int = 64):
-    """Block means: bf16 [B,H,L,64] -> fp32 [B*H, ceil(L/block), 64] (for q and k)."""
+def pool_blocks(q: torch.Tensor, k: Optional[torch.Tensor] = None, block: int = 64,
+                k16_ws: Optional[torch.Tensor] = None):
+    """Block means: bf16 [B,H,L,64] -> fp32 [B*H, ceil(L/block), 64] (for q and k). With
+    `k16_ws` (block 64, uint8 of block_sparse_attn_kernel.k16_workspace_bytes bytes), the k
+    pass also writes the fp16-score workspace of block_sparse_attention (`sa_block_pool_k16`)."""
     _lib.require_gpu(q, k)
     q = _prep(q)
     B, H, L, D = q.shape
@@ -42,6 +45,15 @@ def pool_blocks(q: torch.Tensor, k: Optional[torch.Tensor] = None, block: int = 
             raise ValueError("pool_blocks: q and k must have the same shape")
         kp = torch.empty_like(qp)
     lib = _lib.load()
+    if k16_ws is not None:
+        if k is None or block != 64:
+            raise ValueError("pool_blocks: k16_ws needs k and 64-token blocks")
+        with torch.cuda.device(q.device):
+            rc = lib.sa_block_pool_k16(q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                                       B, H, L, D, qp.data_ptr(), kp.data_ptr(), k16_ws.data_ptr(), k16_ws.numel(),
+                                       _lib.stream_of(q))
+        _lib.check(rc, "sa_block_pool_k16")
+        return qp, kp
     with torch.cuda.device(q.device):
         rc = lib.sa_block_pool(
             q.data_ptr(), _lib.i64(*q.stride()[:3]),
@@ -94,12 +106,26 @@ def topk_kv_list(q_pooled, k_pooled, B: int, H: int, topk: int, n_text_blocks: i
 
 
 def meanpool_topk_kv_list(q, k, topk: int, n_text_blocks: int, block: int = 64,
-                          local_bitmap: Optional[torch.Tensor] = None, **kw):
+                          local_bitmap: Optional[torch.Tensor] = None, with_fp16_keys: bool = False, **kw):
     """q, k bf16 [B,H,L,64] -> kv lists of the mean-pool top-k rule (config 2; with a
-    local bitmap, the combined rule of config 3)."""
-    B, H = q.shape[:2]
-    qp, kp = pool_blocks(q, k, block)
-    return topk_kv_list(qp, kp, B, H, topk, n_text_blocks, local_bitmap=local_bitmap, **kw)
+    local bitmap, the combined rule of config 3). With `with_fp16_keys`, returns (kv, k16):
+    the fp16 keys of block_sparse_attention's fp16 scores, written by the pooling pass, which
+    reads k anyway (`sa_block_pool_k16`; k16 is None when block_sparse_attention's default
+    takes no fp16 scores or the blocks are not 64 tokens)."""
+    from .utils.block_sparse_attn_kernel import FP16Keys, fp16_keys_wanted, k16_workspace_bytes
+    B, H, L = q.shape[:3]
+    ws = None
+    if with_fp16_keys and block == 64 and fp16_keys_wanted(k):
+        ws = torch.empty(k16_workspace_bytes(B, H, L, 64), dtype=torch.uint8, device=k.device)
+    qp, kp = pool_blocks(q, k, block, k16_ws=ws)
+    k16 = None
+    if ws is not None:
+        stream = torch.cuda.current_stream(k.device)
+        event = torch.cuda.Event()
+        event.record(stream)
+        k16 = FP16Keys(k, ws, stream, event)
+    kv = topk_kv_list(qp, kp, B, H, topk, n_text_blocks, local_bitmap=local_bitmap, **kw)
+    return (kv, k16) if with_fp16_keys else kv
 
 
 _LOCAL_CACHE = {}

@@ -107,14 +107,16 @@ class CombinedAttn:
     def n_text_blocks(self) -> int:
         return math.ceil(self.geometry.text_len / self.geometry.block)
 
-    def build_kv_list(self, q, k):
+    def build_kv_list(self, q, k, with_fp16_keys: bool = False):
+        """Combined-rule kv lists; with `with_fp16_keys`, (kv, fp16 keys made beside the top-k
+        kernel) for block_sparse_attention(..., k16=...)."""
         L = q.shape[2]
         if L != self.geometry.L:
             raise ValueError(f"sequence length {L} does not match the geometry (L={self.geometry.L})")
         nb = math.ceil(L / 64)
         local = local_window_bitmap(self.geometry, self.window, q.device)
         return meanpool_topk_kv_list(q, k, topk_count(self.global_ratio, nb), self.n_text_blocks(),
-                                     local_bitmap=local)
+                                     local_bitmap=local, with_fp16_keys=with_fp16_keys)
 
     @staticmethod
     def rearranger(q, k, v):
@@ -212,6 +214,8 @@ class CombinedAttn:
             nb = math.ceil(L / 64)
             kv = dense_kv_list(B, H, nb, math.ceil(k.shape[2] / 64), q.device)
         else:
+            # bf16 scores: these lists (31-46 blocks of 278) earn less in the tile loop than the
+            # fp16 copy of k costs the pooling pass
             kv = self.build_kv_list(q, k)
         self.last_kv = kv
         return block_sparse_attention(q, k, v, kv, self._scale(q), n_text_blocks=self.n_text_blocks())

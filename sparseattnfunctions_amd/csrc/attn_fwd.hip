@@ -59,6 +59,10 @@ constexpr int kSplitFloats = kBlock * kD + 2 * kBlock;
 constexpr int kTileBytes = kBlock * kHeadDim * 2;  // one K or V tile: 64 rows x 128 B
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
+// fp16 scores: largest |S * scale_log2| bound (Cauchy-Schwarz of the row norms) for which an
+// item uses them, and the squared-norm limit below 65504^2 (the largest fp16 value).
+constexpr float kK16Bound = 32.0f;
+constexpr float kK16NormMax = 4.0e9f;
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef short sa_i16x4v __attribute__((ext_vector_type(4)));
@@ -114,6 +118,11 @@ struct FwdArgs {
   int64_t po_sb, po_sh, po_si;
   int pool_nd;      // cdiv(Lq, kPool)
   int pool_causal;  // columns past the query's diagonal 64-key tile were never computed: 0
+  // fp16 scores (kK16): k16 = fp16 copy of k, contiguous [B*H][Lk][64]; k16_norm2[bh * nkb +
+  // kb] = the largest squared row norm of key block kb of head bh (fp32 bits). An item whose
+  // bound passes computes S = K16 (fp16(q * scale_log2))^T, already in the exp2 domain.
+  const uint16_t* k16;
+  const uint32_t* k16_norm2;
 };
 
 __device__ inline sa_bf16x8 as_bf16x8(uint4 x) { return __builtin_bit_cast(sa_bf16x8, x); }
@@ -275,8 +284,10 @@ constexpr int kWaitLgkm0 = 0xC07F;
 // launches.)
 // kDV: value columns that enter P.V and the output, kD or 32 (head dim 64: v tiles are
 // copied as usual and only their first 32 columns are read; out has 32 columns).
-template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64, int kDV = kD>
+template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64, int kDV = kD, bool kK16 = false>
 __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs a) {
+  static_assert(!kK16 || (!kBias && !kMask && kPool == 0 && std::is_same<T, __bf16>::value && kD == 64 && kDV == 64),
+                "fp16 scores: plain bf16 lists at head dim 64");
   static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
   static_assert(kD == 64 || kD == 128, "head dim 64 or 128");
   static_assert(kDV == kD || (kDV == 32 && kD == 64 && kPool == 0 && !kMask), "32 value columns: head dim 64");
@@ -309,7 +320,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const int slot = blockIdx.x * kWaves + wave;
   if (slot >= a.n_slots) return;
   // Key-range parts exist for plain lists only; the other variants compile without them.
-  constexpr bool kSplit = !kBias && !kMask && kPool == 0 && kDV == kD;
+  constexpr bool kSplit = !kBias && !kMask && kPool == 0 && kDV == kD && !kK16;
   const bool split = kSplit && a.n_parts > 1;
   int item, part = 0;
   if (split) {
@@ -348,10 +359,11 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   const uint16_t* vhead = a.v + b * a.v_sb + hk * a.v_sh;
   uint16_t* obase = a.o + b * a.o_sb + h * a.o_sh;
   const float* bhead = kBias ? a.bias + b * a.bias_sb + h * a.bias_sh : nullptr;
-  const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
-  const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
+  uint32_t krow = (uint32_t)(a.k_sl * 2);
+  const uint32_t vrow = (uint32_t)(a.v_sl * 2);
+  uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
   const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
-  const bool c128 = krow == 128 && vrow == 128;  // contiguous d = 64 rows: dma_tile_c128
+  bool c128 = krow == 128 && vrow == 128;  // contiguous d = 64 rows: dma_tile_c128
   lds_u8* kl = (lds_u8*)k_lds + wave * kTileBytes * kHalves;
   lds_u8* vl = (lds_u8*)v_lds + wave * kTileBytes * kHalves;
   float* bl_lds = b_lds + (kBias ? wave * 3 * kBlock : 0);
@@ -462,13 +474,99 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     }
   };
 
+  // fp16 scores: the item takes them when max |q_i * scale_log2| * max |k_j| (largest row
+  // norms of its query rows and of the head's keys) is at most kK16Bound, which bounds every
+  // |S * scale_log2| of the item by Cauchy-Schwarz, and both squared norms are below
+  // kK16NormMax, so no element reaches the fp16 range limit. k16 then equals k from 2^-17 up
+  // (smaller elements move by at most 2^-25) and fp16(q * scale_log2) has a relative error of
+  // at most 2^-11 per element (absolute 2^-25 below fp16's normal range): each logit moves by
+  // about 2^-11 * kK16Bound at most in the exp2 domain. Otherwise (or with a NaN) the item runs on the bf16 operands. The item's first K
+  // tile (from k16) and V tile are requested before the bound is known; an item that fails it
+  // waits for them and starts again from k.
+  bool use16 = false;
+  bool issued16 = false;  // the first copies of the fp16 pass are in flight
+  if constexpr (kK16) {
+    // The head's largest squared key norm: its block norms, 64 per load, maximum over the wave
+    // (loaded before the copies below, which the loop's wait counts then find alone in flight).
+    const uint32_t* bn = a.k16_norm2 + (int64_t)bh * a.nkb;
+    uint32_t kmax = 0u;
+    for (int j0 = 0; j0 < a.nkb; j0 += 256) {
+      uint32_t v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v4[u] = bn[min(j0 + 64 * u + lane, a.nkb - 1)];  // clamped: the maximum is unchanged
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) kmax = max(kmax, v4[u]);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    const uint16_t* const k_bf = khead;
+    const uint32_t krow_bf = krow, kbytes_bf = kbytes, kgo_bf[2] = {kgo[0], kgo[1]};
+    const bool c128_bf = c128;
+    khead = a.k16 + (int64_t)bh * a.Lk * kHeadDim;
+    krow = 2 * kHeadDim;
+    kbytes = (uint32_t)a.Lk * krow;
+    c128 = vrow == 128;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int r = 8 * p + (lane >> 3);
+      kgo[p] = (lane >> 3) * krow + 16 * ((lane & 7) ^ swz(r));
+    }
+    if (cnt > beg) {
+      const int kb0 = entry(beg);
+      issue_k(kb0, beg);
+      issue_v(kb0, beg);
+      issued16 = true;
+    }
+    const float qs = a.scale_log2;
+    float n2[2] = {0.f, 0.f};
+    uint32_t h16[2][kDS][4];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int s = 0; s < kDS; ++s) {
+        const sa_u32x4v w = __builtin_bit_cast(sa_u32x4v, qf[g][s]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x0 = __uint_as_float(w[i] << 16) * qs, x1 = __uint_as_float(w[i] & 0xffff0000u) * qs;
+          n2[g] = fmaf(x1, x1, fmaf(x0, x0, n2[g]));
+          h16[g][s][i] = Elem<_Float16>::pack(x0, x1);
+        }
+      }
+    float qn2 = fmaxf(xhalf_sum(n2[0]), xhalf_sum(n2[1]));  // rows 32g + col of the lane's column
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) qn2 = fmaxf(qn2, __shfl_xor(qn2, o));
+    qn2 = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(qn2)));  // equal in every lane
+    const float kn2 = __uint_as_float(__builtin_amdgcn_readfirstlane(kmax));
+    use16 = qn2 < kK16NormMax && kn2 < kK16NormMax && qn2 * kn2 <= kK16Bound * kK16Bound;
+    if (use16) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int s = 0; s < kDS; ++s)
+          qf[g][s] = __builtin_bit_cast(typename E::v8, sa_u32x4v{h16[g][s][0], h16[g][s][1], h16[g][s][2], h16[g][s][3]});
+    } else {
+      // The requested copies land before the bf16 pass requests its own into the same buffers.
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      issued16 = false;
+      khead = k_bf;
+      krow = krow_bf;
+      kbytes = kbytes_bf;
+      c128 = c128_bf;
+      kgo[0] = kgo_bf[0];
+      kgo[1] = kgo_bf[1];
+    }
+  }
+
   // One pass over the item's key blocks. Fast pass (kSafe = false): P = exp2(S) with no
   // max subtraction. Softmax is invariant to a common factor, and bf16 P keeps fp32's
   // exponent range, so this equals the max-subtracted result as long as the scores stay in
   // range; the caller checks the row sums afterwards and redoes the item with the safe pass
   // (running max, lazy rescale) otherwise.
-  auto run = [&](auto safe_tag) {
+  auto run = [&](auto safe_tag, auto k16_tag, bool first_issued) __attribute__((always_inline)) {
     constexpr bool kSafe = decltype(safe_tag)::value;
+    constexpr bool kQ16 = decltype(k16_tag)::value;  // fp16 K and pre-scaled q: S in the exp2 domain
     // fp16 P keeps 5 exponent bits, so its fast pass subtracts a fixed per-row offset.
     constexpr bool kOffset = !kSafe && !std::is_same<T, __bf16>::value;
 #pragma unroll
@@ -479,7 +577,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     l[0] = l[1] = 0.f;
     int it = beg;
     int kb = entry(beg);
-    if (cnt > beg) {
+    if (cnt > beg && !first_issued) {  // (the fp16 fast pass requested its first tile above)
       if (kBias) issue_bias(beg);
       issue_k(kb, beg);
       issue_v(kb, beg);
@@ -532,7 +630,12 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         for (int g = 0; g < 2; ++g) {
           sa_f32x16 t = {};
 #pragma unroll
-          for (int s = 0; s < kDS; ++s) t = E::mfma(E::as8(kop[c][s]), qf[g][s], t);
+          for (int s = 0; s < kDS; ++s) {
+            if constexpr (kQ16)
+              t = Elem<_Float16>::mfma(Elem<_Float16>::as8(kop[c][s]), __builtin_bit_cast(sa_f16x8, qf[g][s]), t);
+            else
+              t = E::mfma(E::as8(kop[c][s]), qf[g][s], t);
+          }
           S[g][c] = t;
         }
       
@@ -581,7 +684,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       }
 
       // ---- P = exp2(S * sc - m) in bf16 and the row sums (m = 0 in the fast pass).
-      const float sc = kBias ? 1.f : a.scale_log2;  // S is already scaled with a bias
+      const float sc = (kBias || kQ16) ? 1.f : a.scale_log2;  // S is already scaled (bias, fp16 scores)
       if constexpr (kPool != 0) {
         // Row maxima of the scaled logits per kPool-key column. Lane l stores row
         // qb * 64 + l (query group hh, column col): one 256-byte store per column.
@@ -721,7 +824,15 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
 
-  run(std::false_type{});
+  auto run_item = [&](auto safe_tag, bool first_issued) __attribute__((always_inline)) {
+    if constexpr (kK16) {
+      if (use16) run(safe_tag, std::true_type{}, first_issued);
+      else run(safe_tag, std::false_type{}, false);
+    } else {
+      run(safe_tag, std::false_type{}, false);
+    }
+  };
+  run_item(std::false_type{}, issued16);
   // The fast pass is exact unless a row's sum left [2^-90, 2^90] (bf16: scores far from 0,
   // where exp2 would lose range; fp16: a later tile's P at or above 2^16 times the largest P of
   // the first tile, where fp16 P rounds to inf) or an accumulator overflowed; then redo the
@@ -739,7 +850,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
         for (int e = 0; e < 16; e += 2) amax = fmaxf(fmaxf(amax, fabsf(acc[dc][g][e])), fabsf(acc[dc][g][e + 1]));
       bad |= !(amax <= 3.0e38f);
     }
-    if (__ballot(bad) != 0) run(std::true_type{});
+    if (__ballot(bad) != 0) run_item(std::true_type{}, false);
   }
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
@@ -1269,6 +1380,10 @@ template <typename T, int kD>
 void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask, bool bias, int pool_cols,
                     bool v32 = false) {
   if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
+    if (a.k16) {  // fp16 scores (the caller has rejected every other mode)
+      hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, kD, true>), g, blk, 0, s, a);
+      return;
+    }
     if (v32) {  // 32 value columns (the caller has rejected tile masks and pooling)
       if (bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, T, kD, 32>), g, blk, 0, s, a);
       else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, 32>), g, blk, 0, s, a);
@@ -1305,7 +1420,8 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                const int32_t* q_rows, int q_src_rows, const int32_t* o_rows, int o_dst_rows, void* stream,
                const char* fn, int kv_rep = 1, int pool_cols = 0, float* pool_r = nullptr,
                float* pool_lse = nullptr, const PoolOut* pool_out = nullptr, bool fp16 = false,
-               bool v32 = false, int parts = 1, void* split_ws = nullptr, int64_t split_ws_bytes = 0) {
+               bool v32 = false, int parts = 1, void* split_ws = nullptr, int64_t split_ws_bytes = 0,
+               const uint16_t* k16 = nullptr, const uint32_t* k16_norm2 = nullptr) {
   SA_REQUIRE(q && k && v && out && q_strides && k_strides && v_strides && out_strides && kv_idx && kv_cnt,
              "%s: null pointer", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lq > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lq=%d Lk=%d", fn, B, H, Lq, Lk);
@@ -1356,6 +1472,11 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.n_slots = (int)n_slots;
   a.n_parts = 1;
   a.ws = nullptr;
+  a.k16 = k16;
+  a.k16_norm2 = k16_norm2;
+  if (k16 && (!k16_norm2 || D != 64 || fp16 || v32 || kv_slot || key_bias || pool_cols || parts != 1 || q_rows ||
+              o_rows || kv_rep != 1))
+    return sa::fail(SA_ERR_UNSUPPORTED, "%s: fp16 scores need plain bf16 lists at head dim 64", fn);
   a.kv_idx = kv_idx; a.kv_cnt = kv_cnt; a.max_cnt = max_cnt;
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
@@ -1501,6 +1622,137 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
                     max_cnt, false, nullptr, nullptr, key_bias, bias_strides, sm_scale, work_order, n_slots, nullptr,
                     0, nullptr, 0, stream, "sa_block_sparse_fwd");
+}
+
+namespace {
+
+// fp16 copy of k for the fp16-score mode: k16[bh][j] = fp16(k[b][h][j]) (round to nearest
+// even: exact for 2^-17 <= |k| < 65504, fp16's subnormal grid below), and blk_norm2[bh * nkb + kb] =
+// the largest squared row norm of key block kb (fp32 fmaf chain over the 64 dims, as float
+// bits, compared as unsigned: the norms are non-negative, and NaN bits compare above every
+// finite or infinite norm, so a NaN row fails the attention kernel's bound). One wave per
+// 64-row key block, 8 lanes per row (16 bytes each). sa_block_pool_k16 writes the same from
+// the pooling pass.
+struct K16Args {
+  const uint16_t* k;
+  int64_t k_sb, k_sh, k_sl;
+  int H, Lk, nkb;
+  int64_t n_blocks;  // B * H * nkb
+  uint16_t* k16;
+  uint32_t* blk_norm2;  // [n_blocks]
+};
+
+__global__ __launch_bounds__(256) void k16_kernel(K16Args a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (blk >= a.n_blocks) return;
+  const int64_t bh = blk / a.nkb;
+  const int kb = (int)(blk - bh * a.nkb);
+  const int64_t b = bh / a.H, h = bh - b * a.H;
+  const int c8 = lane & 7;
+  const uint16_t* src = a.k + b * a.k_sb + h * a.k_sh + 8 * c8;
+  uint16_t* dst = a.k16 + bh * (int64_t)a.Lk * kHeadDim + 8 * c8;
+  uint4 w[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // rows past Lk load the last row, which is neither stored nor counted
+    const int r = min(kb * kBlock + 8 * i + (lane >> 3), a.Lk - 1);
+    w[i] = *reinterpret_cast<const uint4*>(src + (int64_t)r * a.k_sl);
+  }
+  uint32_t mx = 0u;  // float bits of the largest squared norm seen
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = kb * kBlock + 8 * i + (lane >> 3);
+    const uint32_t e[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    uint32_t o[4];
+    float n = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x0 = __uint_as_float(e[j] << 16), x1 = __uint_as_float(e[j] & 0xffff0000u);
+      n = fmaf(x1, x1, fmaf(x0, x0, n));
+      o[j] = Elem<_Float16>::pack(x0, x1);
+    }
+    // the row's 8 lanes, in a fixed order
+    n += __shfl_xor(n, 1);
+    n += __shfl_xor(n, 2);
+    n += __shfl_xor(n, 4);
+    if (r < a.Lk) {
+      mx = max(mx, __float_as_uint(n));
+      *reinterpret_cast<uint4*>(dst + (int64_t)r * kHeadDim) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  if (lane == 0) a.blk_norm2[blk] = mx;
+}
+
+using sa::k16_bytes;
+using sa::k16_ws_bytes;
+
+}  // namespace
+
+extern "C" int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int64_t* bytes) {
+  SA_REQUIRE(bytes, "sa_block_sparse_fwd_k16_workspace: null bytes");
+  SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "sa_block_sparse_fwd_k16_workspace: bad shape B=%d H=%d Lk=%d", B, H, Lk);
+  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd_k16_workspace: head_dim %d (64)", D);
+  *bytes = k16_ws_bytes(B, H, Lk);
+  return sa::ok();
+}
+
+namespace {
+
+int k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int Lk, int D, void* workspace,
+                int64_t workspace_bytes, void* stream, const char* fn) {
+  SA_REQUIRE(k && k_strides, "%s: null k", fn);
+  SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
+  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64)", fn, D);
+  const int64_t need = k16_ws_bytes(B, H, Lk);
+  SA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s: workspace null or not 256-byte aligned",
+             fn);
+  SA_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes < %lld", fn, (long long)workspace_bytes,
+             (long long)need);
+  if (reinterpret_cast<uintptr_t>(k) % 16 != 0 || k_strides[0] % 8 || k_strides[1] % 8 || k_strides[2] % 8)
+    return sa::fail(SA_ERR_UNSUPPORTED, "%s: k base not 16-byte aligned or strides not multiples of 8", fn);
+  K16Args ka;
+  ka.k = k; ka.k_sb = k_strides[0]; ka.k_sh = k_strides[1]; ka.k_sl = k_strides[2];
+  ka.H = H; ka.Lk = Lk; ka.nkb = sa::cdiv(Lk, kBlock);
+  ka.n_blocks = (int64_t)B * H * ka.nkb;
+  ka.k16 = static_cast<uint16_t*>(workspace);
+  ka.blk_norm2 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + k16_bytes(B, H, Lk));
+  SA_REQUIRE(ka.n_blocks / kWaves < (1LL << 31), "%s: grid too large", fn);
+  hipStream_t s = sa::as_stream(stream);
+  hipLaunchKernelGGL(k16_kernel, dim3((unsigned)((ka.n_blocks + kWaves - 1) / kWaves)), dim3(64 * kWaves), 0, s, ka);
+  return sa::check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int sa_block_sparse_fwd_k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int Lk,
+                                               int D, void* workspace, int64_t workspace_bytes, void* stream) {
+  return k16_prepare(k, k_strides, B, H, Lk, D, workspace, workspace_bytes, stream, "sa_block_sparse_fwd_k16_prepare");
+}
+
+extern "C" int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                       const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
+                                       uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
+                                       int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                                       float sm_scale, const int32_t* work_order, int64_t n_slots, int prepared,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* fn = "sa_block_sparse_fwd_k16";
+  int rc = prepared ? SA_OK : k16_prepare(k, k_strides, B, H, Lk, D, workspace, workspace_bytes, stream, fn);
+  if (rc) return rc;
+  if (prepared) {  // the same checks of the workspace, without the launches
+    SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
+    if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64)", fn, D);
+    SA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+               "%s: workspace null or not 256-byte aligned", fn);
+    SA_REQUIRE(workspace_bytes >= k16_ws_bytes(B, H, Lk), "%s: workspace of %lld bytes < %lld", fn,
+               (long long)workspace_bytes, (long long)k16_ws_bytes(B, H, Lk));
+  }
+  const uint16_t* k16 = static_cast<const uint16_t*>(workspace);
+  const uint32_t* norm2 = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(workspace) + k16_bytes(B, H, Lk));
+  return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
+                    max_cnt, false, nullptr, nullptr, nullptr, nullptr, sm_scale, work_order, n_slots, nullptr, 0,
+                    nullptr, 0, stream, fn, 1, 0, nullptr, nullptr, nullptr, false, false, 1, nullptr, 0, k16, norm2);
 }
 
 extern "C" int sa_block_sparse_fwd_f16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,

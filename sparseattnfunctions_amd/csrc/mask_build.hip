@@ -36,7 +36,14 @@ struct PoolArgs {
   float* out[2];
   int H, L, block, nb;
   int64_t total_blocks;  // B*H*nb
+  // With k16 (block 64, sa_block_pool_k16): the k pass also writes the fp16-score workspace of
+  // the attention, k16 = fp16(k) [B*H][L][64] and k16_norm2[block] = the block's largest
+  // squared row norm (fp32 bits), as sa_block_sparse_fwd_k16_prepare computes them.
+  uint16_t* k16;
+  uint32_t* k16_norm2;
 };
+
+typedef _Float16 sa_f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -111,6 +118,39 @@ __global__ __launch_bounds__(256) void pool64_kernel(PoolArgs a) {
   for (int j = 0; j < 8; ++j) {
     const int row = 8 * j + (lane >> 3);
     *reinterpret_cast<uint4*>(wl + row * kPoolRowB + 16 * (lane & 7)) = w[j];
+  }
+  if (t == 1 && a.k16 && n > 0) {
+    // fp16 copy of the block's key rows (round to nearest even) and its largest squared row
+    // norm: per row an fmaf chain over the lane's 8 dims, then the row's 8 lanes in a fixed
+    // order (the arithmetic of k16_kernel in attn_fwd.hip, so both give the same bits).
+    const int64_t bh = g / a.nb;
+    const int blk = (int)(g - bh * a.nb);
+    uint16_t* dst = a.k16 + (bh * a.L + (int64_t)blk * 64) * kPoolD + 8 * (lane & 7);
+    uint32_t mx = 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 8 * j + (lane >> 3);
+      const uint32_t e[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+      uint32_t o[4];
+      float nr = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = bf16lo(e[i]), x1 = bf16hi(e[i]);
+        nr = fmaf(x1, x1, fmaf(x0, x0, nr));
+        const sa_f16x2 h2 = {(_Float16)x0, (_Float16)x1};
+        o[i] = __builtin_bit_cast(uint32_t, h2);
+      }
+      nr += __shfl_xor(nr, 1);
+      nr += __shfl_xor(nr, 2);
+      nr += __shfl_xor(nr, 4);
+      if (row < n) {
+        mx = max(mx, __float_as_uint(nr));
+        *reinterpret_cast<uint4*>(dst + (int64_t)row * kPoolD) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+    if (lane == 0) a.k16_norm2[g] = mx;
   }
   __syncthreads();
   if (n == 0) return;
@@ -343,9 +383,36 @@ __global__ __launch_bounds__(64 * kRowsPerWG / kR) void topk_kernel(TopkArgs a) 
 
 }  // namespace
 
+namespace {
+int block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3], int B,
+               int H, int L, int D, int block, float* q_pooled, float* k_pooled, uint16_t* k16, uint32_t* k16_norm2,
+               void* stream);
+}  // namespace
+
 extern "C" int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                              const int64_t k_strides[3], int B, int H, int L, int D, int block,
                              float* q_pooled, float* k_pooled, void* stream) {
+  return block_pool(q, q_strides, k, k_strides, B, H, L, D, block, q_pooled, k_pooled, nullptr, nullptr, stream);
+}
+
+extern "C" int sa_block_pool_k16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
+                                 const int64_t k_strides[3], int B, int H, int L, int D, float* q_pooled,
+                                 float* k_pooled, void* workspace, int64_t workspace_bytes, void* stream) {
+  SA_REQUIRE(k && k_strides && k_pooled, "sa_block_pool_k16: null k");
+  SA_REQUIRE(B > 0 && H > 0 && L > 0, "sa_block_pool_k16: bad shape B=%d H=%d L=%d", B, H, L);
+  SA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
+             "sa_block_pool_k16: workspace null or not 256-byte aligned");
+  SA_REQUIRE(workspace_bytes >= sa::k16_ws_bytes(B, H, L), "sa_block_pool_k16: workspace of %lld bytes < %lld",
+             (long long)workspace_bytes, (long long)sa::k16_ws_bytes(B, H, L));
+  uint16_t* k16 = static_cast<uint16_t*>(workspace);
+  uint32_t* norm2 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + sa::k16_bytes(B, H, L));
+  return block_pool(q, q_strides, k, k_strides, B, H, L, D, 64, q_pooled, k_pooled, k16, norm2, stream);
+}
+
+namespace {
+int block_pool(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k, const int64_t k_strides[3], int B,
+               int H, int L, int D, int block, float* q_pooled, float* k_pooled, uint16_t* k16, uint32_t* k16_norm2,
+               void* stream) {
   SA_REQUIRE(q && q_strides && q_pooled, "sa_block_pool: null pointer");
   SA_REQUIRE(!k || (k_strides && k_pooled), "sa_block_pool: k given without k_strides/k_pooled");
   SA_REQUIRE(B > 0 && H > 0 && L > 0 && block > 0, "sa_block_pool: bad shape B=%d H=%d L=%d block=%d", B, H, L, block);
@@ -360,6 +427,8 @@ extern "C" int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], cons
       if (ss[t][i] % 8) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_pool: strides must be multiples of 8");
   }
   PoolArgs a;
+  a.k16 = k16;
+  a.k16_norm2 = k16_norm2;
   a.H = H; a.L = L; a.block = block; a.nb = sa::cdiv(L, block);
   a.total_blocks = (int64_t)B * H * a.nb;
   const int nt = k ? 2 : 1;
@@ -379,6 +448,7 @@ extern "C" int sa_block_pool(const uint16_t* q, const int64_t q_strides[3], cons
   hipLaunchKernelGGL(pool_kernel, dim3((unsigned)grid, nt), dim3(256), 0, sa::as_stream(stream), a);
   return sa::check_launch("sa_block_pool");
 }
+}  // namespace
 
 extern "C" int sa_block_topk_kv_list(const float* q_pooled, const float* k_pooled, const float* scores_in,
                                      int BH, int nqb, int nkb, int D, int topk, int n_text_blocks,

@@ -41,6 +41,12 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
+// Workspace of the fp16-score attention (sa_block_sparse_fwd_k16): the fp16 copy of k,
+// [B*H][Lk][64] contiguous, then the largest squared row norm of each 64-row key block
+// (fp32 bits), [B*H][ceil(Lk/64)]. Written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16.
+inline int64_t k16_bytes(int B, int H, int Lk) { return ((int64_t)B * H * Lk * 64 * 2 + 255) / 256 * 256; }
+inline int64_t k16_ws_bytes(int B, int H, int Lk) { return k16_bytes(B, H, Lk) + (int64_t)B * H * cdiv(Lk, 64) * 4; }
+
 // fp32 attention in pooling mode (attn_f32.hip), for the pooled-map entry point.
 int attn_f32_pooling(const float* q, const int64_t q_strides[3], const float* k, const int64_t k_strides[3],
                      const float* v, const int64_t v_strides[3], float* out, const int64_t out_strides[3], int B,

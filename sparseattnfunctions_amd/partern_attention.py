@@ -62,14 +62,10 @@ composition = torch.log(sample_rate).view(1, 1, 1, 1)
 _CACHE = {}
 OVERLAP_TEXT = True  # text and video-to-text rows on a second stream (see forward)
 OVERLAP_JUDGE = True  # sparsity judge on a second stream (see unified_judge)
-_SIDE = {}
 
 
 def _side_stream(device):
-    s = _SIDE.get(str(device))
-    if s is None:
-        s = _SIDE[str(device)] = torch.cuda.Stream(device=device)
-    return s
+    return _lib.side_stream(device)
 
 
 def _cached(key, make):

@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from typing import Optional
 
 import torch
 
@@ -65,6 +66,57 @@ def split_workspace_bytes(n_items: int, D: int, parts: int) -> int:
                "sa_attn_split_workspace")
     return n.value
 
+
+def k16_workspace_bytes(B: int, H: int, Lk: int, D: int) -> int:
+    """Bytes of the fp16-score workspace (`sa_block_sparse_fwd_k16_workspace`): an fp16 copy of k
+    and the largest squared key-row norm of each head."""
+    n = ctypes.c_int64(0)
+    _lib.check(_lib.load().sa_block_sparse_fwd_k16_workspace(int(B), int(H), int(Lk), int(D), ctypes.byref(n)),
+               "sa_block_sparse_fwd_k16_workspace")
+    return n.value
+
+# Gate of the fp16 scores (block_sparse_attention's default and prepare_fp16_keys): with False,
+# every launch takes the bf16 operands.
+FP16_SCORES = True
+# Dense lists take fp16 scores by default from this many query blocks and key blocks.
+DENSE_FP16_BLOCKS = 128
+
+
+class FP16Keys:
+    """The fp16 copy of k and its per-head key norms for `block_sparse_attention(..., k16=...)`
+    (`sa_block_sparse_fwd_k16_prepare`), made on `stream`; `event` marks its completion."""
+
+    def __init__(self, k: torch.Tensor, ws: torch.Tensor, stream, event):
+        self.key = (k.data_ptr(), tuple(k.shape), tuple(k.stride()))
+        self.ws, self.stream, self.event = ws, stream, event
+
+    def matches(self, k: torch.Tensor) -> bool:
+        return self.key == (k.data_ptr(), tuple(k.shape), tuple(k.stride()))
+
+
+def fp16_keys_wanted(k: torch.Tensor) -> bool:
+    """Whether block_sparse_attention's default takes fp16 scores with this k (bf16 [B,H,Lk,64])."""
+    return FP16_SCORES and k.is_cuda and k.dtype == torch.bfloat16 and k.dim() == 4 and k.shape[3] == 64
+
+
+def prepare_fp16_keys(k: torch.Tensor) -> Optional[FP16Keys]:
+    """Enqueues the fp16 copy of k (bf16 [B,H,Lk,64]) on the current stream; None for other
+    dtypes or head dims (those launches take no fp16 scores)."""
+    if not fp16_keys_wanted(k):
+        return None
+    k_in, k = k, _prep_qkv(k, (torch.bfloat16,))
+    B, H, Lk, D = k.shape
+    ws = torch.empty(k16_workspace_bytes(B, H, Lk, D), dtype=torch.uint8, device=k.device)
+    stream = torch.cuda.current_stream(k.device)
+    with torch.cuda.device(k.device):
+        rc = _lib.load().sa_block_sparse_fwd_k16_prepare(k.data_ptr(), _lib.i64(*k.stride()[:3]), B, H, Lk, D,
+                                                          ws.data_ptr(), ws.numel(), stream.cuda_stream)
+    _lib.check(rc, "sa_block_sparse_fwd_k16_prepare")
+    event = torch.cuda.Event()
+    event.record(stream)
+    return FP16Keys(k_in, ws, stream, event)
+
+
 _ORDER_CACHE = {}
 
 
@@ -93,7 +145,8 @@ def _row_map(rows, device):
 
 
 def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, out=None,
-                           n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None, v_cols: int = None):
+                           n_text_blocks: int = 0, q_rows=None, o_rows=None, tile_masks=None, v_cols: int = None,
+                           fp16_scores: Optional[bool] = None, k16: Optional[FP16Keys] = None):
     """out = block-sparse softmax(q k^T * sm_scale [+ key_bias]) v over the blocks of `kv`.
 
     q [B,H,Lq,D], k/v [B,H,Lk,D] on the GPU, bf16 or fp16 (one dtype), D = 64 or 128, or fp32
@@ -110,9 +163,25 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
 
     `v_cols=32` (bf16, head dim 64, no row maps or tile masks): only v's first 32 columns
     enter P.V and the output is [B,H,Lq,32] (`sa_block_sparse_fwd_v32`; segment-indicator v).
+
+    fp16 scores (`sa_block_sparse_fwd_k16`; plain bf16 lists at head dim 64, no key_bias, row
+    maps, tile masks or key-range parts): an fp16 copy of k (exact for 2^-17 <= |k| < 65504)
+    and q scaled by sm_scale*log2(e) into fp16 inside the kernel, so the softmax takes no
+    multiply per score. A query block takes them only when max|q_i*sm_scale*log2(e)| *
+    max|k_j| <= 32 (row norms; it bounds every exp2-domain score), which limits each score's
+    change to about 2^-6; other blocks use the bf16 operands (`sa_block_sparse_fwd`, the
+    arithmetic of every other mode). The fp16 copy of k costs one pass over k (about 2.8 ns
+    per key block and head at C2 sizes, against about 0.03 ns saved per tile), which pays from
+    about 100 tiles per key block: by default (`fp16_scores=None`) a launch takes fp16 scores
+    when `k16` holds keys already made for this k (`prepare_fp16_keys`, or the pooling pass of
+    the mask builders, `with_fp16_keys`; possibly on another stream, whose event this call's
+    stream waits for) or when the lists are dense over at least DENSE_FP16_BLOCKS query and key
+    blocks; fp16_scores=True makes the copy here, False never. FP16_SCORES = False turns the
+    mode off everywhere.
     """
     _lib.require_gpu(q, k, v)
     types = (torch.bfloat16, torch.float16, torch.float32)
+    k_in = k
     q, k, v = _prep_qkv(q, types), _prep_qkv(k, types), _prep_qkv(v, types)
     if not q.dtype == k.dtype == v.dtype:
         raise TypeError(f"q, k, v must share one dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
@@ -191,6 +260,31 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
                 B, H, Lq, Lk, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, bias_ptr, bias_strides,
                 float(sm_scale), order.data_ptr(), order.numel(), _lib.stream_of(q))
         _lib.check(rc, "sa_block_sparse_fwd_v32")
+        return out
+    if fp16_scores is None:
+        fp16_scores = k16 is not None or (kv.dense and min(kv.nqb, kv.nkb) >= DENSE_FP16_BLOCKS)
+    fp16_scores = fp16_scores and FP16_SCORES
+    if fp16_scores and not fp16 and not fp32 and key_bias is None and D == 64:
+        # fp16 scores (`sa_block_sparse_fwd_k16`): an fp16 copy of k, and q scaled into the exp2
+        # domain in fp16 inside the kernel, so the softmax needs no multiply per score; query
+        # blocks whose score bound fails run on the bf16 operands.
+        stream = torch.cuda.current_stream(q.device)
+        if k16 is not None:
+            if not k16.matches(k_in):
+                raise ValueError("k16 was prepared for another k")
+            stream.wait_event(k16.event)
+            if k16.stream != stream:
+                k16.ws.record_stream(stream)
+            ws, prepared = k16.ws, 1
+        else:
+            ws, prepared = torch.empty(k16_workspace_bytes(B, H, Lk, D), dtype=torch.uint8, device=q.device), 0
+        with torch.cuda.device(q.device):
+            rc = lib.sa_block_sparse_fwd_k16(
+                q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
+                v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
+                B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, float(sm_scale),
+                order.data_ptr(), order.numel(), prepared, ws.data_ptr(), ws.numel(), stream.cuda_stream)
+        _lib.check(rc, "sa_block_sparse_fwd_k16")
         return out
     fn = "sa_block_sparse_fwd_f16" if fp16 else ("sa_block_sparse_fwd_f32" if fp32 else "sa_block_sparse_fwd")
     with torch.cuda.device(q.device):

@@ -544,7 +544,8 @@ def test_key_range_split_sparse_lists(dev):
 
 def test_key_range_split_matches_unsplit(dev):
     # The same query blocks in a launch with enough blocks to run unsplit: the outputs agree
-    # up to the fp32 summation order of the partials (one bf16 rounding step).
+    # up to the fp32 summation order of the partials (one bf16 rounding step). The unsplit
+    # launch takes the bf16 scores of the split one (fp16_scores=False).
     case("key-range split vs unsplit")
     Lk = 8192
     q, k, v = _rand((1, 2, 128, 64), 520), _rand((1, 2, Lk, 64), 521), _rand((1, 2, Lk, 64), 522)
@@ -553,7 +554,7 @@ def test_key_range_split_matches_unsplit(dev):
     kd, vd = k.to(dev), v.to(dev)
     small = block_sparse_attention(q.to(dev), kd, vd, dense_kv_list(1, 2, 2, Lk // 64, dev), 0.125)
     big = block_sparse_attention(q.repeat(1, 1, reps, 1).to(dev), kd, vd, dense_kv_list(1, 2, 2 * reps, Lk // 64, dev),
-                                 0.125)
+                                 0.125, fp16_scores=False)
     torch.cuda.synchronize()
     d = (small.float() - big[:, :, :128].float()).abs()
     assert d.max().item() <= 2 ** -8, d.max().item()
@@ -608,7 +609,8 @@ def test_v32_matches_first_columns(dev, with_bias):
     bias = torch.log(torch.randint(1, 5, (B, 1, Lk), generator=g).float()) if with_bias else None
     kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
     bd = None if bias is None else bias.to(dev)
-    full = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bd)
+    # the 64-column launch with the bf16 scores that the 32-column one computes
+    full = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bd, fp16_scores=False)
     wide = torch.full((B, H, Lq, 48), 5.0, dtype=torch.bfloat16, device=dev)
     got = block_sparse_attention(q.to(dev), k.to(dev), v.to(dev), kv, 0.125, key_bias=bd, out=wide[..., 8:40],
                                  v_cols=32)

@@ -1,0 +1,241 @@
+"""GPU tests of the fp16-score path of the block-sparse attention (`sa_block_sparse_fwd_k16`).
+
+Plain bf16 lists at head dim 64 compute their scores in fp16 by default: k is copied to fp16
+(exact for 2^-17 <= |k| < 65504) and q * sm_scale * log2(e) is rounded to fp16 inside the kernel. A query
+block takes them only when max_i |q_i * c| * max_j |k_j| <= 32 (row norms, c = sm_scale *
+log2(e); the head's largest key norm), with both squared norms below 4e9; every other block
+runs on the bf16 operands and is bit-identical to fp16_scores=False. Outputs are held to the
+attention bar against the fp64 oracle (max-abs 2e-2, mean-abs 2e-3, and the reference's
+allclose(1e-2, 1e-2)).
+"""
+import math
+
+import pytest
+import torch
+
+from conftest import case
+from oracle.attention import masked_attention
+from sparseattnfunctions_amd._kv import kv_list_from_mask
+from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+LOG2E = 1.4426950408889634
+BOUND = 32.0
+
+
+def _rand(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).bfloat16()
+
+
+def _check(got, want):
+    got = got.float().cpu().double()
+    err = (got - want).abs()
+    assert torch.isfinite(got).all()
+    assert err.max().item() <= MAX_ABS, err.max().item()
+    assert err.mean().item() <= MEAN_ABS, err.mean().item()
+    assert torch.allclose(got, want, atol=1e-2, rtol=1e-2)
+
+
+def _block_bounds(q, k, sm_scale):
+    """[B, H, nqb]: the kernel's bound max_i |q_i * c| * max_j |k_j| of each query block (fp64)."""
+    c = sm_scale * LOG2E
+    qn = (q.double() * c).pow(2).sum(-1)
+    kn = k.double().pow(2).sum(-1).amax(-1)
+    B, H, L = qn.shape
+    nqb = math.ceil(L / 64)
+    qb = torch.nn.functional.pad(qn, (0, nqb * 64 - L)).view(B, H, nqb, 64).amax(-1)
+    return (qb * kn[..., None]).sqrt()
+
+
+def _setup(q, k, v, seed, density=0.6):
+    B, H, Lq, _ = q.shape
+    Lk = k.shape[2]
+    nqb, nkb = math.ceil(Lq / 64), math.ceil(Lk / 64)
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.rand(B, H, nqb, nkb, generator=g) < density
+    mask[..., 0] = True
+    return mask, nqb, nkb
+
+
+def _both(q, k, v, mask, dev):
+    B, H, nqb, nkb = mask.shape
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o16 = block_sparse_attention(qd, kd, vd, kv, 0.125, fp16_scores=True)
+    obf = block_sparse_attention(qd, kd, vd, kv, 0.125, fp16_scores=False)
+    torch.cuda.synchronize()
+    return o16.cpu(), obf.cpu()
+
+
+def _rows(x, b, h, qb):
+    return x[b, h, 64 * qb: 64 * (qb + 1)]
+
+
+@pytest.mark.parametrize("k_scale", [1.0, 1.45])
+def test_fp16_scores_taken_within_bar(dev, k_scale):
+    # randn inputs: every block's bound is below 32 (about 20, and about 29 with k * 1.45), so
+    # every block runs on fp16 scores: the output differs from the bf16-score launch and stays
+    # within the bar.
+    case(f"fp16 scores taken, k scale {k_scale}")
+    q, k, v = _rand((2, 3, 700, 64), 900), _rand((2, 3, 1500, 64), 901), _rand((2, 3, 1500, 64), 902)
+    k = (k.float() * k_scale).bfloat16()
+    bounds = _block_bounds(q, k, 0.125)
+    assert bounds.max().item() < BOUND * 0.98 and bounds.max().item() > (26.0 if k_scale > 1 else 15.0)
+    mask, _, _ = _setup(q, k, v, 903)
+    o16, obf = _both(q, k, v, mask, "cuda")
+    assert not torch.equal(o16, obf)
+    want = masked_attention(q, k, v, mask, 0.125)
+    _check(o16, want)
+    _check(obf, want)
+
+
+def test_fp16_scores_bound_fails_everywhere(dev):
+    # k * 3: every bound is above 32, so every block runs on the bf16 operands.
+    case("fp16 scores: bound fails in every block")
+    q, k, v = _rand((1, 2, 500, 64), 910), _rand((1, 2, 900, 64), 911), _rand((1, 2, 900, 64), 912)
+    k = (k.float() * 3).bfloat16()
+    assert _block_bounds(q, k, 0.125).min().item() > BOUND * 1.05
+    mask, _, _ = _setup(q, k, v, 913)
+    o16, obf = _both(q, k, v, mask, "cuda")
+    assert torch.equal(o16, obf)
+    _check(o16, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_fp16_scores_mixed_blocks(dev):
+    # The query rows of block 1 of head (0, 1) scaled by 3: that block's bound passes 32 and it
+    # runs on the bf16 operands; the other blocks (bounds near 20) take fp16 scores.
+    case("fp16 scores: one block over the bound")
+    q, k, v = _rand((1, 2, 320, 64), 920), _rand((1, 2, 640, 64), 921), _rand((1, 2, 640, 64), 922)
+    q = q.float()
+    q[0, 1, 64:128] *= 3
+    q = q.bfloat16()
+    bounds = _block_bounds(q, k, 0.125)
+    assert bounds[0, 1, 1].item() > BOUND * 1.05
+    others = torch.ones_like(bounds, dtype=torch.bool)
+    others[0, 1, 1] = False
+    assert bounds[others].max().item() < BOUND * 0.9
+    mask, nqb, _ = _setup(q, k, v, 923, density=0.7)
+    o16, obf = _both(q, k, v, mask, "cuda")
+    assert torch.equal(_rows(o16, 0, 1, 1), _rows(obf, 0, 1, 1))
+    differ = [not torch.equal(_rows(o16, 0, h, b), _rows(obf, 0, h, b))
+              for h in range(2) for b in range(nqb) if (h, b) != (1, 1)]
+    assert sum(differ) >= len(differ) - 1
+    _check(o16, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_fp16_scores_outside_fp16_range(dev):
+    # Head 0 holds a key element of 1e5 (beyond fp16) with q scaled down so far that the
+    # Cauchy-Schwarz bound alone would pass: the squared-norm limit sends its blocks to the bf16
+    # operands. Head 1 is ordinary and takes fp16 scores.
+    case("fp16 scores: key beyond the fp16 range")
+    q, k, v = _rand((1, 2, 200, 64), 930), _rand((1, 2, 300, 64), 931), _rand((1, 2, 300, 64), 932)
+    q, k = q.float(), k.float()
+    q[0, 0] *= 1e-4
+    k[0, 0, 37, 5] = 1.0e5
+    q, k = q.bfloat16(), k.bfloat16()
+    assert _block_bounds(q, k, 0.125)[0, 0].max().item() < BOUND
+    mask, _, _ = _setup(q, k, v, 933, density=1.0)
+    o16, obf = _both(q, k, v, mask, "cuda")
+    assert torch.equal(o16[0, 0], obf[0, 0])
+    assert not torch.equal(o16[0, 1], obf[0, 1])
+    _check(o16, masked_attention(q, k, v, mask, 0.125))
+
+
+def test_fp16_scores_nan_key(dev):
+    # A NaN key element makes its head's norm NaN, which fails the bound: that head runs on the
+    # bf16 operands, bit for bit (NaN outputs in the same places); the other head takes fp16.
+    case("fp16 scores: NaN key")
+    q, k, v = _rand((1, 2, 192, 64), 940), _rand((1, 2, 256, 64), 941), _rand((1, 2, 256, 64), 942)
+    k = k.float()
+    k[0, 0, 70, 9] = float("nan")
+    k = k.bfloat16()
+    mask, _, _ = _setup(q, k, v, 943, density=1.0)
+    o16, obf = _both(q, k, v, mask, "cuda")
+    assert torch.equal(o16[0, 0].view(torch.int16), obf[0, 0].view(torch.int16))
+    assert torch.isnan(o16[0, 0]).any()
+    assert not torch.equal(o16[0, 1], obf[0, 1])
+    want = masked_attention(q[:, 1:], k[:, 1:], v[:, 1:], mask[:, 1:], 0.125)
+    _check(o16[:, 1:], want)
+
+
+def test_pool_k16_matches_prepare(dev):
+    # The pooling pass's fp16 keys (sa_block_pool_k16) equal sa_block_sparse_fwd_k16_prepare's
+    # bit for bit (strided k with a partial last block), the pooled means are those of
+    # sa_block_pool, and attention from either workspace gives the same output.
+    from sparseattnfunctions_amd.block_masks import pool_blocks
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import (k16_workspace_bytes,
+                                                                         prepare_fp16_keys)
+    case("fp16 keys: pooling pass vs prepare")
+    B, H, L = 2, 3, 1000
+    q = _rand((B, H, L, 64), 950).to(dev)
+    kw = _rand((B, L, H, 64), 951).to(dev)
+    k = kw.transpose(1, 2)  # strided view [B, H, L, 64]
+    v = _rand((B, H, L, 64), 952).to(dev)
+    prep = prepare_fp16_keys(k)
+    ws = torch.empty(k16_workspace_bytes(B, H, L, 64), dtype=torch.uint8, device=dev)
+    qp, kp = pool_blocks(q, k, 64, k16_ws=ws)
+    qp0, kp0 = pool_blocks(q, k, 64)
+    torch.cuda.synchronize()
+    assert torch.equal(qp, qp0) and torch.equal(kp, kp0)
+    nk = B * H * L * 64 * 2
+    off = (nk + 255) // 256 * 256
+    nb = math.ceil(L / 64)
+    assert torch.equal(ws[:nk], prep.ws[:nk])
+    assert torch.equal(ws[off:off + B * H * nb * 4], prep.ws[off:off + B * H * nb * 4])
+    # the fp16 copy is k rounded to fp16 (torch's conversion, round to nearest even): k itself
+    # from 2^-17 up, fp16's subnormal grid below
+    k16 = ws[:nk].view(torch.float16).view(B, H, L, 64)
+    assert torch.equal(k16, k.half())
+    big = k.float().abs() >= 2.0 ** -17
+    assert torch.equal(k16.float()[big], k.float()[big])
+    g = torch.Generator().manual_seed(953)
+    mask = torch.rand(B, H, nb, nb, generator=g) < 0.5
+    mask[..., 0] = True
+    kv = kv_list_from_mask(mask.to(dev), B, H, nb, nb)
+    o_prep = block_sparse_attention(q, k, v, kv, 0.125, k16=prep)
+    o_inline = block_sparse_attention(q, k, v, kv, 0.125, fp16_scores=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_prep, o_inline)
+    _check(o_prep, masked_attention(q.cpu(), k.cpu(), v.cpu(), mask, 0.125))
+
+
+def test_processor_fp16_keys_from_pool(dev):
+    # BlockSparseAttention.forward takes the pooling pass's fp16 keys: the same output as the
+    # kernel-level call on the same lists with the keys prepared inline; the kernel-level call
+    # on these (sparse) lists defaults to bf16 scores.
+    from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention
+    from sparseattnfunctions_amd.workloads import Geometry
+    case("BlockSparseAttention with fp16 keys from the pooling pass")
+    geom = Geometry(text_len=100, T=3, Hp=12, Wp=16)
+    L = geom.L
+    q, k, v = (_rand((1, 2, L, 64), 960 + i).to(dev) for i in range(3))
+    proc = BlockSparseAttention(64, keep_ratio=0.3, geometry=geom)
+    out = proc(q, k, v)
+    kv = proc.last_kv
+    want = block_sparse_attention(q, k, v, kv, proc.sm_scale, n_text_blocks=proc.n_text_blocks(), fp16_scores=True)
+    bf = block_sparse_attention(q, k, v, kv, proc.sm_scale, n_text_blocks=proc.n_text_blocks())  # default: bf16
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    assert not torch.equal(out, bf)
+
+
+def test_fp16_scores_default_selection(dev):
+    # fp16_scores=None: dense lists over at least 128 x 128 blocks take fp16 scores, smaller
+    # dense lists bf16 (both checked against the explicit choices). 16 heads of 128 query
+    # blocks fill the wave slots, so neither launch is split into key ranges (which keeps bf16).
+    from sparseattnfunctions_amd.block_mask_attn import dense_kv_list
+    case("fp16 scores: default selection")
+    q, k, v = (_rand((1, 16, 128 * 64, 64), 970 + i).to(dev) for i in range(3))
+    big = dense_kv_list(1, 16, 128, 128, dev)
+    small_q = q[:, :, :127 * 64]
+    small = dense_kv_list(1, 16, 127, 128, dev)
+    o_big = block_sparse_attention(q, k, v, big, 0.125)
+    o_small = block_sparse_attention(small_q, k, v, small, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(o_big, block_sparse_attention(q, k, v, big, 0.125, fp16_scores=True))
+    assert not torch.equal(o_big, block_sparse_attention(q, k, v, big, 0.125, fp16_scores=False))
+    assert torch.equal(o_small, block_sparse_attention(small_q, k, v, small, 0.125, fp16_scores=False))

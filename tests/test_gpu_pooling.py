@@ -3,7 +3,7 @@
 Tolerances: out max-abs <= 2e-2 and mean-abs <= 2e-3 (the attention bar); Po relative 5e-3
 (+1e-7 absolute): its entries are exp2 of fp32 logits minus the row's log-sum-exp, whose
 row sum accumulates bf16-rounded probabilities.
-At the C2 shape, size-independent properties: out is bit-identical to the block-sparse kernel
+At the C2 shape, size-independent properties: out is bit-identical to the block-sparse kernel (bf16 scores)
 over every block (the pooling mode only adds stores), Po rows sum to one, causal Po is zero
 above the diagonal.
 """
@@ -181,5 +181,6 @@ def test_pooled_attention_c2_shape_properties(dev, causal):
                                                                v[:1, :2].float(), is_causal=True)
         assert (o[:1, :2].float() - ref).abs().max().item() <= 2e-2
     else:
-        dense = block_sparse_attention(q, k, v, dense_kv_list(B, H, nd, nd, q.device), 0.125)
+        # the plain kernel with the bf16 scores that the pooling mode computes
+        dense = block_sparse_attention(q, k, v, dense_kv_list(B, H, nd, nd, q.device), 0.125, fp16_scores=False)
         assert torch.equal(o, dense)
