@@ -117,7 +117,7 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
 
 /*
  * sa_block_sparse_fwd with the scores in fp16 (same block_sparse_attn_kernel.py:52-209 work,
- * bf16 q, k, v and out, head dim 64, no key_bias). The workspace holds an fp16 copy of k (round
+ * bf16 q, k, v and out, head dim 64, optional key_bias as there). The workspace holds an fp16 copy of k (round
  * to nearest even: exact for 2^-17 <= |k| < 65504, on fp16's subnormal grid below, an absolute
  * error of at most 2^-25) and the largest squared key-row norm of each 64-row key block,
  * written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16 (or by this call first, with
@@ -128,19 +128,22 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
  * every |S * sm_scale * log2(e)| by 32 (Cauchy-Schwarz), and the 2^-11 relative rounding of each
  * q element then moves a score by at most 2^-6 in the exp2 domain. Any other query block (or
  * one with a NaN norm) runs exactly as in sa_block_sparse_fwd. Row sums, P (bf16) and P.V are
- * as there. The fp16 operands have no counterpart in the reference, whose kernel scales the
+ * as there. A key bias is first written to the workspace multiplied by log2(e) (the product the
+ * bf16 path forms per tile), and the fp16 path's S MFMAs start from it. The fp16 operands have no counterpart in the reference, whose kernel scales the
  * fp32 scores (:84-85).
- *   workspace  256-byte aligned, >= sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64) bytes; with
- *              prepared = 1 it must hold this k's preparation, done earlier in stream order
- *              (another stream: the caller orders the two).
+ *   workspace  256-byte aligned, >= sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, with_bias)
+ *              bytes (with_bias: room for the scaled bias too); with prepared = 1 it must hold
+ *              this k's preparation, done earlier in stream order (another stream: the caller
+ *              orders the two).
  */
-int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int64_t* bytes);
+int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int with_bias, int64_t* bytes);
 int sa_block_sparse_fwd_k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int Lk,
                                     int D, void* workspace, int64_t workspace_bytes, void* stream);
 int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
                             const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
                             uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
-                            int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt, float sm_scale,
+                            int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
+                            const float* key_bias, const int64_t bias_strides[2], float sm_scale,
                             const int32_t* work_order, int64_t n_slots, int prepared, void* workspace,
                             int64_t workspace_bytes, void* stream);
 

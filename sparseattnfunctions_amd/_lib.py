@@ -75,12 +75,12 @@ _PROTOTYPES = {
     "sa_attn_work_order": (_I, [_I, _I, _I, _I, _I, _P, _I64P]),
     "sa_attn_split_parts": (_I, [ctypes.c_int64, _I, _I, _I, ctypes.POINTER(_I)]),
     "sa_attn_split_workspace": (_I, [ctypes.c_int64, _I, _I, _I64P]),
-    "sa_block_sparse_fwd_k16_workspace": (_I, [_I, _I, _I, _I, _I64P]),
+    "sa_block_sparse_fwd_k16_workspace": (_I, [_I, _I, _I, _I, _I, _I64P]),
     "sa_block_sparse_fwd_k16_prepare": (_I, [_P, _I64P, _I, _I, _I, _I, _P, ctypes.c_int64, _P]),
     "sa_block_sparse_fwd_k16": (
         _I,
-        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P, ctypes.c_int64, _I,
-         _P, ctypes.c_int64, _P],
+        [_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I, _I, _I, _I, _P, _P, _I, _P, _I64P, _F, _P,
+         ctypes.c_int64, _I, _P, ctypes.c_int64, _P],
     ),
     "sa_block_sparse_fwd_split": (
         _I,

@@ -286,8 +286,10 @@ constexpr int kWaitLgkm0 = 0xC07F;
 // copied as usual and only their first 32 columns are read; out has 32 columns).
 template <bool kBias, bool kMask, int kPool, typename T = __bf16, int kD = 64, int kDV = kD, bool kK16 = false>
 __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs a) {
-  static_assert(!kK16 || (!kBias && !kMask && kPool == 0 && std::is_same<T, __bf16>::value && kD == 64 && kDV == 64),
-                "fp16 scores: plain bf16 lists at head dim 64");
+  static_assert(!kK16 || (!kMask && kPool == 0 && std::is_same<T, __bf16>::value && kD == 64 && kDV == 64),
+                "fp16 scores: plain or key-bias bf16 lists at head dim 64");
+  // With fp16 scores the key bias arrives multiplied by log2(e) (the entry point's scaled copy).
+  constexpr bool kBiasLog2 = kK16;
   static_assert(kPool == 0 || ((kPool == 32 || kPool == 64) && !kBias), "pooling: 32- or 64-key columns, no bias");
   static_assert(kD == 64 || kD == 128, "head dim 64 or 128");
   static_assert(kDV == kD || (kDV == 32 && kD == 64 && kPool == 0 && !kMask), "32 value columns: head dim 64");
@@ -513,8 +515,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       const int r = 8 * p + (lane >> 3);
       kgo[p] = (lane >> 3) * krow + 16 * ((lane & 7) ^ swz(r));
     }
-    if (cnt > beg) {
+    if (cnt > beg) {  // the first copies of run(), in its order
       const int kb0 = entry(beg);
+      if (kBias) issue_bias(beg);
       issue_k(kb0, beg);
       issue_v(kb0, beg);
       issued16 = true;
@@ -622,13 +625,31 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
       issue_k(kb_next, it_next);
 
       // ---- S^T = K Q^T: S[g][c] element e is key 32c + 8(e/4) + 4hh + e%4, query 32g + col.
+      // fp16 scores with a key bias: the MFMA chains start from the tile's biases (log2 units),
+      // so S = K (q * scale_log2)^T + bias * log2(e) takes no VALU at all.
+      sa_f32x16 bias0[2] = {};
+      if constexpr (kQ16 && kBias) {
+        // This tile's bias copy was issued before the previous tile's V copy, so the wait for
+        // this tile's K copy at the top covered it.
+        const float* bt = bl_lds + (it & 1) * kBlock;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 b4 = *reinterpret_cast<const float4*>(bt + 32 * c + 8 * q4 + 4 * hh);
+            bias0[c][4 * q4] = b4.x;
+            bias0[c][4 * q4 + 1] = b4.y;
+            bias0[c][4 * q4 + 2] = b4.z;
+            bias0[c][4 * q4 + 3] = b4.w;
+          }
+      }
       sa_f32x16 S[2][2];
-      
+
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          sa_f32x16 t = {};
+          sa_f32x16 t = bias0[c];
 #pragma unroll
           for (int s = 0; s < kDS; ++s) {
             if constexpr (kQ16)
@@ -639,7 +660,7 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
           S[g][c] = t;
         }
       
-      if (kBias) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
+      if (kBias && !kQ16) {  // S = (s * sm_scale + bias) * log2(e), the exp2 domain
         // This tile's bias copy was issued before the previous tile's V copy, so the wait for
         // this tile's K copy at the top covered it.
         const float* bt = bl_lds + (it & 1) * kBlock;
@@ -648,7 +669,8 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             const float4 b4 = *reinterpret_cast<const float4*>(bt + 32 * c + 8 * q4 + 4 * hh);
-            const float bq[4] = {b4.x * kLog2e, b4.y * kLog2e, b4.z * kLog2e, b4.w * kLog2e};
+            const float bq[4] = {kBiasLog2 ? b4.x : b4.x * kLog2e, kBiasLog2 ? b4.y : b4.y * kLog2e,
+                                 kBiasLog2 ? b4.z : b4.z * kLog2e, kBiasLog2 ? b4.w : b4.w * kLog2e};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               S[0][c][4 * q4 + j] = fmaf(S[0][c][4 * q4 + j], a.scale_log2, bq[j]);
@@ -1380,8 +1402,9 @@ template <typename T, int kD>
 void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask, bool bias, int pool_cols,
                     bool v32 = false) {
   if constexpr (kD == 64 && std::is_same<T, __bf16>::value) {
-    if (a.k16) {  // fp16 scores (the caller has rejected every other mode)
-      hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, kD, true>), g, blk, 0, s, a);
+    if (a.k16) {  // fp16 scores (the caller has rejected every mode but the key bias)
+      if (bias) hipLaunchKernelGGL((bsa_fwd_kernel<true, false, 0, T, kD, kD, true>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((bsa_fwd_kernel<false, false, 0, T, kD, kD, true>), g, blk, 0, s, a);
       return;
     }
     if (v32) {  // 32 value columns (the caller has rejected tile masks and pooling)
@@ -1474,9 +1497,9 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.ws = nullptr;
   a.k16 = k16;
   a.k16_norm2 = k16_norm2;
-  if (k16 && (!k16_norm2 || D != 64 || fp16 || v32 || kv_slot || key_bias || pool_cols || parts != 1 || q_rows ||
-              o_rows || kv_rep != 1))
-    return sa::fail(SA_ERR_UNSUPPORTED, "%s: fp16 scores need plain bf16 lists at head dim 64", fn);
+  if (k16 && (!k16_norm2 || D != 64 || fp16 || v32 || kv_slot || pool_cols || parts != 1 || q_rows || o_rows ||
+              kv_rep != 1))
+    return sa::fail(SA_ERR_UNSUPPORTED, "%s: fp16 scores need plain or key-bias bf16 lists at head dim 64", fn);
   a.kv_idx = kv_idx; a.kv_cnt = kv_cnt; a.max_cnt = max_cnt;
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
@@ -1688,13 +1711,24 @@ __global__ __launch_bounds__(256) void k16_kernel(K16Args a) {
 using sa::k16_bytes;
 using sa::k16_ws_bytes;
 
+// bias2[(b * H + h) * Lk + j] = bias[b * sb + h * sh + j] * log2(e): the key bias in the exp2
+// domain for the fp16-score kernel (the bf16-score kernel forms the same product per tile).
+__global__ __launch_bounds__(256) void bias_log2_kernel(const float* bias, int64_t sb, int64_t sh, int H, int Lk,
+                                                        int64_t n, float* bias2) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t bh = i / Lk, j = i - bh * Lk;
+  const int64_t b = bh / H, h = bh - b * H;
+  bias2[i] = bias[b * sb + h * sh + j] * kLog2e;
+}
+
 }  // namespace
 
-extern "C" int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int64_t* bytes) {
+extern "C" int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int with_bias, int64_t* bytes) {
   SA_REQUIRE(bytes, "sa_block_sparse_fwd_k16_workspace: null bytes");
   SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "sa_block_sparse_fwd_k16_workspace: bad shape B=%d H=%d Lk=%d", B, H, Lk);
   if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd_k16_workspace: head_dim %d (64)", D);
-  *bytes = k16_ws_bytes(B, H, Lk);
+  *bytes = with_bias ? sa::k16_ws_bytes_bias(B, H, Lk) : k16_ws_bytes(B, H, Lk);
   return sa::ok();
 }
 
@@ -1735,9 +1769,16 @@ extern "C" int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_stride
                                        const int64_t k_strides[3], const uint16_t* v, const int64_t v_strides[3],
                                        uint16_t* out, const int64_t out_strides[3], int B, int H, int Lq, int Lk,
                                        int D, const int32_t* kv_idx, const int32_t* kv_cnt, int max_cnt,
-                                       float sm_scale, const int32_t* work_order, int64_t n_slots, int prepared,
-                                       void* workspace, int64_t workspace_bytes, void* stream) {
+                                       const float* key_bias, const int64_t bias_strides[2], float sm_scale,
+                                       const int32_t* work_order, int64_t n_slots, int prepared, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   const char* fn = "sa_block_sparse_fwd_k16";
+  SA_REQUIRE(!key_bias || bias_strides, "%s: key_bias without bias_strides", fn);
+  if (key_bias) {
+    SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
+    SA_REQUIRE(workspace_bytes >= sa::k16_ws_bytes_bias(B, H, Lk), "%s: workspace of %lld bytes < %lld with key_bias",
+               fn, (long long)workspace_bytes, (long long)sa::k16_ws_bytes_bias(B, H, Lk));
+  }
   int rc = prepared ? SA_OK : k16_prepare(k, k_strides, B, H, Lk, D, workspace, workspace_bytes, stream, fn);
   if (rc) return rc;
   if (prepared) {  // the same checks of the workspace, without the launches
@@ -1750,8 +1791,18 @@ extern "C" int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_stride
   }
   const uint16_t* k16 = static_cast<const uint16_t*>(workspace);
   const uint32_t* norm2 = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(workspace) + k16_bytes(B, H, Lk));
+  const float* bias2 = nullptr;
+  int64_t bias2_strides[2] = {(int64_t)H * Lk, Lk};
+  if (key_bias) {  // the bias in log2 units, behind the k16 part of the workspace
+    float* b2 = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + sa::k16_bias_offset(B, H, Lk));
+    const int64_t n = (int64_t)B * H * Lk;
+    hipLaunchKernelGGL(bias_log2_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, sa::as_stream(stream),
+                       key_bias, bias_strides[0], bias_strides[1], H, Lk, n, b2);
+    if ((rc = sa::check_launch(fn))) return rc;
+    bias2 = b2;
+  }
   return launch_fwd(q, q_strides, k, k_strides, v, v_strides, out, out_strides, B, H, Lq, Lk, D, kv_idx, kv_cnt,
-                    max_cnt, false, nullptr, nullptr, nullptr, nullptr, sm_scale, work_order, n_slots, nullptr, 0,
+                    max_cnt, false, nullptr, nullptr, bias2, bias2_strides, sm_scale, work_order, n_slots, nullptr, 0,
                     nullptr, 0, stream, fn, 1, 0, nullptr, nullptr, nullptr, false, false, 1, nullptr, 0, k16, norm2);
 }
 

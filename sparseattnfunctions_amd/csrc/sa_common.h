@@ -46,6 +46,9 @@ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 // (fp32 bits), [B*H][ceil(Lk/64)]. Written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16.
 inline int64_t k16_bytes(int B, int H, int Lk) { return ((int64_t)B * H * Lk * 64 * 2 + 255) / 256 * 256; }
 inline int64_t k16_ws_bytes(int B, int H, int Lk) { return k16_bytes(B, H, Lk) + (int64_t)B * H * cdiv(Lk, 64) * 4; }
+// With a key bias: then, 256-byte aligned, the bias times log2(e), fp32 [B*H][Lk] contiguous.
+inline int64_t k16_bias_offset(int B, int H, int Lk) { return (k16_ws_bytes(B, H, Lk) + 255) / 256 * 256; }
+inline int64_t k16_ws_bytes_bias(int B, int H, int Lk) { return k16_bias_offset(B, H, Lk) + (int64_t)B * H * Lk * 4; }
 
 // fp32 attention in pooling mode (attn_f32.hip), for the pooled-map entry point.
 int attn_f32_pooling(const float* q, const int64_t q_strides[3], const float* k, const int64_t k_strides[3],

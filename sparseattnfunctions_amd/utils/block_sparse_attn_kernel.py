@@ -67,11 +67,13 @@ def split_workspace_bytes(n_items: int, D: int, parts: int) -> int:
     return n.value
 
 
-def k16_workspace_bytes(B: int, H: int, Lk: int, D: int) -> int:
-    """Bytes of the fp16-score workspace (`sa_block_sparse_fwd_k16_workspace`): an fp16 copy of k
-    and the largest squared key-row norm of each head."""
+def k16_workspace_bytes(B: int, H: int, Lk: int, D: int, with_bias: bool = False) -> int:
+    """Bytes of the fp16-score workspace (`sa_block_sparse_fwd_k16_workspace`): an fp16 copy of k,
+    the largest squared key-row norm of each 64-row key block and, with_bias, the key bias times
+    log2(e)."""
     n = ctypes.c_int64(0)
-    _lib.check(_lib.load().sa_block_sparse_fwd_k16_workspace(int(B), int(H), int(Lk), int(D), ctypes.byref(n)),
+    _lib.check(_lib.load().sa_block_sparse_fwd_k16_workspace(int(B), int(H), int(Lk), int(D), int(bool(with_bias)),
+                                                              ctypes.byref(n)),
                "sa_block_sparse_fwd_k16_workspace")
     return n.value
 
@@ -164,7 +166,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     `v_cols=32` (bf16, head dim 64, no row maps or tile masks): only v's first 32 columns
     enter P.V and the output is [B,H,Lq,32] (`sa_block_sparse_fwd_v32`; segment-indicator v).
 
-    fp16 scores (`sa_block_sparse_fwd_k16`; plain bf16 lists at head dim 64, no key_bias, row
+    fp16 scores (`sa_block_sparse_fwd_k16`; plain or key-bias bf16 lists at head dim 64, no row
     maps, tile masks or key-range parts): an fp16 copy of k (exact for 2^-17 <= |k| < 65504)
     and q scaled by sm_scale*log2(e) into fp16 inside the kernel, so the softmax takes no
     multiply per score. A query block takes them only when max|q_i*sm_scale*log2(e)| *
@@ -264,7 +266,7 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     if fp16_scores is None:
         fp16_scores = k16 is not None or (kv.dense and min(kv.nqb, kv.nkb) >= DENSE_FP16_BLOCKS)
     fp16_scores = fp16_scores and FP16_SCORES
-    if fp16_scores and not fp16 and not fp32 and key_bias is None and D == 64:
+    if fp16_scores and not fp16 and not fp32 and D == 64:
         # fp16 scores (`sa_block_sparse_fwd_k16`): an fp16 copy of k, and q scaled into the exp2
         # domain in fp16 inside the kernel, so the softmax needs no multiply per score; query
         # blocks whose score bound fails run on the bf16 operands.
@@ -272,18 +274,23 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
         if k16 is not None:
             if not k16.matches(k_in):
                 raise ValueError("k16 was prepared for another k")
+            if key_bias is not None:
+                raise ValueError("k16 with key_bias: the prepared workspace holds no bias (pass fp16_scores=True)")
             stream.wait_event(k16.event)
             if k16.stream != stream:
                 k16.ws.record_stream(stream)
             ws, prepared = k16.ws, 1
         else:
-            ws, prepared = torch.empty(k16_workspace_bytes(B, H, Lk, D), dtype=torch.uint8, device=q.device), 0
+            ws = torch.empty(k16_workspace_bytes(B, H, Lk, D, with_bias=key_bias is not None), dtype=torch.uint8,
+                             device=q.device)
+            prepared = 0
         with torch.cuda.device(q.device):
             rc = lib.sa_block_sparse_fwd_k16(
                 q.data_ptr(), _lib.i64(*q.stride()[:3]), k.data_ptr(), _lib.i64(*k.stride()[:3]),
                 v.data_ptr(), _lib.i64(*v.stride()[:3]), out.data_ptr(), _lib.i64(*out.stride()[:3]),
-                B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, float(sm_scale),
-                order.data_ptr(), order.numel(), prepared, ws.data_ptr(), ws.numel(), stream.cuda_stream)
+                B, H, Lq, Lk, D, kv.idx.data_ptr(), kv.cnt.data_ptr(), kv.max_cnt, bias_ptr, bias_strides,
+                float(sm_scale), order.data_ptr(), order.numel(), prepared, ws.data_ptr(), ws.numel(),
+                stream.cuda_stream)
         _lib.check(rc, "sa_block_sparse_fwd_k16")
         return out
     fn = "sa_block_sparse_fwd_f16" if fp16 else ("sa_block_sparse_fwd_f32" if fp32 else "sa_block_sparse_fwd")

@@ -239,3 +239,32 @@ def test_fp16_scores_default_selection(dev):
     assert torch.equal(o_big, block_sparse_attention(q, k, v, big, 0.125, fp16_scores=True))
     assert not torch.equal(o_big, block_sparse_attention(q, k, v, big, 0.125, fp16_scores=False))
     assert torch.equal(o_small, block_sparse_attention(small_q, k, v, small, 0.125, fp16_scores=False))
+
+
+@pytest.mark.parametrize("k_scale", [1.0, 3.0])
+def test_fp16_scores_key_bias(dev, k_scale):
+    # A log(size) key bias (MergeAttention's proportional attention) with fp16 scores: the S
+    # MFMAs start from the bias times log2(e). k * 1: every block takes fp16 scores (outputs
+    # differ from the bf16 path, both within the bar); k * 3: every bound fails and the output
+    # is the bf16 bias path's bit for bit (the bias pre-scaled by log2(e) in the workspace is
+    # the product that path forms per tile).
+    case(f"fp16 scores with a key bias, k scale {k_scale}")
+    B, H, L = 1, 2, 1200
+    q, k, v = _rand((B, H, L, 64), 980), _rand((B, H, L, 64), 981), _rand((B, H, L, 64), 982)
+    k = (k.float() * k_scale).bfloat16()
+    g = torch.Generator().manual_seed(983)
+    bias = torch.log(torch.randint(1, 9, (B, 1, L), generator=g).float())
+    bounds = _block_bounds(q, k, 0.125)
+    if k_scale == 1.0:
+        assert bounds.max().item() < BOUND * 0.98
+    else:
+        assert bounds.min().item() > BOUND * 1.05
+    mask, nqb, nkb = _setup(q, k, v, 984, density=0.6)
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    qd, kd, vd, bd = q.to(dev), k.to(dev), v.to(dev), bias.to(dev)
+    o16 = block_sparse_attention(qd, kd, vd, kv, 0.125, key_bias=bd, fp16_scores=True)
+    obf = block_sparse_attention(qd, kd, vd, kv, 0.125, key_bias=bd, fp16_scores=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o16, obf) == (k_scale != 1.0)
+    want = masked_attention(q, k, v, mask, 0.125, key_bias=bias.double())
+    _check(o16, want)
