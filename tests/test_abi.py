@@ -1,6 +1,7 @@
 """The C ABI library loads, exports every symbol include/sa_api.h declares, and rejects bad
 arguments before touching the GPU (no compute calls here; runs without a GPU)."""
 import ctypes
+import math
 import os
 import re
 
@@ -145,6 +146,55 @@ def test_split_launch_validates_workspace(lib):
     assert call(4, dummy, need.value - 1) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
     assert call(4, ctypes.c_void_p(4104), need.value) == _lib.SA_ERR_INVALID
     assert b"aligned" in lib.sa_last_error()
+
+
+def test_k16_workspace_query(lib):
+    # fp16 copy of k (256-byte aligned), one norm per 64-row key block, then (with_bias) the
+    # bias times log2(e), 256-byte aligned.
+    n = ctypes.c_int64(-1)
+    B, H, Lk = 2, 30, 17776
+    k16 = (B * H * Lk * 64 * 2 + 255) // 256 * 256
+    norms = B * H * math.ceil(Lk / 64) * 4
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, 0, ctypes.byref(n)) == _lib.SA_OK
+    assert n.value == k16 + norms
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, 1, ctypes.byref(n)) == _lib.SA_OK
+    assert n.value == (k16 + norms + 255) // 256 * 256 + B * H * Lk * 4
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 128, 0, ctypes.byref(n)) == _lib.SA_ERR_UNSUPPORTED
+    assert lib.sa_block_sparse_fwd_k16_workspace(0, H, Lk, 64, 0, ctypes.byref(n)) == _lib.SA_ERR_INVALID
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, 0, None) == _lib.SA_ERR_INVALID
+
+
+def test_k16_launches_validate_workspace(lib):
+    # fp16-score entry points reject a missing, short or misaligned workspace, a bias without
+    # strides and other head dims before any GPU work.
+    dummy = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    s3 = _lib.i64(0, 0, 0)
+    B, H, Lq, Lk, D = 1, 2, 128, 1024, 64
+    need, need_b = ctypes.c_int64(0), ctypes.c_int64(0)
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, D, 0, ctypes.byref(need)) == _lib.SA_OK
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, D, 1, ctypes.byref(need_b)) == _lib.SA_OK
+
+    def fwd(prepared, ws, nbytes, bias=None, bias_strides=None, d=D):
+        return lib.sa_block_sparse_fwd_k16(dummy, s3, dummy, s3, dummy, s3, dummy, s3, B, H, Lq, Lk, d, dummy, dummy,
+                                           Lk // 64, bias, bias_strides, 0.125, None, 0, prepared, ws, nbytes, None)
+
+    for prepared in (0, 1):
+        assert fwd(prepared, None, need.value) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
+        assert fwd(prepared, dummy, need.value - 1) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
+        assert fwd(prepared, ctypes.c_void_p(4096 + 16), need.value) == _lib.SA_ERR_INVALID
+        assert b"aligned" in lib.sa_last_error()
+        assert fwd(prepared, dummy, need.value, d=128) == _lib.SA_ERR_UNSUPPORTED
+        # a key bias needs its strides, and the larger workspace
+        assert fwd(prepared, dummy, need_b.value, bias=dummy) == _lib.SA_ERR_INVALID
+        assert fwd(prepared, dummy, need.value, bias=dummy, bias_strides=_lib.i64(0, 0)) == _lib.SA_ERR_INVALID
+        assert b"key_bias" in lib.sa_last_error()
+    assert lib.sa_block_sparse_fwd_k16_prepare(dummy, s3, B, H, Lk, D, dummy, need.value - 1, None) == _lib.SA_ERR_INVALID
+    assert lib.sa_block_sparse_fwd_k16_prepare(dummy, s3, B, H, Lk, 128, dummy, need.value, None) == \
+        _lib.SA_ERR_UNSUPPORTED
+    assert lib.sa_block_pool_k16(dummy, s3, dummy, s3, B, H, Lk, D, dummy, dummy, dummy, need.value - 1,
+                                 None) == _lib.SA_ERR_INVALID
+    assert lib.sa_block_pool_k16(dummy, s3, None, s3, B, H, Lk, D, dummy, dummy, dummy, need.value,
+                                 None) == _lib.SA_ERR_INVALID
 
 
 def test_library_allocates_no_device_memory():
