@@ -482,9 +482,9 @@ __global__ __launch_bounds__(256, kD == 64 ? 2 : 1) void bsa_fwd_kernel(FwdArgs 
   // kK16NormMax, so no element reaches the fp16 range limit. k16 then equals k from 2^-17 up
   // (smaller elements move by at most 2^-25) and fp16(q * scale_log2) has a relative error of
   // at most 2^-11 per element (absolute 2^-25 below fp16's normal range): each logit moves by
-  // about 2^-11 * kK16Bound at most in the exp2 domain. Otherwise (or with a NaN) the item runs on the bf16 operands. The item's first K
-  // tile (from k16) and V tile are requested before the bound is known; an item that fails it
-  // waits for them and starts again from k.
+  // about 2^-11 * kK16Bound at most in the exp2 domain. Otherwise (or with a NaN) the item runs
+  // on the bf16 operands. The item's first K tile (from k16) and V tile are requested before the
+  // bound is known; an item that fails it waits for them and starts again from k.
   bool use16 = false;
   bool issued16 = false;  // the first copies of the fp16 pass are in flight
   if constexpr (kK16) {
@@ -1650,8 +1650,8 @@ extern "C" int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3]
 namespace {
 
 // fp16 copy of k for the fp16-score mode: k16[bh][j] = fp16(k[b][h][j]) (round to nearest
-// even: exact for 2^-17 <= |k| < 65504, fp16's subnormal grid below), and blk_norm2[bh * nkb + kb] =
-// the largest squared row norm of key block kb (fp32 fmaf chain over the 64 dims, as float
+// even: exact for 2^-17 <= |k| < 65504, fp16's subnormal grid below), and blk_norm2[bh * nkb +
+// kb] = the largest squared row norm of key block kb (fp32 fmaf chain over the 64 dims, as float
 // bits, compared as unsigned: the norms are non-negative, and NaN bits compare above every
 // finite or infinite norm, so a NaN row fails the attention kernel's bound). One wave per
 // 64-row key block, 8 lanes per row (16 bytes each). sa_block_pool_k16 writes the same from
