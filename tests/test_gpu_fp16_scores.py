@@ -268,3 +268,39 @@ def test_fp16_scores_key_bias(dev, k_scale):
     assert torch.equal(o16, obf) == (k_scale != 1.0)
     want = masked_attention(q, k, v, mask, 0.125, key_bias=bias.double())
     _check(o16, want)
+
+
+@pytest.mark.parametrize("Lq,Lk", [(1, 7), (65, 64), (333, 130), (700, 1000)])
+def test_fp16_scores_strided_ragged_empty(dev, Lq, Lk):
+    # Strided q, k, v and out (views of [B, L, H, 64] buffers), partial last blocks down to one
+    # query row and seven keys, query blocks with empty lists (they write 0) and sm_scale 0.09:
+    # every query block that takes fp16 scores stays within the bar, and the blocks whose bound
+    # fails (or whose list is empty) are the bf16-score launch's bit for bit.
+    case(f"fp16 scores: strided views, Lq {Lq}, Lk {Lk}, empty lists")
+    B, H, scale = 2, 3, 0.09
+    qw, kw, vw = _rand((B, Lq, H, 64), 990), _rand((B, Lk, H, 64), 991), _rand((B, Lk, H, 64), 992)
+    kw = kw.float()
+    kw[1] *= 6.0  # batch 1: bounds of 50-90, so those blocks run on the bf16 operands
+    kw = kw.bfloat16()
+    q, k, v = (t.transpose(1, 2) for t in (qw, kw, vw))
+    mask, nqb, nkb = _setup(q, k, v, 993, density=0.6)
+    mask[0, 1, 0] = False  # empty lists
+    mask[1, 2, nqb - 1] = False
+    bounds = _block_bounds(q, k, scale)
+    kv = kv_list_from_mask(mask.to(dev), B, H, nqb, nkb)
+    qd, kd, vd = (t.to(dev).transpose(1, 2) for t in (qw, kw, vw))
+    assert qd.stride(2) == kd.stride(2) == vd.stride(2) == H * 64  # rows of the [B, L, H, 64] buffers
+    o16 = torch.full((B, Lq, H, 64), 7.0, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    obf = torch.full((B, Lq, H, 64), 7.0, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    block_sparse_attention(qd, kd, vd, kv, scale, out=o16, fp16_scores=True)
+    block_sparse_attention(qd, kd, vd, kv, scale, out=obf, fp16_scores=False)
+    torch.cuda.synchronize()
+    o16, obf = o16.cpu(), obf.cpu()
+    assert bounds[1].min().item() > BOUND * 1.05 and bounds[0].max().item() < BOUND * 0.9
+    assert torch.equal(o16[1], obf[1])
+    assert (o16[0, 1, :64] == 0).all() and (o16[1, 2, 64 * (nqb - 1):] == 0).all()
+    if Lk > 7:
+        assert not torch.equal(o16[0], obf[0])
+    want = masked_attention(q, k, v, mask, scale)
+    _check(o16, want)
+    _check(obf, want)
