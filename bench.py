@@ -116,7 +116,8 @@ def other_configs(q, k, v, dev):
     from sparseattnfunctions_amd.block_mask_attn import BlockSparseAttention, dense_kv_list
     from sparseattnfunctions_amd.combined_attn import CombinedAttn
     from sparseattnfunctions_amd.MergeAttention import MergeAttention
-    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import block_sparse_attention, block_sparse_triton_fn
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import (block_sparse_attention, block_sparse_triton_fn,
+                                                                         prepare_fp16_keys)
     from sparseattnfunctions_amd.workloads import COGVIDEOX_2B, cogvideox_qkv, config1_inputs
 
     out = {}
@@ -308,11 +309,17 @@ def other_configs(q, k, v, dev):
     g128 = torch.Generator(device=dev).manual_seed(128)
     q8, k8, v8 = (torch.randn(2, 15, L, 128, device=dev, generator=g128).to(torch.bfloat16) for _ in range(3))
     f128 = 4 * 128 * kv128.computed_pairs(L, L)
+    # The default (bf16 scores at this head dim), and fp16 scores from keys prepared once
+    # outside the timed calls.
+    k16_128 = prepare_fp16_keys(k8)
     ms_128 = time_fn(lambda: block_sparse_attention(q8, k8, v8, kv128, 1 / math.sqrt(128), n_text_blocks=4))
-    del q8, k8, v8
+    ms_128_k16 = time_fn(lambda: block_sparse_attention(q8, k8, v8, kv128, 1 / math.sqrt(128), n_text_blocks=4,
+                                                        k16=k16_128))
+    del q8, k8, v8, k16_128
     out["attention_variants"] = {"fp16_c2_ms": round(ms_f16, 4), "fp16_c2_tflops": _tflops(f_c2, ms_f16),
                                  "fp32_c2_ms": round(ms_f32, 4), "fp32_c2_tflops": _tflops(f_c2, ms_f32),
                                  "head_dim_128_ms": round(ms_128, 4), "head_dim_128_tflops": _tflops(f128, ms_128),
+                                 "head_dim_128_fp16_scores_ms": round(ms_128_k16, 4),
                                  "head_dim_128_shape": [2, 15, L, 128]}
     _progress("attention_variants done")
 

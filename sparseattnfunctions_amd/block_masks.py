@@ -115,7 +115,7 @@ def meanpool_topk_kv_list(q, k, topk: int, n_text_blocks: int, block: int = 64,
     from .utils.block_sparse_attn_kernel import FP16Keys, fp16_keys_wanted, k16_workspace_bytes
     B, H, L = q.shape[:3]
     ws = None
-    if with_fp16_keys and block == 64 and fp16_keys_wanted(k):
+    if with_fp16_keys and block == 64 and k.shape[3] == 64 and fp16_keys_wanted(k):
         ws = torch.empty(k16_workspace_bytes(B, H, L, 64), dtype=torch.uint8, device=k.device)
     qp, kp = pool_blocks(q, k, block, k16_ws=ws)
     k16 = None

@@ -999,8 +999,9 @@ __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "mem
 // Slots: the four slots of dispatch group w (the work order's unit, placed on XCD w % 8)
 // go to the workgroups x = 32 (w / 8) + 8 i + w % 8, i = 0..3, which the dispatcher places
 // on the same XCD.
-template <typename T>
+template <typename T, bool kK16 = false>
 __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
+  static_assert(!kK16 || std::is_same<T, __bf16>::value, "fp16 scores take bf16 inputs");
   typedef Elem<T> E;
   constexpr int kD = 128;
   constexpr int kDS = kD / 16;        // 16-wide d steps of S = K Q^T
@@ -1010,6 +1011,7 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t k_lds[kHalves * kTileBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t v_lds[kHalves * kTileBytes];
   __shared__ int redo_lds[2];
+  __shared__ float qn_lds[2];  // fp16 scores: each wave's largest squared query-row norm
 
   const int lane = threadIdx.x & 63;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // query rows 32g .. 32g + 31
@@ -1035,8 +1037,9 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
   const int hk = a.kv_rep > 1 ? h / a.kv_rep : h;
   const uint16_t* khead = a.k + b * a.k_sb + hk * a.k_sh;
   const uint16_t* vhead = a.v + b * a.v_sb + hk * a.v_sh;
-  const uint32_t krow = (uint32_t)(a.k_sl * 2), vrow = (uint32_t)(a.v_sl * 2);
-  const uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
+  uint32_t krow = (uint32_t)(a.k_sl * 2);
+  const uint32_t vrow = (uint32_t)(a.v_sl * 2);
+  uint32_t kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
   const uint32_t vbytes = (uint32_t)(a.Lk - 1) * vrow + 2 * kHeadDim;
   lds_u8* const kl = (lds_u8*)k_lds;
   lds_u8* const vl = (lds_u8*)v_lds;
@@ -1084,9 +1087,68 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
       qf[s] = __builtin_bit_cast(typename E::v8, zero ? make_uint4(0u, 0u, 0u, 0u) : w);
     }
   }
+  // fp16 scores: the head's largest squared key norm (its block norms, clamped loads).
+  uint32_t kmax = 0u;
+  if constexpr (kK16) {
+    const uint32_t* bn = a.k16_norm2 + (int64_t)bh * a.nkb;
+    for (int j0 = 0; j0 < a.nkb; j0 += 256) {
+      uint32_t v4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v4[u] = bn[min(j0 + 64 * u + lane, a.nkb - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) kmax = max(kmax, v4[u]);
+    }
+  }
   // The Q operands have landed before the first copy is issued, so that no load issued
   // before the loop is pending inside it.
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+
+  // fp16 scores, as in bsa_fwd_kernel: the pair takes them when max |q_i * scale_log2| *
+  // max |k_j| <= kK16Bound over its 64 query rows (both waves' rows: they decide together,
+  // since their barriers must match) and the head's keys, with both squared norms below
+  // kK16NormMax; q is then rounded to fp16 after the scaling and the K tiles come from the
+  // fp16 copy of k. Otherwise the pair runs on the bf16 operands.
+  bool use16 = false;
+  if constexpr (kK16) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+    const float qs = a.scale_log2;
+    float n2 = 0.f;
+    uint32_t h16[kDS][4];
+#pragma unroll
+    for (int s = 0; s < kDS; ++s) {
+      const sa_u32x4v w = __builtin_bit_cast(sa_u32x4v, qf[s]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = __uint_as_float(w[i] << 16) * qs, x1 = __uint_as_float(w[i] & 0xffff0000u) * qs;
+        n2 = fmaf(x1, x1, fmaf(x0, x0, n2));
+        h16[s][i] = Elem<_Float16>::pack(x0, x1);
+      }
+    }
+    float qn2 = xhalf_sum(n2);  // row 32g + col
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) qn2 = fmaxf(qn2, __shfl_xor(qn2, o));
+    if (lane == 0) qn_lds[g] = qn2;
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    wg_barrier();
+    qn2 = fmaxf(qn_lds[0], qn_lds[1]);
+    qn2 = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(qn2)));
+    const float kn2 = __uint_as_float(__builtin_amdgcn_readfirstlane(kmax));
+    use16 = qn2 < kK16NormMax && kn2 < kK16NormMax && qn2 * kn2 <= kK16Bound * kK16Bound;
+    if (use16) {
+#pragma unroll
+      for (int s = 0; s < kDS; ++s)
+        qf[s] = __builtin_bit_cast(typename E::v8, sa_u32x4v{h16[s][0], h16[s][1], h16[s][2], h16[s][3]});
+      khead = a.k16 + (int64_t)bh * a.Lk * kD;
+      krow = 2 * kD;
+      kbytes = (uint32_t)(a.Lk - 1) * krow + 2 * kHeadDim;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int r = 8 * p + (lane >> 3);
+        kgo[p] = (lane >> 3) * krow + 16 * ((lane & 7) ^ swz(r));
+      }
+    }
+  }
 
   sa_f32x16 acc[kDC];
   float m = -INFINITY, l = 0.f;
@@ -1104,8 +1166,9 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
   // One pass over the list. Fast pass (kSafe = false): P = exp2(S) with no max (fp16: minus
   // the row's maximum over the first tile), checked by the caller; safe pass: running max
   // with lazy rescale.
-  auto run = [&](auto safe_tag) {
+  auto run = [&](auto safe_tag, auto k16_tag) __attribute__((always_inline)) {
     constexpr bool kSafe = decltype(safe_tag)::value;
+    constexpr bool kQ16 = decltype(k16_tag)::value;  // fp16 K and pre-scaled q: S in the exp2 domain
     constexpr bool kOffset = !kSafe && !std::is_same<T, __bf16>::value;
 #pragma unroll
     for (int dc = 0; dc < kDC; ++dc) acc[dc] = sa_f32x16{};
@@ -1133,7 +1196,12 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
       for (int c = 0; c < 2; ++c) {
         sa_f32x16 t = {};
 #pragma unroll
-        for (int s = 0; s < kDS; ++s) t = E::mfma(E::as8(kop[c][s]), qf[s], t);
+        for (int s = 0; s < kDS; ++s) {
+          if constexpr (kQ16)
+            t = Elem<_Float16>::mfma(Elem<_Float16>::as8(kop[c][s]), __builtin_bit_cast(sa_f16x8, qf[s]), t);
+          else
+            t = E::mfma(E::as8(kop[c][s]), qf[s], t);
+        }
         S[c] = t;
       }
       __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
@@ -1148,7 +1216,7 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
           for (int e = 0; e < 16; ++e)
             if (32 * c + 8 * (e >> 2) + 4 * hh + (e & 3) >= nvalid) S[c][e] = -INFINITY;
       }
-      const float sc = a.scale_log2;
+      const float sc = kQ16 ? 1.f : a.scale_log2;  // fp16 scores: S is already scaled
       float mu = 0.f;
       // Row max of this tile's scaled scores (sc > 0: max(S) * sc = max(S * sc)).
       auto tile_row_max = [&]() {
@@ -1230,8 +1298,16 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
     // is written again or the wave ends.
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   };
+  auto run_item = [&](auto safe_tag) __attribute__((always_inline)) {
+    if constexpr (kK16) {
+      if (use16) run(safe_tag, std::true_type{});
+      else run(safe_tag, std::false_type{});
+    } else {
+      run(safe_tag, std::false_type{});
+    }
+  };
 
-  run(std::false_type{});
+  run_item(std::false_type{});
   // The fast pass is exact unless a row's sum left [2^-90, 2^90] (fp16: P rounded to inf)
   // or an accumulator overflowed; then the pair redoes its block with the safe pass. Both
   // waves decide together (their barriers must match).
@@ -1251,7 +1327,7 @@ __global__ __launch_bounds__(128, 2) void bsa_fwd_pair_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
   wg_barrier();
   const bool redo = (redo_lds[0] | redo_lds[1]) != 0;
-  if (redo) run(std::true_type{});
+  if (redo) run_item(std::true_type{});
 
   // ---- Epilogue: out = acc / l (each lane half holds a partial l of its keys).
   const float l_tot = xhalf_sum(l);
@@ -1418,7 +1494,14 @@ void launch_variant(const FwdArgs& a, dim3 g, dim3 blk, hipStream_t s, bool mask
       // Workgroup x runs slot 4 (8 (x / 32) + x % 8) + (x / 8) % 4: the four slots of each
       // dispatch group on that group's XCD.
       const int64_t groups = a.n_slots / kWaves;
-      hipLaunchKernelGGL((bsa_fwd_pair_kernel<T>), dim3((unsigned)((groups + 7) / 8 * 32)), dim3(128), 0, s, a);
+      const dim3 pg((unsigned)((groups + 7) / 8 * 32));
+      if constexpr (std::is_same<T, __bf16>::value) {
+        if (a.k16) {  // fp16 scores
+          hipLaunchKernelGGL((bsa_fwd_pair_kernel<T, true>), pg, dim3(128), 0, s, a);
+          return;
+        }
+      }
+      hipLaunchKernelGGL((bsa_fwd_pair_kernel<T>), pg, dim3(128), 0, s, a);
       return;
     }
   }
@@ -1497,9 +1580,10 @@ int launch_fwd(const uint16_t* q, const int64_t q_strides[3], const uint16_t* k,
   a.ws = nullptr;
   a.k16 = k16;
   a.k16_norm2 = k16_norm2;
-  if (k16 && (!k16_norm2 || D != 64 || fp16 || v32 || kv_slot || pool_cols || parts != 1 || q_rows || o_rows ||
-              kv_rep != 1))
-    return sa::fail(SA_ERR_UNSUPPORTED, "%s: fp16 scores need plain or key-bias bf16 lists at head dim 64", fn);
+  if (k16 && (!k16_norm2 || (D != 64 && !(D == 128 && !key_bias)) || fp16 || v32 || kv_slot || pool_cols ||
+              parts != 1 || q_rows || o_rows || kv_rep != 1))
+    return sa::fail(SA_ERR_UNSUPPORTED,
+                    "%s: fp16 scores need plain or key-bias bf16 lists at head dim 64, or plain ones at 128", fn);
   a.kv_idx = kv_idx; a.kv_cnt = kv_cnt; a.max_cnt = max_cnt;
   a.bias = key_bias;
   a.bias_sb = key_bias ? bias_strides[0] : 0;
@@ -1665,26 +1749,30 @@ struct K16Args {
   uint32_t* blk_norm2;  // [n_blocks]
 };
 
+template <int kD>
 __global__ __launch_bounds__(256) void k16_kernel(K16Args a) {
+  constexpr int kLpr = kD / 8;        // lanes per row, 16 bytes each
+  constexpr int kRpp = 64 / kLpr;     // rows per load of the wave
+  constexpr int kPass = kBlock / kRpp;
   const int lane = threadIdx.x & 63;
   const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (blk >= a.n_blocks) return;
   const int64_t bh = blk / a.nkb;
   const int kb = (int)(blk - bh * a.nkb);
   const int64_t b = bh / a.H, h = bh - b * a.H;
-  const int c8 = lane & 7;
+  const int c8 = lane % kLpr;
   const uint16_t* src = a.k + b * a.k_sb + h * a.k_sh + 8 * c8;
-  uint16_t* dst = a.k16 + bh * (int64_t)a.Lk * kHeadDim + 8 * c8;
-  uint4 w[8];
+  uint16_t* dst = a.k16 + bh * (int64_t)a.Lk * kD + 8 * c8;
+  uint4 w[kPass];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {  // rows past Lk load the last row, which is neither stored nor counted
-    const int r = min(kb * kBlock + 8 * i + (lane >> 3), a.Lk - 1);
+  for (int i = 0; i < kPass; ++i) {  // rows past Lk load the last row, which is neither stored nor counted
+    const int r = min(kb * kBlock + kRpp * i + lane / kLpr, a.Lk - 1);
     w[i] = *reinterpret_cast<const uint4*>(src + (int64_t)r * a.k_sl);
   }
   uint32_t mx = 0u;  // float bits of the largest squared norm seen
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = kb * kBlock + 8 * i + (lane >> 3);
+  for (int i = 0; i < kPass; ++i) {
+    const int r = kb * kBlock + kRpp * i + lane / kLpr;
     const uint32_t e[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
     uint32_t o[4];
     float n = 0.f;
@@ -1694,17 +1782,16 @@ __global__ __launch_bounds__(256) void k16_kernel(K16Args a) {
       n = fmaf(x1, x1, fmaf(x0, x0, n));
       o[j] = Elem<_Float16>::pack(x0, x1);
     }
-    // the row's 8 lanes, in a fixed order
-    n += __shfl_xor(n, 1);
-    n += __shfl_xor(n, 2);
-    n += __shfl_xor(n, 4);
+    // the row's kLpr lanes, in a fixed order
+#pragma unroll
+    for (int off = 1; off < kLpr; off <<= 1) n += __shfl_xor(n, off);
     if (r < a.Lk) {
       mx = max(mx, __float_as_uint(n));
-      *reinterpret_cast<uint4*>(dst + (int64_t)r * kHeadDim) = make_uint4(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<uint4*>(dst + (int64_t)r * kD) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
 #pragma unroll
-  for (int off = 8; off < 64; off <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
+  for (int off = kLpr; off < 64; off <<= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off));
   if (lane == 0) a.blk_norm2[blk] = mx;
 }
 
@@ -1727,8 +1814,9 @@ __global__ __launch_bounds__(256) void bias_log2_kernel(const float* bias, int64
 extern "C" int sa_block_sparse_fwd_k16_workspace(int B, int H, int Lk, int D, int with_bias, int64_t* bytes) {
   SA_REQUIRE(bytes, "sa_block_sparse_fwd_k16_workspace: null bytes");
   SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "sa_block_sparse_fwd_k16_workspace: bad shape B=%d H=%d Lk=%d", B, H, Lk);
-  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd_k16_workspace: head_dim %d (64)", D);
-  *bytes = with_bias ? sa::k16_ws_bytes_bias(B, H, Lk) : k16_ws_bytes(B, H, Lk);
+  if (D != kHeadDim && !(D == 128 && !with_bias))
+    return sa::fail(SA_ERR_UNSUPPORTED, "sa_block_sparse_fwd_k16_workspace: head_dim %d (64; 128 without a key bias)", D);
+  *bytes = with_bias ? sa::k16_ws_bytes_bias(B, H, Lk) : k16_ws_bytes(B, H, Lk, D);
   return sa::ok();
 }
 
@@ -1738,8 +1826,8 @@ int k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int
                 int64_t workspace_bytes, void* stream, const char* fn) {
   SA_REQUIRE(k && k_strides, "%s: null k", fn);
   SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
-  if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64)", fn, D);
-  const int64_t need = k16_ws_bytes(B, H, Lk);
+  if (D != kHeadDim && D != 128) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", fn, D);
+  const int64_t need = k16_ws_bytes(B, H, Lk, D);
   SA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0, "%s: workspace null or not 256-byte aligned",
              fn);
   SA_REQUIRE(workspace_bytes >= need, "%s: workspace of %lld bytes < %lld", fn, (long long)workspace_bytes,
@@ -1751,10 +1839,12 @@ int k16_prepare(const uint16_t* k, const int64_t k_strides[3], int B, int H, int
   ka.H = H; ka.Lk = Lk; ka.nkb = sa::cdiv(Lk, kBlock);
   ka.n_blocks = (int64_t)B * H * ka.nkb;
   ka.k16 = static_cast<uint16_t*>(workspace);
-  ka.blk_norm2 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + k16_bytes(B, H, Lk));
+  ka.blk_norm2 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(workspace) + k16_bytes(B, H, Lk, D));
   SA_REQUIRE(ka.n_blocks / kWaves < (1LL << 31), "%s: grid too large", fn);
   hipStream_t s = sa::as_stream(stream);
-  hipLaunchKernelGGL(k16_kernel, dim3((unsigned)((ka.n_blocks + kWaves - 1) / kWaves)), dim3(64 * kWaves), 0, s, ka);
+  const dim3 grid((unsigned)((ka.n_blocks + kWaves - 1) / kWaves));
+  if (D == 128) hipLaunchKernelGGL(k16_kernel<128>, grid, dim3(64 * kWaves), 0, s, ka);
+  else hipLaunchKernelGGL(k16_kernel<64>, grid, dim3(64 * kWaves), 0, s, ka);
   return sa::check_launch(fn);
 }
 
@@ -1776,6 +1866,7 @@ extern "C" int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_stride
   SA_REQUIRE(!key_bias || bias_strides, "%s: key_bias without bias_strides", fn);
   if (key_bias) {
     SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
+    if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: a key bias needs head_dim 64, got %d", fn, D);
     SA_REQUIRE(workspace_bytes >= sa::k16_ws_bytes_bias(B, H, Lk), "%s: workspace of %lld bytes < %lld with key_bias",
                fn, (long long)workspace_bytes, (long long)sa::k16_ws_bytes_bias(B, H, Lk));
   }
@@ -1783,14 +1874,15 @@ extern "C" int sa_block_sparse_fwd_k16(const uint16_t* q, const int64_t q_stride
   if (rc) return rc;
   if (prepared) {  // the same checks of the workspace, without the launches
     SA_REQUIRE(B > 0 && H > 0 && Lk > 0, "%s: bad shape B=%d H=%d Lk=%d", fn, B, H, Lk);
-    if (D != kHeadDim) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64)", fn, D);
+    if (D != kHeadDim && D != 128) return sa::fail(SA_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", fn, D);
     SA_REQUIRE(workspace && reinterpret_cast<uintptr_t>(workspace) % 256 == 0,
                "%s: workspace null or not 256-byte aligned", fn);
-    SA_REQUIRE(workspace_bytes >= k16_ws_bytes(B, H, Lk), "%s: workspace of %lld bytes < %lld", fn,
-               (long long)workspace_bytes, (long long)k16_ws_bytes(B, H, Lk));
+    SA_REQUIRE(workspace_bytes >= k16_ws_bytes(B, H, Lk, D), "%s: workspace of %lld bytes < %lld", fn,
+               (long long)workspace_bytes, (long long)k16_ws_bytes(B, H, Lk, D));
   }
   const uint16_t* k16 = static_cast<const uint16_t*>(workspace);
-  const uint32_t* norm2 = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(workspace) + k16_bytes(B, H, Lk));
+  const uint32_t* norm2 =
+      reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(workspace) + k16_bytes(B, H, Lk, D));
   const float* bias2 = nullptr;
   int64_t bias2_strides[2] = {(int64_t)H * Lk, Lk};
   if (key_bias) {  // the bias in log2 units, behind the k16 part of the workspace

@@ -42,11 +42,16 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 // Workspace of the fp16-score attention (sa_block_sparse_fwd_k16): the fp16 copy of k,
-// [B*H][Lk][64] contiguous, then the largest squared row norm of each 64-row key block
-// (fp32 bits), [B*H][ceil(Lk/64)]. Written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16.
-inline int64_t k16_bytes(int B, int H, int Lk) { return ((int64_t)B * H * Lk * 64 * 2 + 255) / 256 * 256; }
-inline int64_t k16_ws_bytes(int B, int H, int Lk) { return k16_bytes(B, H, Lk) + (int64_t)B * H * cdiv(Lk, 64) * 4; }
-// With a key bias: then, 256-byte aligned, the bias times log2(e), fp32 [B*H][Lk] contiguous.
+// [B*H][Lk][D] contiguous (D = 64 or 128), then the largest squared row norm of each 64-row
+// key block (fp32 bits), [B*H][ceil(Lk/64)]. Written by sa_block_sparse_fwd_k16_prepare or
+// (D = 64) sa_block_pool_k16.
+inline int64_t k16_bytes(int B, int H, int Lk, int D = 64) {
+  return ((int64_t)B * H * Lk * D * 2 + 255) / 256 * 256;
+}
+inline int64_t k16_ws_bytes(int B, int H, int Lk, int D = 64) {
+  return k16_bytes(B, H, Lk, D) + (int64_t)B * H * cdiv(Lk, 64) * 4;
+}
+// With a key bias (D = 64): then, 256-byte aligned, the bias times log2(e), fp32 [B*H][Lk] contiguous.
 inline int64_t k16_bias_offset(int B, int H, int Lk) { return (k16_ws_bytes(B, H, Lk) + 255) / 256 * 256; }
 inline int64_t k16_ws_bytes_bias(int B, int H, int Lk) { return k16_bias_offset(B, H, Lk) + (int64_t)B * H * Lk * 4; }
 

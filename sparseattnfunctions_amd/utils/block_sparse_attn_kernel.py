@@ -97,13 +97,14 @@ class FP16Keys:
 
 
 def fp16_keys_wanted(k: torch.Tensor) -> bool:
-    """Whether block_sparse_attention's default takes fp16 scores with this k (bf16 [B,H,Lk,64])."""
-    return FP16_SCORES and k.is_cuda and k.dtype == torch.bfloat16 and k.dim() == 4 and k.shape[3] == 64
+    """Whether block_sparse_attention's default takes fp16 scores with this k (bf16 [B,H,Lk,D],
+    D = 64 or 128)."""
+    return FP16_SCORES and k.is_cuda and k.dtype == torch.bfloat16 and k.dim() == 4 and k.shape[3] in (64, 128)
 
 
 def prepare_fp16_keys(k: torch.Tensor) -> Optional[FP16Keys]:
-    """Enqueues the fp16 copy of k (bf16 [B,H,Lk,64]) on the current stream; None for other
-    dtypes or head dims (those launches take no fp16 scores)."""
+    """Enqueues the fp16 copy of k (bf16 [B,H,Lk,D], D = 64 or 128) on the current stream; None
+    for other dtypes or head dims (those launches take no fp16 scores)."""
     if not fp16_keys_wanted(k):
         return None
     k_in, k = k, _prep_qkv(k, (torch.bfloat16,))
@@ -166,8 +167,8 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     `v_cols=32` (bf16, head dim 64, no row maps or tile masks): only v's first 32 columns
     enter P.V and the output is [B,H,Lq,32] (`sa_block_sparse_fwd_v32`; segment-indicator v).
 
-    fp16 scores (`sa_block_sparse_fwd_k16`; plain or key-bias bf16 lists at head dim 64, no row
-    maps, tile masks or key-range parts): an fp16 copy of k (exact for 2^-17 <= |k| < 65504)
+    fp16 scores (`sa_block_sparse_fwd_k16`; plain or key-bias bf16 lists at head dim 64, plain
+    ones at 128, no row maps, tile masks or key-range parts): an fp16 copy of k (exact for 2^-17 <= |k| < 65504)
     and q scaled by sm_scale*log2(e) into fp16 inside the kernel, so the softmax takes no
     multiply per score. A query block takes them only when max|q_i*sm_scale*log2(e)| *
     max|k_j| <= 32 (row norms; it bounds every exp2-domain score), which limits each score's
@@ -178,7 +179,8 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
     when `k16` holds keys already made for this k (`prepare_fp16_keys`, or the pooling pass of
     the mask builders, `with_fp16_keys`; possibly on another stream, whose event this call's
     stream waits for) or when the lists are dense over at least DENSE_FP16_BLOCKS query and key
-    blocks; fp16_scores=True makes the copy here, False never. FP16_SCORES = False turns the
+    blocks at head dim 64 (at 128 the pair kernel runs as fast on bf16 scores, 1.119 against
+    1.116 ms on the C2 lists); fp16_scores=True makes the copy here, False never. FP16_SCORES = False turns the
     mode off everywhere.
     """
     _lib.require_gpu(q, k, v)
@@ -264,9 +266,9 @@ def block_sparse_attention(q, k, v, kv: KVList, sm_scale: float, key_bias=None, 
         _lib.check(rc, "sa_block_sparse_fwd_v32")
         return out
     if fp16_scores is None:
-        fp16_scores = k16 is not None or (kv.dense and min(kv.nqb, kv.nkb) >= DENSE_FP16_BLOCKS)
+        fp16_scores = k16 is not None or (D == 64 and kv.dense and min(kv.nqb, kv.nkb) >= DENSE_FP16_BLOCKS)
     fp16_scores = fp16_scores and FP16_SCORES
-    if fp16_scores and not fp16 and not fp32 and D == 64:
+    if fp16_scores and not fp16 and not fp32 and (D == 64 or (D == 128 and key_bias is None)):
         # fp16 scores (`sa_block_sparse_fwd_k16`): an fp16 copy of k, and q scaled into the exp2
         # domain in fp16 inside the kernel, so the softmax needs no multiply per score; query
         # blocks whose score bound fails run on the bf16 operands.

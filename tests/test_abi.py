@@ -159,7 +159,11 @@ def test_k16_workspace_query(lib):
     assert n.value == k16 + norms
     assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, 1, ctypes.byref(n)) == _lib.SA_OK
     assert n.value == (k16 + norms + 255) // 256 * 256 + B * H * Lk * 4
-    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 128, 0, ctypes.byref(n)) == _lib.SA_ERR_UNSUPPORTED
+    # head dim 128: plain lists only (the pair kernel), a 128-wide fp16 copy of k
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 128, 0, ctypes.byref(n)) == _lib.SA_OK
+    assert n.value == (B * H * Lk * 128 * 2 + 255) // 256 * 256 + norms
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 128, 1, ctypes.byref(n)) == _lib.SA_ERR_UNSUPPORTED
+    assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 96, 0, ctypes.byref(n)) == _lib.SA_ERR_UNSUPPORTED
     assert lib.sa_block_sparse_fwd_k16_workspace(0, H, Lk, 64, 0, ctypes.byref(n)) == _lib.SA_ERR_INVALID
     assert lib.sa_block_sparse_fwd_k16_workspace(B, H, Lk, 64, 0, None) == _lib.SA_ERR_INVALID
 
@@ -183,13 +187,19 @@ def test_k16_launches_validate_workspace(lib):
         assert fwd(prepared, dummy, need.value - 1) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
         assert fwd(prepared, ctypes.c_void_p(4096 + 16), need.value) == _lib.SA_ERR_INVALID
         assert b"aligned" in lib.sa_last_error()
-        assert fwd(prepared, dummy, need.value, d=128) == _lib.SA_ERR_UNSUPPORTED
+        # head dim 128 needs the 128-wide workspace and no key bias; other head dims are refused
+        assert fwd(prepared, dummy, need.value, d=128) == _lib.SA_ERR_INVALID and b"workspace" in lib.sa_last_error()
+        assert fwd(prepared, dummy, need_b.value * 2, d=128, bias=dummy,
+                   bias_strides=_lib.i64(H * Lk, Lk)) == _lib.SA_ERR_UNSUPPORTED
+        assert fwd(prepared, dummy, need_b.value * 2, d=96) == _lib.SA_ERR_UNSUPPORTED
         # a key bias needs its strides, and the larger workspace
         assert fwd(prepared, dummy, need_b.value, bias=dummy) == _lib.SA_ERR_INVALID
         assert fwd(prepared, dummy, need.value, bias=dummy, bias_strides=_lib.i64(0, 0)) == _lib.SA_ERR_INVALID
         assert b"key_bias" in lib.sa_last_error()
     assert lib.sa_block_sparse_fwd_k16_prepare(dummy, s3, B, H, Lk, D, dummy, need.value - 1, None) == _lib.SA_ERR_INVALID
     assert lib.sa_block_sparse_fwd_k16_prepare(dummy, s3, B, H, Lk, 128, dummy, need.value, None) == \
+        _lib.SA_ERR_INVALID
+    assert lib.sa_block_sparse_fwd_k16_prepare(dummy, s3, B, H, Lk, 96, dummy, need.value * 2, None) == \
         _lib.SA_ERR_UNSUPPORTED
     assert lib.sa_block_pool_k16(dummy, s3, dummy, s3, B, H, Lk, D, dummy, dummy, dummy, need.value - 1,
                                  None) == _lib.SA_ERR_INVALID

@@ -304,3 +304,41 @@ def test_fp16_scores_strided_ragged_empty(dev, Lq, Lk):
     want = masked_attention(q, k, v, mask, scale)
     _check(o16, want)
     _check(obf, want)
+
+
+def test_fp16_scores_head_dim_128(dev):
+    # Head dim 128 (bsa_fwd_pair_kernel; the pair of waves decides together): batch 0's
+    # bounds are below 32 and take fp16 scores within the bar; batch 1's keys * 4 fail the
+    # bound and give the bf16-score launch's bits; a NaN key sends head (0, 2) to the bf16
+    # operands too. Prepared keys (the fp16 copy is k.half()) give the inline call's output.
+    from sparseattnfunctions_amd.utils.block_sparse_attn_kernel import prepare_fp16_keys
+    case("fp16 scores at head dim 128")
+    scale = 1 / math.sqrt(128)
+    q, k, v = _rand((2, 3, 700, 128), 1500), _rand((2, 3, 1500, 128), 1501), _rand((2, 3, 1500, 128), 1502)
+    k = k.float()
+    k[1] *= 4.0
+    k[0, 2, 900, 17] = float("nan")
+    k = k.bfloat16()
+    finite = k.clone()
+    finite[0, 2, 900, 17] = 0
+    bounds = _block_bounds(q, finite, scale)
+    assert bounds[0].max().item() < BOUND * 0.98 and bounds[1].min().item() > BOUND * 1.05
+    mask, nqb, nkb = _setup(q, k, v, 1503, density=0.6)
+    kv = kv_list_from_mask(mask.to(dev), 2, 3, nqb, nkb)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o16 = block_sparse_attention(qd, kd, vd, kv, scale, fp16_scores=True)
+    obf = block_sparse_attention(qd, kd, vd, kv, scale, fp16_scores=False)
+    prep = prepare_fp16_keys(kd)
+    o_prep = block_sparse_attention(qd, kd, vd, kv, scale, k16=prep)
+    torch.cuda.synchronize()
+    nk = 2 * 3 * 1500 * 128 * 2
+    assert torch.equal(prep.ws[:nk].view(torch.float16).view(2, 3, 1500, 128).view(torch.int16),
+                       kd.half().view(torch.int16))
+    assert torch.equal(o_prep.view(torch.int16), o16.view(torch.int16))  # NaN rows of head (0, 2) included
+    o16, obf = o16.cpu(), obf.cpu()
+    assert torch.equal(o16[1], obf[1])
+    assert torch.equal(o16[0, 2].view(torch.int16), obf[0, 2].view(torch.int16))
+    assert not torch.equal(o16[0, :2], obf[0, :2])
+    want = masked_attention(q[:, :2], k[:, :2], v[:, :2], mask[:, :2], scale)
+    _check(o16[:, :2], want)
+    _check(o16[1:], masked_attention(q[1:], k[1:], v[1:], mask[1:], scale))
