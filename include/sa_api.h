@@ -117,7 +117,10 @@ int sa_block_sparse_fwd(const uint16_t* q, const int64_t q_strides[3], const uin
 
 /*
  * sa_block_sparse_fwd with the scores in fp16 (same block_sparse_attn_kernel.py:52-209 work,
- * bf16 q, k, v and out, head dim 64, optional key_bias as there). The workspace holds an fp16 copy of k (round
+ * bf16 q, k, v and out, head dim 64 with an optional key_bias as there, or head dim 128 without
+ * one; other head dims, or 128 with a key_bias, return SA_ERR_UNSUPPORTED). The workspace
+ * (sa_block_sparse_fwd_k16_workspace with the same D; sa_block_pool_k16 writes it for D = 64
+ * only) holds an fp16 copy of k (round
  * to nearest even: exact for 2^-17 <= |k| < 65504, on fp16's subnormal grid below, an absolute
  * error of at most 2^-25) and the largest squared key-row norm of each 64-row key block,
  * written by sa_block_sparse_fwd_k16_prepare or sa_block_pool_k16 (or by this call first, with
